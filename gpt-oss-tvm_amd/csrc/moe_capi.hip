@@ -1,0 +1,286 @@
+// C ABI of libmoe_gfx950: argument validation, workspace layout and the
+// block-level chain.  Declarations and reference citations: include/moe_gfx950.h.
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/moe_gfx950.h"
+
+extern "C" {
+int moe_launch_dequant(const void* blocks, const void* scales, void* out, int64_t rows, int fast,
+                       hipStream_t stream);
+int moe_launch_router(const void* x, const void* norm_w, const void* gate_w, const void* gate_b,
+                      int n, int H, int E, int k, float eps, void* t_out, void* idx_out,
+                      void* w_out, hipStream_t stream);
+int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void* sorted_pairs,
+                       void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
+int moe_launch_expert_gemv(const void* x, int x_f32, const void* indptr, const void* sorted_pairs,
+                           int k_top, int brow_mode, int orow_mode, const void* blocks,
+                           const void* scales, const void* bias, int E, int N, int K, int swiglu,
+                           float alpha, float limit, void* out, int out_ld, hipStream_t stream);
+int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
+                      hipStream_t stream);
+int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
+                      hipStream_t stream);
+}
+
+namespace {
+
+constexpr int64_t kMaxK = 3072;  // reduction length limit (scale staging in LDS)
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline hipStream_t as_stream(moe_stream_t s) { return (hipStream_t)s; }
+
+// Common shape checks of the block: see the header's "Supported shapes".
+int check_dims(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
+  if (n < 0 || H <= 0 || I <= 0) return MOE_ERR_SHAPE;
+  if (H % 64 || I % 32 || H > kMaxK || I > kMaxK) return MOE_ERR_SHAPE;
+  if (k < 1 || k > 8 || E < k || E > 256) return MOE_ERR_UNSUPPORTED;
+  if (n * k >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
+  return MOE_OK;
+}
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[10], size_t* total) {
+  const size_t nk = (size_t)n * (size_t)k;
+  const size_t sizes[10] = {
+      (size_t)n * H * 2,      // t       bf16 [n, H]
+      nk * 4,                 // idx     int32 [n, k]
+      nk * 2,                 // w       bf16 [n, k]
+      (size_t)(E + 1) * 4,    // indptr  int32 [E+1]
+      nk * 4,                 // sorted_pairs
+      nk * 4,                 // token_indices
+      nk * 4,                 // expert_ids
+      nk * 4,                 // pair_pos
+      nk * (size_t)I * 4,     // act     fp32 [n*k, I]
+      nk * (size_t)H * 4,     // y       fp32 [n*k, H]
+  };
+  size_t o = 0;
+  for (int i = 0; i < 10; ++i) {
+    off[i] = o;
+    o = round_up(o + sizes[i], 256);
+  }
+  *total = o;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_version(void) { return 100; }
+
+const char* moe_status_string(int status) {
+  switch (status) {
+    case MOE_OK: return "ok";
+    case MOE_ERR_NULL: return "null pointer";
+    case MOE_ERR_SHAPE: return "unsupported or inconsistent shape";
+    case MOE_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case MOE_ERR_UNSUPPORTED: return "unsupported parameter value";
+    case MOE_ERR_LAUNCH: return "kernel launch failed";
+    case MOE_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+static int dequant_common(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
+                          int64_t rows, int fast, moe_stream_t stream) {
+  if (rows < 0 || rows > ((int64_t)1 << 36)) return MOE_ERR_SHAPE;
+  if (rows == 0) return MOE_OK;
+  if (!blocks || !scales || !out) return MOE_ERR_NULL;
+  if (!aligned16(blocks) || !aligned16(out)) return MOE_ERR_ALIGN;
+  return moe_launch_dequant(blocks, scales, out, rows, fast, as_stream(stream));
+}
+
+int moe_dequant_mxfp4(const uint8_t* blocks, const uint8_t* scales, uint16_t* out, int64_t rows,
+                      moe_stream_t stream) {
+  return dequant_common(blocks, scales, out, rows, 0, stream);
+}
+
+int moe_dequant_mxfp4_fast(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
+                           int64_t rows, moe_stream_t stream) {
+  return dequant_common(blocks, scales, out, rows, 1, stream);
+}
+
+int moe_router_topk(const uint16_t* x, const uint16_t* norm_w, const uint16_t* gate_w,
+                    const uint16_t* gate_b, int64_t n, int64_t H, int64_t E, int64_t k, float eps,
+                    uint16_t* t, int32_t* idx, uint16_t* w, moe_stream_t stream) {
+  if (n < 0 || H <= 0 || H % 8 || H > 8192 || n >= ((int64_t)1 << 31) / 8) return MOE_ERR_SHAPE;
+  if (k < 1 || k > 8 || E < k || E > 256) return MOE_ERR_UNSUPPORTED;
+  if (n == 0) return MOE_OK;
+  if (!x || !norm_w || !gate_w || !gate_b || !t || !idx || !w) return MOE_ERR_NULL;
+  if (!aligned16(x) || !aligned16(norm_w) || !aligned16(gate_w) || !aligned16(t))
+    return MOE_ERR_ALIGN;
+  return moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t, idx,
+                           w, as_stream(stream));
+}
+
+int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int32_t* indptr,
+                int32_t* sorted_pairs, int32_t* token_indices, int32_t* expert_ids,
+                int32_t* pair_pos, moe_stream_t stream) {
+  if (n < 0 || k < 1 || k > 8 || n * k >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
+  if (E < 1 || E > 256) return MOE_ERR_UNSUPPORTED;
+  if (!indptr) return MOE_ERR_NULL;
+  if (n > 0 && (!idx || !sorted_pairs || !token_indices || !expert_ids || !pair_pos))
+    return MOE_ERR_NULL;
+  return moe_launch_permute(idx, (int)(n * k), (int)k, (int)E, indptr, sorted_pairs, token_indices,
+                            expert_ids, pair_pos, as_stream(stream));
+}
+
+size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E) {
+  if (n < 0 || k < 1 || E < 1) return 0;
+  const size_t nk = (size_t)n * (size_t)k;
+  return round_up((size_t)(E + 1) * 4, 256) + 4 * round_up(nk * 4, 256);
+}
+
+// Rows per expert matmul must be a multiple of the 64-row wave tile.
+static int check_matmul(int64_t n, int64_t k, int64_t E, int64_t N, int64_t K) {
+  if (n < 0 || N <= 0 || K <= 0 || N % 64 || K % 32 || K > kMaxK) return MOE_ERR_SHAPE;
+  if (k < 1 || k > 8 || E < k || E > 256) return MOE_ERR_UNSUPPORTED;
+  if (n * k >= ((int64_t)1 << 31) || N * E >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
+  return MOE_OK;
+}
+
+int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indices, int64_t n,
+                     int64_t k, int64_t E, int64_t N, int64_t K, const uint8_t* blocks,
+                     const uint8_t* scales, const uint16_t* bias, float* out, void* workspace,
+                     size_t workspace_bytes, moe_stream_t stream) {
+  int rc = check_matmul(n, k, E, N, K);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!x || !expert_indices || !blocks || !scales || !bias || !out || !workspace) return MOE_ERR_NULL;
+  if (!aligned16(x) || !aligned16(blocks) || !aligned16(scales) || !aligned16(out) ||
+      !aligned16(workspace))
+    return MOE_ERR_ALIGN;
+  if (workspace_bytes < moe_einsum_workspace_bytes(n, k, E)) return MOE_ERR_WORKSPACE;
+  const size_t nk = (size_t)n * (size_t)k;
+  char* ws = (char*)workspace;
+  int32_t* indptr = (int32_t*)ws;
+  ws += round_up((size_t)(E + 1) * 4, 256);
+  int32_t* sp = (int32_t*)ws;
+  int32_t* ti = (int32_t*)(ws + round_up(nk * 4, 256));
+  int32_t* ei = (int32_t*)(ws + 2 * round_up(nk * 4, 256));
+  int32_t* pp = (int32_t*)(ws + 3 * round_up(nk * 4, 256));
+  hipStream_t s = as_stream(stream);
+  rc = moe_launch_permute(expert_indices, (int)nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s);
+  if (rc) return rc;
+  // mlp1-style input: B row = token; mlp2-style: B row = pair.  Output row = pair.
+  return moe_launch_expert_gemv(x, x_is_3d_f32 ? 1 : 0, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0,
+                                0, blocks, scales, bias, (int)E, (int)N, (int)K, 0, 0.f, 0.f, out,
+                                (int)N, s);
+}
+
+int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
+                    int64_t n, int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
+                    const uint8_t* scales, const uint16_t* bias, float alpha, float limit,
+                    float* act, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!t || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act) return MOE_ERR_NULL;
+  if (!aligned16(t) || !aligned16(blocks) || !aligned16(scales) || !aligned16(act))
+    return MOE_ERR_ALIGN;
+  return moe_launch_expert_gemv(t, 0, indptr, sorted_pairs, (int)k, 0, 1, blocks, scales, bias,
+                                (int)E, (int)(2 * I), (int)H, 1, alpha, limit, act, (int)I,
+                                as_stream(stream));
+}
+
+int moe_mlp2(const float* act, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
+             int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
+             const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!act || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y) return MOE_ERR_NULL;
+  if (!aligned16(act) || !aligned16(blocks) || !aligned16(scales) || !aligned16(y))
+    return MOE_ERR_ALIGN;
+  return moe_launch_expert_gemv(act, 1, indptr, sorted_pairs, (int)k, 2, 0, blocks, scales, bias,
+                                (int)E, (int)H, (int)I, 0, 0.f, 0.f, y, (int)H, as_stream(stream));
+}
+
+int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
+                    int64_t N, uint16_t* out, moe_stream_t stream) {
+  if (n < 0 || k < 1 || k > 8 || N <= 0 || N % 4 || n >= ((int64_t)1 << 31) / 8 ||
+      N >= ((int64_t)1 << 28))
+    return MOE_ERR_SHAPE;
+  if (n == 0) return MOE_OK;
+  if (!y || !w || !out) return MOE_ERR_NULL;
+  if (!aligned16(y) || ((uintptr_t)out & 7u) || (x && ((uintptr_t)x & 7u))) return MOE_ERR_ALIGN;
+  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)N, out, as_stream(stream));
+}
+
+int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, float limit, float* out,
+               moe_stream_t stream) {
+  if (rows < 0 || d < 0) return MOE_ERR_SHAPE;
+  if (rows == 0 || d == 0) return MOE_OK;
+  if (!x || !out) return MOE_ERR_NULL;
+  if ((uintptr_t)x & 7u) return MOE_ERR_ALIGN;
+  return moe_launch_swiglu(x, rows * d, alpha, limit, out, as_stream(stream));
+}
+
+size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
+  if (check_dims(n, E, k, H, I)) return 0;
+  size_t off[10], total;
+  layout(n, E, k, H, I, off, &total);
+  return total;
+}
+
+int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
+                         size_t offsets[10]) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (!offsets) return MOE_ERR_NULL;
+  size_t total;
+  layout(n, E, k, H, I, offsets, &total);
+  return MOE_OK;
+}
+
+int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
+                      const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,
+                      const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                      const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                      const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
+                      float alpha, float limit, uint16_t* out, void* workspace,
+                      size_t workspace_bytes, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!x || !norm_w || !gate_w || !gate_b || !mlp1_blocks || !mlp1_scales || !mlp1_bias ||
+      !mlp2_blocks || !mlp2_scales || !mlp2_bias || !out || !workspace)
+    return MOE_ERR_NULL;
+  if (!aligned16(x) || !aligned16(norm_w) || !aligned16(gate_w) || !aligned16(mlp1_blocks) ||
+      !aligned16(mlp1_scales) || !aligned16(mlp2_blocks) || !aligned16(mlp2_scales) ||
+      ((uintptr_t)out & 7u) || ((uintptr_t)workspace & 255u))
+    return MOE_ERR_ALIGN;
+  size_t off[10], total;
+  layout(n, E, k, H, I, off, &total);
+  if (workspace_bytes < total) return MOE_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  uint16_t* t = (uint16_t*)(ws + off[0]);
+  int32_t* idx = (int32_t*)(ws + off[1]);
+  uint16_t* w = (uint16_t*)(ws + off[2]);
+  int32_t* indptr = (int32_t*)(ws + off[3]);
+  int32_t* sp = (int32_t*)(ws + off[4]);
+  int32_t* ti = (int32_t*)(ws + off[5]);
+  int32_t* ei = (int32_t*)(ws + off[6]);
+  int32_t* pp = (int32_t*)(ws + off[7]);
+  float* act = (float*)(ws + off[8]);
+  float* y = (float*)(ws + off[9]);
+  hipStream_t s = as_stream(stream);
+  const int nk = (int)(n * k);
+  if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
+                              idx, w, s)))
+    return rc;
+  if ((rc = moe_launch_permute(idx, nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s))) return rc;
+  if ((rc = moe_launch_expert_gemv(t, 0, indptr, sp, (int)k, 0, 1, mlp1_blocks, mlp1_scales,
+                                   mlp1_bias, (int)E, (int)(2 * I), (int)H, 1, alpha, limit, act,
+                                   (int)I, s)))
+    return rc;
+  if ((rc = moe_launch_expert_gemv(act, 1, indptr, sp, (int)k, 2, 0, mlp2_blocks, mlp2_scales,
+                                   mlp2_bias, (int)E, (int)H, (int)I, 0, 0.f, 0.f, y, (int)H, s)))
+    return rc;
+  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
+}
+
+}  // extern "C"

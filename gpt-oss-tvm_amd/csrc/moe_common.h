@@ -1,0 +1,88 @@
+// Shared device helpers for the gfx950 MXFP4 MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+constexpr int kWave = 64;
+
+// Status codes returned across the C ABI (mirrored in include/moe_gfx950.h).
+enum Status : int {
+  kOk = 0,
+  kErrNull = -1,
+  kErrShape = -2,
+  kErrAlign = -3,
+  kErrUnsupported = -4,
+  kErrLaunch = -5,
+  kErrWorkspace = -6,
+};
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 round-to-nearest-even on the bit pattern (NaN -> quiet NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// E8M0 byte -> fp32 2^(s-127); s = 0 is the fp32 subnormal 2^-127 and s = 255
+// is +inf, as exp2(float(s - 127)) gives (model/mlp.py:297-298).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+  return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// e2m1 code -> fp32 value (model/mlp.py:9-26), by construction from the bits:
+// exponent field e = (c>>1)&3, mantissa bit m = c&1; e = 0 is the subnormal
+// 0.5*m, otherwise 2^(e-1) * (1 + m/2); bit 3 is the sign.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 1) & 3u, m = c & 1u;
+  const float mag = e == 0 ? 0.5f * (float)m : __uint_as_float((126u + e) << 23) * (1.0f + 0.5f * (float)m);
+  return (c & 8u) ? -mag : mag;
+}
+
+// Eight e2m1 codes (one dword, element 2b from the low nibble of byte b) ->
+// eight bf16 values scaled by 2^(s-127) via gfx950's scaled fp4 conversion.
+// Exact for scales whose products stay normal in bf16.
+__device__ __forceinline__ bf16x8 dequant8(uint32_t w, float scale) {
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  bf16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Split eight fp32 values into bf16 hi + bf16 lo with a = hi + lo + O(2^-17 |a|).
+__device__ __forceinline__ void split8(const float* a, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 h = (__bf16)a[i];
+    hi[i] = h;
+    lo[i] = (__bf16)(a[i] - (float)h);
+  }
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace moe

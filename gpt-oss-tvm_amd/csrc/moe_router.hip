@@ -1,0 +1,268 @@
+// Fused RMSNorm + router GEMV + top-k + softmax, and the expert-grouping pass.
+//
+// Router: model/mlp.py:375-382 (norm -> gate -> topk -> softmax); the decode
+// variant's gating_softmax_topk call is model/mlp_optimized.py:187.
+// Grouping: mlc-llm moe_cumsum / get_indices / get_indptr / moe_expand_indptr
+// as called at model/mlp_optimized.py:119-148.
+#include <climits>
+
+#include "moe_common.h"
+
+namespace moe {
+
+// Unpack the eight bf16 of a 16-byte chunk to fp32.
+__device__ __forceinline__ void unpack8(u32x4 v, float* f) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    f[2 * d] = bf2f((uint16_t)(v[d] & 0xFFFFu));
+    f[2 * d + 1] = bf2f((uint16_t)(v[d] >> 16));
+  }
+}
+
+// One workgroup of 256 threads routes TB tokens.
+//  phase 1  one wave per token: fp64 sum of squares, r = fp32(1/sqrt(ss/H+eps)),
+//           t = bf16(x*r*w) to HBM and to LDS;
+//  phase 2  256/E threads per expert, each a strided set of 16-byte chunks of
+//           the expert's gate row, fp64 partial dots for all TB tokens; the
+//           partials are summed in a fixed order, rounded fp64->fp32->bf16, the
+//           bias added in fp32 and rounded to bf16 again;
+//  phase 3  one wave per token: k rounds of a wave arg-max under the order
+//           (logit descending, expert ascending), then an fp64 softmax.
+template <int TB>
+__global__ __launch_bounds__(256) void moe_router_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+    const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
+    int k, float eps, uint16_t* __restrict__ t_out, int32_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* t_lds = (uint16_t*)smem;                              // [TB][H]
+  double* part = (double*)(smem + (size_t)TB * H * 2);            // [256][TB]
+  float* logit = (float*)((unsigned char*)part + 256 * TB * 8);   // [TB][E]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tok0 = blockIdx.x * TB;
+  const int H8 = H >> 3;
+
+  for (int tb = wave; tb < TB; tb += 4) {
+    const int tok = tok0 + tb;
+    u32x4* trow_lds = (u32x4*)(t_lds + (size_t)tb * H);
+    if (tok < n) {
+      const u32x4* xr = (const u32x4*)(x + (size_t)tok * H);
+      double ss = 0.0;
+      for (int c = lane; c < H8; c += kWave) {
+        float f[8];
+        unpack8(xr[c], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fma((double)f[i], (double)f[i], ss);
+      }
+      ss = wave_sum(ss);
+      const float r = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
+      u32x4* trow = (u32x4*)(t_out + (size_t)tok * H);
+      const u32x4* wr = (const u32x4*)norm_w;
+      for (int c = lane; c < H8; c += kWave) {
+        float f[8], g[8];
+        unpack8(xr[c], f);
+        unpack8(wr[c], g);
+        u32x4 o;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], r), g[2 * d]));
+          const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], r), g[2 * d + 1]));
+          o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        trow[c] = o;
+        trow_lds[c] = o;
+      }
+    } else {
+      for (int c = lane; c < H8; c += kWave) trow_lds[c] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __syncthreads();
+
+  const int ks = 256 / E;  // threads per expert
+  {
+    const int e = tid / ks, s = tid - (tid / ks) * ks;
+    double acc[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[tb] = 0.0;
+    if (e < E) {
+      const u32x4* wr = (const u32x4*)(gate_w + (size_t)e * H);
+      for (int c = s; c < H8; c += ks) {
+        float wf[8];
+        unpack8(wr[c], wf);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          float tf[8];
+          unpack8(((const u32x4*)(t_lds + (size_t)tb * H))[c], tf);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[tb] = fma((double)tf[i], (double)wf[i], acc[tb]);
+        }
+      }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) part[tid * TB + tb] = acc[tb];
+  }
+  __syncthreads();
+  for (int pi = tid; pi < E * TB; pi += 256) {
+    const int e = pi / TB, tb = pi - (pi / TB) * TB;
+    double sum = 0.0;
+    for (int s = 0; s < ks; ++s) sum += part[(e * ks + s) * TB + tb];
+    const float dot = bf2f(f2bf((float)sum));
+    logit[tb * E + e] = bf2f(f2bf(__fadd_rn(dot, bf2f(gate_b[e]))));
+  }
+  __syncthreads();
+
+  for (int tb = wave; tb < TB; tb += 4) {
+    const int tok = tok0 + tb;
+    if (tok >= n) continue;
+    float v[4];
+    bool taken[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < E ? logit[tb * E + e] : 0.0f;
+      taken[j] = e >= E;
+    }
+    double sel_v[8];
+    int sel_i[8];
+    for (int j = 0; j < k; ++j) {
+      float bv = -INFINITY;
+      int bi = INT_MAX;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int e = lane + 64 * jj;
+        if (!taken[jj] && (v[jj] > bv || (v[jj] == bv && e < bi))) {
+          bv = v[jj];
+          bi = e;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (bi < E && (bi & 63) == lane) taken[bi >> 6] = true;
+      sel_v[j] = (double)bv;
+      sel_i[j] = bi < E ? bi : 0;
+    }
+    if (lane == 0) {
+      double ex[8], sum = 0.0;
+      for (int j = 0; j < k; ++j) {
+        ex[j] = exp(sel_v[j] - sel_v[0]);
+        sum = j == 0 ? ex[0] : sum + ex[j];
+      }
+      for (int j = 0; j < k; ++j) {
+        idx_out[(size_t)tok * k + j] = sel_i[j];
+        w_out[(size_t)tok * k + j] = f2bf((float)(ex[j] / sum));
+      }
+    }
+  }
+}
+
+// Stable counting sort of the n*k (token, slot) pairs by expert, one
+// workgroup.  Totals come from LDS atomics (order-free); placement is
+// deterministic: within a round of 1024 pairs a pair's rank among same-expert
+// pairs comes from ballots, so pairs keep flattened (token, slot) order inside
+// each expert, exactly as np.argsort(kind="stable").  Pairs whose expert id is
+// out of range are not placed (pair_pos = -1).
+__global__ __launch_bounds__(1024) void moe_permute_kernel(
+    const int32_t* __restrict__ idx, int nk, int k, int E, int32_t* __restrict__ indptr,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
+  __shared__ int cnt[256];
+  __shared__ int base[256];
+  __shared__ int wcnt[16 * 256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < nk; p += 1024) {
+    const int v = idx[p];
+    if (v >= 0 && v < E) atomicAdd(&cnt[v], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      base[e] = run;
+      indptr[e] = run;
+      run += cnt[e];
+    }
+    indptr[E] = run;
+  }
+  __syncthreads();
+
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int round0 = 0; round0 < nk; round0 += 1024) {
+    const int p = round0 + tid;
+    const bool inb = p < nk;
+    const int v = inb ? idx[p] : -1;
+    const bool ok = inb && v >= 0 && v < E;
+    for (int i = tid; i < 16 * E; i += 1024) wcnt[(i / E) * 256 + (i % E)] = 0;
+    __syncthreads();
+    uint64_t same = __ballot(ok);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = ((v >> b) & 1) != 0;
+      const uint64_t bb = __ballot(ok && bit);
+      same &= bit ? bb : ~bb;
+    }
+    const int rank = __popcll(same & lt);
+    if (ok && rank == 0) wcnt[wave * 256 + v] = __popcll(same);
+    __syncthreads();
+    if (ok) {
+      int pos = base[v] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcnt[w * 256 + v];
+      sorted_pairs[pos] = p;
+      token_indices[pos] = p / k;
+      expert_ids[pos] = v;
+      pair_pos[p] = pos;
+    } else if (inb) {
+      pair_pos[p] = -1;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 1024) {
+      int s = 0;
+      for (int w = 0; w < 16; ++w) s += wcnt[w * 256 + e];
+      base[e] += s;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace moe
+
+extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* gate_w,
+                                 const void* gate_b, int n, int H, int E, int k, float eps,
+                                 void* t_out, void* idx_out, void* w_out, hipStream_t stream) {
+  if (n == 0) return moe::kOk;
+  const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
+                 *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
+  uint16_t *pt = (uint16_t*)t_out, *pw = (uint16_t*)w_out;
+  int32_t* pi = (int32_t*)idx_out;
+  // One token per workgroup while that fills the chip; four once the gate
+  // matrix re-reads (one per workgroup) start to cost more than latency.
+  if (n <= 512) {
+    const size_t lds = (size_t)1 * H * 2 + 256 * 1 * 8 + (size_t)1 * E * 4;
+    hipLaunchKernelGGL(moe::moe_router_kernel<1>, dim3(n), dim3(256), lds, stream, px, pn, pg, pb,
+                       n, H, E, k, eps, pt, pi, pw);
+  } else {
+    const size_t lds = (size_t)4 * H * 2 + 256 * 4 * 8 + (size_t)4 * E * 4;
+    hipLaunchKernelGGL(moe::moe_router_kernel<4>, dim3((n + 3) / 4), dim3(256), lds, stream, px, pn,
+                       pg, pb, n, H, E, k, eps, pt, pi, pw);
+  }
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}
+
+extern "C" int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr,
+                                  void* sorted_pairs, void* token_indices, void* expert_ids,
+                                  void* pair_pos, hipStream_t stream) {
+  hipLaunchKernelGGL(moe::moe_permute_kernel, dim3(1), dim3(1024), 0, stream, (const int32_t*)idx,
+                     nk, k, E, (int32_t*)indptr, (int32_t*)sorted_pairs, (int32_t*)token_indices,
+                     (int32_t*)expert_ids, (int32_t*)pair_pos);
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}

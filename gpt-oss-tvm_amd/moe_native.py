@@ -1,0 +1,250 @@
+"""ctypes binding of libmoe_gfx950.so (the C ABI declared in include/moe_gfx950.h).
+
+Every wrapper takes torch tensors that already live on the GPU, checks dtype,
+shape, device and contiguity the way the reference's ``T.match_buffer`` does
+(a mismatch raises before anything is launched), and launches on torch's
+current HIP stream.  A non-zero status from the library raises RuntimeError.
+
+There is no fallback: if the library is missing this module raises on import.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoe_gfx950.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it with `python gpt-oss-tvm_amd/build_native.py` "
+        "(or __graft_entry__.build()); the MoE block has no non-HIP fallback")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_INT = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "moe_version": ([], _INT),
+    "moe_status_string": ([_INT], ctypes.c_char_p),
+    "moe_dequant_mxfp4": ([_P, _P, _P, _I64, _P], _INT),
+    "moe_dequant_mxfp4_fast": ([_P, _P, _P, _I64, _P], _INT),
+    "moe_router_topk": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P], _INT),
+    "moe_permute": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P], _INT),
+    "moe_einsum_workspace_bytes": ([_I64, _I64, _I64], _SZ),
+    "moe_einsum_fused": ([_P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P],
+                         _INT),
+    "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P], _INT),
+    "moe_mlp2": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
+    "moe_gemv_gating": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _INT),
+    "moe_swiglu": ([_P, _I64, _I64, _F, _F, _P, _P], _INT),
+    "moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
+    "moe_workspace_layout": ([_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)], _INT),
+    "moe_block_forward": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                           _F, _F, _F, _P, _P, _SZ, _P], _INT),
+}
+for _name, (_args, _ret) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _ret
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib():
+    return _lib
+
+
+def status_string(code: int) -> str:
+    return _lib.moe_status_string(code).decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {status_string(rc)} ({rc})")
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _expect(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a GPU tensor, got device {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous tensor")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+# ---------------------------------------------------------------------------
+# Operators (one per C entry point)
+# ---------------------------------------------------------------------------
+
+def dequant_mxfp4(blocks: torch.Tensor, scales: torch.Tensor, fast: bool = False) -> torch.Tensor:
+    """[..., 16] u8 blocks + [...] u8 scales -> [..., 32] bf16 (model/mlp.py:172-234)."""
+    _expect(blocks, "blocks", torch.uint8)
+    _expect(scales, "scales", torch.uint8, tuple(blocks.shape[:-1]))
+    if blocks.shape[-1] != 16:
+        raise ValueError(f"blocks: last dim must be 16, got {blocks.shape[-1]}")
+    rows = scales.numel()
+    out = torch.empty(tuple(blocks.shape[:-1]) + (32,), dtype=torch.bfloat16, device=blocks.device)
+    fn = _lib.moe_dequant_mxfp4_fast if fast else _lib.moe_dequant_mxfp4
+    _check(fn(_ptr(blocks), _ptr(scales), _ptr(out), rows, _stream()), "moe_dequant_mxfp4")
+    return out
+
+
+def router_topk(x, norm_w, gate_w, gate_b, k: int, eps: float = 1e-5):
+    """x [n, H] -> (t [n, H] bf16, idx [n, k] int32, w [n, k] bf16); model/mlp.py:375-382."""
+    n, H = x.shape
+    E = gate_w.shape[0]
+    _expect(x, "x", torch.bfloat16)
+    _expect(norm_w, "norm.weight", torch.bfloat16, (H,))
+    _expect(gate_w, "gate.weight", torch.bfloat16, (E, H))
+    _expect(gate_b, "gate.bias", torch.bfloat16, (E,))
+    t = torch.empty_like(x)
+    idx = torch.empty((n, k), dtype=torch.int32, device=x.device)
+    w = torch.empty((n, k), dtype=torch.bfloat16, device=x.device)
+    _check(_lib.moe_router_topk(_ptr(x), _ptr(norm_w), _ptr(gate_w), _ptr(gate_b), n, H, E, k, eps,
+                                _ptr(t), _ptr(idx), _ptr(w), _stream()), "moe_router_topk")
+    return t, idx, w
+
+
+def permute(idx: torch.Tensor, num_experts: int) -> dict:
+    """Group (token, slot) pairs by expert; model/mlp_optimized.py:119-148."""
+    _expect(idx, "expert_indices", torch.int32)
+    n, k = idx.shape
+    dev = idx.device
+    nk = n * k
+    res = {
+        "indptr": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        "sorted_pairs": torch.empty(nk, dtype=torch.int32, device=dev),
+        "token_indices": torch.empty(nk, dtype=torch.int32, device=dev),
+        "expert_ids": torch.empty(nk, dtype=torch.int32, device=dev),
+        "pair_pos": torch.empty(nk, dtype=torch.int32, device=dev),
+    }
+    _check(_lib.moe_permute(_ptr(idx), n, k, num_experts, _ptr(res["indptr"]),
+                            _ptr(res["sorted_pairs"]), _ptr(res["token_indices"]),
+                            _ptr(res["expert_ids"]), _ptr(res["pair_pos"]), _stream()),
+           "moe_permute")
+    return res
+
+
+def einsum_fused(x, expert_indices, blocks, scales, bias) -> torch.Tensor:
+    """moe_einsum_fused (model/mlp.py:267-326): fp32 out [n, k, N]."""
+    _expect(expert_indices, "expert_indices", torch.int32)
+    n, k = expert_indices.shape
+    E, N, G, _ = blocks.shape
+    K = G * 32
+    x3 = x.dim() == 3
+    if x3:
+        _expect(x, "x", torch.float32, (n, k, K))
+    else:
+        _expect(x, "x", torch.bfloat16, (n, K))
+    _expect(blocks, "weight_blocks", torch.uint8, (E, N, G, 16))
+    _expect(scales, "weight_scales", torch.uint8, (E, N, G))
+    _expect(bias, "bias", torch.bfloat16, (E, N))
+    out = torch.empty((n, k, N), dtype=torch.float32, device=x.device)
+    wsb = _lib.moe_einsum_workspace_bytes(n, k, E)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    _check(_lib.moe_einsum_fused(_ptr(x), int(x3), _ptr(expert_indices), n, k, E, N, K, _ptr(blocks),
+                                 _ptr(scales), _ptr(bias), _ptr(out), _ptr(ws), wsb, _stream()),
+           "moe_einsum_fused")
+    return out
+
+
+def mlp1_swiglu(t, indptr, sorted_pairs, k, blocks, scales, bias, alpha, limit, act=None):
+    n, H = t.shape
+    E, N2, G, _ = blocks.shape
+    inter = N2 // 2
+    _expect(t, "t", torch.bfloat16)
+    _expect(blocks, "mlp1_weight_blocks", torch.uint8, (E, 2 * inter, H // 32, 16))
+    _expect(scales, "mlp1_weight_scales", torch.uint8, (E, 2 * inter, H // 32))
+    _expect(bias, "mlp1_bias", torch.bfloat16, (E, 2 * inter))
+    if act is None:
+        act = torch.empty((n * k, inter), dtype=torch.float32, device=t.device)
+    _check(_lib.moe_mlp1_swiglu(_ptr(t), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
+                                _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit, _ptr(act),
+                                _stream()), "moe_mlp1_swiglu")
+    return act
+
+
+def mlp2(act, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
+    E, H, G, _ = blocks.shape
+    inter = G * 32
+    _expect(act, "act", torch.float32, (n * k, inter))
+    _expect(blocks, "mlp2_weight_blocks", torch.uint8, (E, H, G, 16))
+    _expect(scales, "mlp2_weight_scales", torch.uint8, (E, H, G))
+    _expect(bias, "mlp2_bias", torch.bfloat16, (E, H))
+    if y is None:
+        y = torch.empty((n * k, H), dtype=torch.float32, device=act.device)
+    _check(_lib.moe_mlp2(_ptr(act), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
+                         _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()), "moe_mlp2")
+    return y
+
+
+def gemv_gating(y: torch.Tensor, w: torch.Tensor, x: torch.Tensor | None = None, out=None):
+    """moe_gemv_gating (model/mlp.py:340-369) [+ residual, mlp.py:402]."""
+    n, k, N = y.shape
+    _expect(y, "x", torch.float32)
+    _expect(w, "e_weights", torch.bfloat16, (n, k))
+    if x is not None:
+        _expect(x, "residual", torch.bfloat16, (n, N))
+    if out is None:
+        out = torch.empty((n, N), dtype=torch.bfloat16, device=y.device)
+    _check(_lib.moe_gemv_gating(_ptr(y), _ptr(w), _ptr(x), n, k, N, _ptr(out), _stream()),
+           "moe_gemv_gating")
+    return out
+
+
+def swiglu(x: torch.Tensor, alpha: float, limit: float) -> torch.Tensor:
+    """Interleaved clamped SwiGLU, fp32 (model/mlp.py:29-60)."""
+    _expect(x, "x", torch.float32)
+    if x.shape[-1] % 2:
+        raise ValueError("swiglu: last dim must be even")
+    d = x.shape[-1] // 2
+    rows = x.numel() // max(x.shape[-1], 1)
+    out = torch.empty(tuple(x.shape[:-1]) + (d,), dtype=torch.float32, device=x.device)
+    _check(_lib.moe_swiglu(_ptr(x), rows, d, alpha, limit, _ptr(out), _stream()), "moe_swiglu")
+    return out
+
+
+def workspace_bytes(n, E, k, H, inter) -> int:
+    return int(_lib.moe_workspace_bytes(n, E, k, H, inter))
+
+
+def workspace_layout(n, E, k, H, inter) -> list[int]:
+    offs = (_SZ * 10)()
+    _check(_lib.moe_workspace_layout(n, E, k, H, inter, offs), "moe_workspace_layout")
+    return list(offs)
+
+
+def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
+    """Whole block in one C call (model/mlp.py:371-402).  x [n, H] bf16."""
+    n, H = x.shape
+    E = params["gate.weight"].shape[0]
+    inter = params["mlp2_weight_blocks"].shape[2] * 32
+    if out is None:
+        out = torch.empty_like(x)
+    _check(_lib.moe_block_forward(
+        _ptr(x), n, E, k, H, inter, _ptr(params["norm.weight"]), _ptr(params["gate.weight"]),
+        _ptr(params["gate.bias"]), _ptr(params["mlp1_weight_blocks"]),
+        _ptr(params["mlp1_weight_scales"]), _ptr(params["mlp1_bias"]),
+        _ptr(params["mlp2_weight_blocks"]), _ptr(params["mlp2_weight_scales"]),
+        _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
+        workspace.numel(), _stream()), "moe_block_forward")
+    return out

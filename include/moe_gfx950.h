@@ -1,0 +1,188 @@
+/*
+ * libmoe_gfx950 -- C ABI of the MI355X (gfx950) MXFP4 mixture-of-experts block.
+ *
+ * Every entry point replaces one operator of the reference MoE path
+ * (brekkylab/gpt-oss-tvm); the citation above each declaration names the
+ * reference operator and where it is defined or called.  The reference's
+ * operators are destination-passing TIR prim_funcs called through
+ * nn.tensor_ir_op: the caller (Relax VM) owns every output and the kernel
+ * allocates nothing.  These entry points keep that contract:
+ *
+ *   - all buffers are caller-owned device pointers; outputs come last but one;
+ *   - nothing is allocated and the host never waits on the device, so every
+ *     call can be captured in a HIP graph;
+ *   - the last argument is the HIP stream (hipStream_t) to launch on, NULL for
+ *     the default stream;
+ *   - the return value is MOE_OK or a negative MOE_ERR_* code; on error no
+ *     kernel was launched and no output was written.  Nothing throws across
+ *     the ABI.
+ *
+ * Tensor conventions: bf16 tensors are uint16_t bit patterns, row-major,
+ * 16-byte aligned.  MXFP4 weights stay in the checkpoint layout of
+ * model/mlp.py:100-144: blocks uint8 [E, N, K/32, 16] (element 2j of a block
+ * in the low nibble of byte j), scales uint8 E8M0 [E, N, K/32], bias bf16
+ * [E, N].  H = hidden size, I = intermediate size, E = experts, k = experts
+ * per token, n = tokens.
+ *
+ * Supported shapes: H % 64 == 0, I % 32 == 0, H <= 3072, I <= 3072,
+ * 1 <= k <= 8, k <= E <= 256, 0 <= n and n*k < 2^31.
+ *
+ * Threading: stateless and re-entrant; calls on one stream execute in order.
+ */
+#ifndef MOE_GFX950_H_
+#define MOE_GFX950_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_ERR_NULL (-1)        /* a required pointer is NULL */
+#define MOE_ERR_SHAPE (-2)       /* unsupported or inconsistent shape */
+#define MOE_ERR_ALIGN (-3)       /* a pointer is not 16-byte aligned */
+#define MOE_ERR_UNSUPPORTED (-4) /* valid but unsupported parameter value */
+#define MOE_ERR_LAUNCH (-5)      /* the HIP runtime rejected a launch */
+#define MOE_ERR_WORKSPACE (-6)   /* workspace smaller than moe_workspace_bytes() */
+
+typedef void* moe_stream_t; /* a hipStream_t */
+
+#if defined(__GNUC__)
+#define MOE_API __attribute__((visibility("default")))
+#else
+#define MOE_API
+#endif
+
+/* Library version (major*10000 + minor*100 + patch). */
+MOE_API int moe_version(void);
+
+/* Static description of a status code. */
+MOE_API const char* moe_status_string(int status);
+
+/*
+ * Standalone MXFP4 -> bf16 dequantisation.
+ * Replaces: dequant_mxfp4, model/mlp.py:172-234 (MLPBlock.__dequantize_mxfp4_weight,
+ * mlp.py:146-236).  blocks [rows, 16] u8, scales [rows] u8 E8M0 (the raw byte;
+ * the reference subtracts 127 before the call, mlp.py:155), out [rows, 32] bf16.
+ * Bit-exact for all 256 x 256 (byte, scale) pairs.
+ */
+MOE_API int moe_dequant_mxfp4(const uint8_t* blocks, const uint8_t* scales, uint16_t* out, int64_t rows,
+                      moe_stream_t stream);
+
+/*
+ * The same dequantisation through the hardware conversion used inside the
+ * expert matmuls (v_cvt_scalef32_pk_bf16_fp4); exposed so the fused path's
+ * dequantisation can be compared with moe_dequant_mxfp4.
+ * Replaces: the in-kernel LUT dequant of mxfp4_moe_mlp*_{prefill,decode},
+ * model/mlp_optimized.py:324-331, 441-446, 549-554, 644-647.
+ */
+MOE_API int moe_dequant_mxfp4_fast(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
+                           int64_t rows, moe_stream_t stream);
+
+/*
+ * RMSNorm + router linear + top-k + softmax.
+ * Replaces: model/mlp.py:375-382 (self.norm, self.gate, nn.op.topk, nn.op.softmax);
+ * mlc-llm gating_softmax_topk as called at model/mlp_optimized.py:118,187.
+ * x [n, H] bf16, norm_w [H], gate_w [E, H], gate_b [E] bf16 ->
+ * t [n, H] bf16 (normalised tokens), idx [n, k] int32 (descending logit,
+ * lower index on ties), w [n, k] bf16 (softmax over the k selected logits).
+ */
+MOE_API int moe_router_topk(const uint16_t* x, const uint16_t* norm_w, const uint16_t* gate_w,
+                    const uint16_t* gate_b, int64_t n, int64_t H, int64_t E, int64_t k, float eps,
+                    uint16_t* t, int32_t* idx, uint16_t* w, moe_stream_t stream);
+
+/*
+ * Expert grouping: stable counting sort of the n*k (token, slot) pairs by expert.
+ * Replaces: mlc-llm moe_cumsum + get_indices + get_indptr(inclusive=False) and the
+ * moe_expand_indptr prim_func, model/mlp_optimized.py:119-148.
+ * idx [n, k] int32 -> indptr [E+1], sorted_pairs [n*k] (sorted position -> pair
+ * p = token*k + slot), token_indices [n*k] (-> token), expert_ids [n*k]
+ * (-> expert), pair_pos [n*k] (pair -> sorted position, -1 if idx was out of range).
+ */
+MOE_API int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int32_t* indptr,
+                int32_t* sorted_pairs, int32_t* token_indices, int32_t* expert_ids,
+                int32_t* pair_pos, moe_stream_t stream);
+
+/*
+ * Raw expert matmul: out[s, r, c] = bias[e, c] + sum_i x[s, (r,) i] * W_e[c, i],
+ * e = expert_indices[s, r], fp32 out [n, k, N].
+ * Replaces: moe_einsum_fused, model/mlp.py:267-326 (MLPBlock.run_einsum, mlp.py:238-326).
+ * x is bf16 [n, K] when x_is_3d_f32 == 0 (the mlp1 call, mlp.py:387) or fp32
+ * [n, k, K] when 1 (the mlp2 call, mlp.py:395).  workspace holds the grouping:
+ * at least moe_einsum_workspace_bytes(n, k, E) bytes.
+ */
+MOE_API size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E);
+MOE_API int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indices, int64_t n,
+                     int64_t k, int64_t E, int64_t N, int64_t K, const uint8_t* blocks,
+                     const uint8_t* scales, const uint16_t* bias, float* out, void* workspace,
+                     size_t workspace_bytes, moe_stream_t stream);
+
+/*
+ * mlp1 with the interleaved clamped SwiGLU epilogue, over grouped pairs.
+ * Replaces: mxfp4_moe_mlp1_{prefill,decode}, model/mlp_optimized.py:214-571, with
+ * the fp32 semantics of model/mlp.py:387-390 (run_einsum + swiglu(out_dtype=float32)).
+ * t [n, H] bf16, indptr/sorted_pairs from moe_permute; weights [E, 2I, H/32, 16],
+ * [E, 2I, H/32], bias [E, 2I] -> act [n*k, I] fp32, row = sorted position.
+ */
+MOE_API int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
+                    int64_t n, int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
+                    const uint8_t* scales, const uint16_t* bias, float alpha, float limit,
+                    float* act, moe_stream_t stream);
+
+/*
+ * mlp2 over grouped pairs.
+ * Replaces: mxfp4_moe_mlp2_{prefill,decode}, model/mlp_optimized.py:353-460, 573-660,
+ * with the fp32 semantics of model/mlp.py:395.
+ * act [n*k, I] fp32 (row = sorted position); weights [E, H, I/32, 16], [E, H, I/32],
+ * bias [E, H] -> y [n*k, H] fp32, row = pair p = token*k + slot.
+ */
+MOE_API int moe_mlp2(const float* act, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
+             int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
+             const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream);
+
+/*
+ * Gate-weighted sum of the k expert outputs, plus the residual when x != NULL.
+ * Replaces: moe_gemv_gating, model/mlp.py:340-369 (MLPBlock.run_gating, mlp.py:328-369)
+ * and the residual add of mlp.py:402; the prefill combine scatter_output * w +
+ * moe_sum + x of model/mlp_optimized.py:168-172.
+ * y [n, k, N] fp32, w [n, k] bf16, x [n, N] bf16 or NULL -> out [n, N] bf16.
+ */
+MOE_API int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
+                    int64_t N, uint16_t* out, moe_stream_t stream);
+
+/*
+ * Interleaved clamped SwiGLU, fp32: x [rows, 2d] -> out [rows, d].
+ * Replaces: swiglu, model/mlp.py:29-60 (out_dtype float32 as called at mlp.py:390).
+ */
+MOE_API int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, float limit, float* out,
+               moe_stream_t stream);
+
+/*
+ * Whole block: out = x + MoE(RMSNorm(x)).
+ * Replaces: MLPBlock.forward, model/mlp.py:371-402 (and model/mlp_optimized.py:94-107).
+ * x [n, H] bf16 and the nine parameters in checkpoint layout (model/mlp.py:63-144)
+ * -> out [n, H] bf16.  workspace: at least moe_workspace_bytes(n, E, k, H, I)
+ * bytes, 256-byte aligned; its layout is given by moe_workspace_layout().
+ */
+MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I);
+
+/* Byte offsets of the intermediates inside the block workspace, in this order:
+ * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos, act, y. */
+MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
+                         size_t offsets[10]);
+
+MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
+                      const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,
+                      const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                      const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                      const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
+                      float alpha, float limit, uint16_t* out, void* workspace,
+                      size_t workspace_bytes, moe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_GFX950_H_ */

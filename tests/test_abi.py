@@ -1,0 +1,118 @@
+"""The C-ABI library loads, exports every entry point of include/moe_gfx950.h, and
+rejects bad arguments with the documented status codes before touching the GPU.
+
+No kernel is launched here (this suite runs without a GPU): every call below
+fails host-side validation.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "moe_gfx950.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"MOE_API\s+[\w\s\*]+?\b(moe_\w+)\s*\(", text)))
+
+
+def header_codes():
+    return {m[0]: int(m[1]) for m in re.findall(r"#define (MOE_\w+) \(?(-?\d+)\)?", open(HEADER).read())}
+
+
+@pytest.fixture(scope="module")
+def native():
+    import moe_native
+    return moe_native
+
+
+def test_header_declares_entry_points():
+    syms = header_symbols()
+    for name in ("moe_block_forward", "moe_router_topk", "moe_permute", "moe_einsum_fused",
+                 "moe_mlp1_swiglu", "moe_mlp2", "moe_gemv_gating", "moe_dequant_mxfp4"):
+        assert name in syms
+
+
+def test_library_exports_every_header_symbol(native):
+    lib = native.lib()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+        assert name in native.EXPORTED, f"{name} has no ctypes signature in moe_native"
+
+
+def test_internal_launchers_are_hidden(native):
+    with pytest.raises(AttributeError):
+        getattr(native.lib(), "moe_launch_expert_gemv")
+
+
+def test_status_codes_match_header(native):
+    codes = header_codes()
+    assert codes["MOE_OK"] == 0
+    for name in ("MOE_ERR_NULL", "MOE_ERR_SHAPE", "MOE_ERR_ALIGN", "MOE_ERR_UNSUPPORTED",
+                 "MOE_ERR_LAUNCH", "MOE_ERR_WORKSPACE"):
+        assert codes[name] < 0
+        assert native.status_string(codes[name]) not in ("unknown status", "ok")
+    assert native.lib().moe_version() >= 100
+
+
+def test_validation_rejects_bad_arguments(native):
+    L = native.lib()
+    codes = header_codes()
+    P = ctypes.c_void_p
+    fake = P(0x1000)        # aligned, never dereferenced: validation fails first
+    odd = P(0x1008)
+    # unsupported k / E
+    assert L.moe_router_topk(fake, fake, fake, fake, 4, 2880, 32, 9, 1e-5, fake, fake, fake, None) \
+        == codes["MOE_ERR_UNSUPPORTED"]
+    assert L.moe_router_topk(fake, fake, fake, fake, 4, 2880, 300, 4, 1e-5, fake, fake, fake, None) \
+        == codes["MOE_ERR_UNSUPPORTED"]
+    # H not a multiple of 8
+    assert L.moe_router_topk(fake, fake, fake, fake, 4, 2882, 32, 4, 1e-5, fake, fake, fake, None) \
+        == codes["MOE_ERR_SHAPE"]
+    # null / misaligned pointers
+    assert L.moe_router_topk(None, fake, fake, fake, 4, 2880, 32, 4, 1e-5, fake, fake, fake, None) \
+        == codes["MOE_ERR_NULL"]
+    assert L.moe_router_topk(odd, fake, fake, fake, 4, 2880, 32, 4, 1e-5, fake, fake, fake, None) \
+        == codes["MOE_ERR_ALIGN"]
+    # block: hidden not a multiple of 64, intermediate not a multiple of 32
+    args = [fake] * 9
+    assert L.moe_block_forward(fake, 4, 32, 4, 2880 + 32, 2880, *args, 1e-5, 1.702, 7.0, fake,
+                               fake, 1 << 30, None) == codes["MOE_ERR_SHAPE"]
+    assert L.moe_block_forward(fake, 4, 32, 4, 2880, 2880 + 16, *args, 1e-5, 1.702, 7.0, fake,
+                               fake, 1 << 30, None) == codes["MOE_ERR_SHAPE"]
+    # workspace too small
+    assert L.moe_block_forward(fake, 4, 32, 4, 2880, 2880, *args, 1e-5, 1.702, 7.0, fake, fake,
+                               16, None) == codes["MOE_ERR_WORKSPACE"]
+    # workspace not 256-byte aligned
+    assert L.moe_block_forward(fake, 4, 32, 4, 2880, 2880, *args, 1e-5, 1.702, 7.0, fake,
+                               P(0x1010), 1 << 30, None) == codes["MOE_ERR_ALIGN"]
+    # einsum: N not a multiple of 64, K beyond the supported maximum
+    assert L.moe_einsum_fused(fake, 0, fake, 4, 4, 32, 100, 2880, fake, fake, fake, fake, fake,
+                              1 << 20, None) == codes["MOE_ERR_SHAPE"]
+    assert L.moe_einsum_fused(fake, 0, fake, 4, 4, 32, 128, 4096, fake, fake, fake, fake, fake,
+                              1 << 20, None) == codes["MOE_ERR_SHAPE"]
+    assert L.moe_einsum_fused(fake, 0, fake, 4, 4, 32, 128, 2880, fake, fake, fake, fake, fake,
+                              8, None) == codes["MOE_ERR_WORKSPACE"]
+    # permute: E out of range
+    assert L.moe_permute(fake, 4, 4, 0, fake, fake, fake, fake, fake, None) == codes["MOE_ERR_UNSUPPORTED"]
+    # gating: N not a multiple of 4
+    assert L.moe_gemv_gating(fake, fake, None, 4, 4, 2882, fake, None) == codes["MOE_ERR_SHAPE"]
+    # dequant: negative rows, null
+    assert L.moe_dequant_mxfp4(fake, fake, fake, -1, None) == codes["MOE_ERR_SHAPE"]
+    assert L.moe_dequant_mxfp4(None, fake, fake, 16, None) == codes["MOE_ERR_NULL"]
+    # empty inputs are a successful no-op without any launch
+    assert L.moe_block_forward(fake, 0, 32, 4, 2880, 2880, *args, 1e-5, 1.702, 7.0, fake, fake, 0,
+                               None) == codes["MOE_OK"]
+    assert L.moe_dequant_mxfp4(None, None, None, 0, None) == codes["MOE_OK"]
+
+
+def test_workspace_layout(native):
+    n, E, k, H, I = 64, 32, 4, 2880, 2880
+    total = native.workspace_bytes(n, E, k, H, I)
+    offs = native.workspace_layout(n, E, k, H, I)
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert offs[-1] + n * k * H * 4 <= total
+    assert native.workspace_bytes(n, E, k, H + 1, I) == 0
