@@ -173,9 +173,12 @@ def main() -> int:
     value = n / (dt / args.steps)
     log(f"timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {value:.0f} tok/s")
 
-    # second pass: per-stage HIP events on the launch stream
+    # second pass: per-stage HIP events on the launch stream.  A spin kernel is
+    # queued first so the host runs ahead of the GPU and the events time the
+    # kernels, not gaps left by Python between launches.
     stages = ("router", "permute", "mlp1", "mlp2", "combine")
     recs = []
+    torch.cuda._sleep(int(2.4e9 * 0.4e-3 * args.steps))
     for i in range(args.steps):
         ev = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for s in stages}

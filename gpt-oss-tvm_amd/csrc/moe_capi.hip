@@ -14,10 +14,12 @@ int moe_launch_router(const void* x, const void* norm_w, const void* gate_w, con
                       void* w_out, hipStream_t stream);
 int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void* sorted_pairs,
                        void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
-int moe_launch_expert_gemv(const void* x, int x_f32, const void* indptr, const void* sorted_pairs,
-                           int k_top, int brow_mode, int orow_mode, const void* blocks,
-                           const void* scales, const void* bias, int E, int N, int K, int swiglu,
-                           float alpha, float limit, void* out, int out_ld, hipStream_t stream);
+int moe_launch_expert_gemv(const void* x, const void* x_lo, int x_ld, const void* indptr,
+                           const void* sorted_pairs, int k_top, int brow_mode, int orow_mode,
+                           const void* blocks, const void* scales, const void* bias, int E, int N,
+                           int K, int max_tokens, int swiglu, float alpha, float limit, void* out,
+                           void* out_lo, int out_ld, hipStream_t stream);
+int moe_launch_split(const void* x, int64_t count, void* hi, void* lo, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -43,9 +45,12 @@ int check_dims(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[10], size_t* total) {
+constexpr int kNumRegions = 11;
+
+void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kNumRegions],
+            size_t* total) {
   const size_t nk = (size_t)n * (size_t)k;
-  const size_t sizes[10] = {
+  const size_t sizes[kNumRegions] = {
       (size_t)n * H * 2,      // t       bf16 [n, H]
       nk * 4,                 // idx     int32 [n, k]
       nk * 2,                 // w       bf16 [n, k]
@@ -54,11 +59,12 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[10
       nk * 4,                 // token_indices
       nk * 4,                 // expert_ids
       nk * 4,                 // pair_pos
-      nk * (size_t)I * 4,     // act     fp32 [n*k, I]
+      nk * (size_t)I * 2,     // act_hi  bf16 [n*k, I]
+      nk * (size_t)I * 2,     // act_lo  bf16 [n*k, I]
       nk * (size_t)H * 4,     // y       fp32 [n*k, H]
   };
   size_t o = 0;
-  for (int i = 0; i < 10; ++i) {
+  for (int i = 0; i < kNumRegions; ++i) {
     off[i] = o;
     o = round_up(o + sizes[i], 256);
   }
@@ -106,7 +112,7 @@ int moe_dequant_mxfp4_fast(const uint8_t* blocks, const uint8_t* scales, uint16_
 int moe_router_topk(const uint16_t* x, const uint16_t* norm_w, const uint16_t* gate_w,
                     const uint16_t* gate_b, int64_t n, int64_t H, int64_t E, int64_t k, float eps,
                     uint16_t* t, int32_t* idx, uint16_t* w, moe_stream_t stream) {
-  if (n < 0 || H <= 0 || H % 8 || H > 8192 || n >= ((int64_t)1 << 31) / 8) return MOE_ERR_SHAPE;
+  if (n < 0 || H <= 0 || H % 8 || H > 4096 || n >= ((int64_t)1 << 31) / 8) return MOE_ERR_SHAPE;
   if (k < 1 || k > 8 || E < k || E > 256) return MOE_ERR_UNSUPPORTED;
   if (n == 0) return MOE_OK;
   if (!x || !norm_w || !gate_w || !gate_b || !t || !idx || !w) return MOE_ERR_NULL;
@@ -128,10 +134,12 @@ int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int32_t* in
                             expert_ids, pair_pos, as_stream(stream));
 }
 
-size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E) {
-  if (n < 0 || k < 1 || E < 1) return 0;
+size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K, int x_is_3d_f32) {
+  if (n < 0 || k < 1 || E < 1 || K < 0) return 0;
   const size_t nk = (size_t)n * (size_t)k;
-  return round_up((size_t)(E + 1) * 4, 256) + 4 * round_up(nk * 4, 256);
+  size_t b = round_up((size_t)(E + 1) * 4, 256) + 4 * round_up(nk * 4, 256);
+  if (x_is_3d_f32) b += 2 * round_up(nk * (size_t)K * 2, 256);
+  return b;
 }
 
 // Rows per expert matmul must be a multiple of the 64-row wave tile.
@@ -153,50 +161,64 @@ int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indic
   if (!aligned16(x) || !aligned16(blocks) || !aligned16(scales) || !aligned16(out) ||
       !aligned16(workspace))
     return MOE_ERR_ALIGN;
-  if (workspace_bytes < moe_einsum_workspace_bytes(n, k, E)) return MOE_ERR_WORKSPACE;
+  if (workspace_bytes < moe_einsum_workspace_bytes(n, k, E, K, x_is_3d_f32))
+    return MOE_ERR_WORKSPACE;
   const size_t nk = (size_t)n * (size_t)k;
   char* ws = (char*)workspace;
   int32_t* indptr = (int32_t*)ws;
   ws += round_up((size_t)(E + 1) * 4, 256);
+  const size_t seg = round_up(nk * 4, 256);
   int32_t* sp = (int32_t*)ws;
-  int32_t* ti = (int32_t*)(ws + round_up(nk * 4, 256));
-  int32_t* ei = (int32_t*)(ws + 2 * round_up(nk * 4, 256));
-  int32_t* pp = (int32_t*)(ws + 3 * round_up(nk * 4, 256));
+  int32_t* ti = (int32_t*)(ws + seg);
+  int32_t* ei = (int32_t*)(ws + 2 * seg);
+  int32_t* pp = (int32_t*)(ws + 3 * seg);
   hipStream_t s = as_stream(stream);
   rc = moe_launch_permute(expert_indices, (int)nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s);
   if (rc) return rc;
-  // mlp1-style input: B row = token; mlp2-style: B row = pair.  Output row = pair.
-  return moe_launch_expert_gemv(x, x_is_3d_f32 ? 1 : 0, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0,
-                                0, blocks, scales, bias, (int)E, (int)N, (int)K, 0, 0.f, 0.f, out,
-                                (int)N, s);
+  if (!x_is_3d_f32)  // mlp1-style: bf16 rows per token
+    return moe_launch_expert_gemv(x, nullptr, (int)K, indptr, sp, (int)k, 0, 0, blocks, scales,
+                                  bias, (int)E, (int)N, (int)K, (int)n, 0, 0.f, 0.f, out, nullptr,
+                                  (int)N, s);
+  // mlp2-style: fp32 rows per pair, split into bf16 hi/lo planes first
+  void* hi = ws + 4 * seg;
+  void* lo = (char*)hi + round_up(nk * (size_t)K * 2, 256);
+  if ((rc = moe_launch_split(x, (int64_t)(nk * K), hi, lo, s))) return rc;
+  return moe_launch_expert_gemv(hi, lo, (int)K, indptr, sp, (int)k, 1, 0, blocks, scales, bias,
+                                (int)E, (int)N, (int)K, (int)n, 0, 0.f, 0.f, out, nullptr, (int)N, s);
 }
 
 int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
                     int64_t n, int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
                     const uint8_t* scales, const uint16_t* bias, float alpha, float limit,
-                    float* act, moe_stream_t stream) {
+                    uint16_t* act_hi, uint16_t* act_lo, moe_stream_t stream) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (n == 0) return MOE_OK;
-  if (!t || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act) return MOE_ERR_NULL;
-  if (!aligned16(t) || !aligned16(blocks) || !aligned16(scales) || !aligned16(act))
+  if (!t || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act_hi || !act_lo)
+    return MOE_ERR_NULL;
+  if (!aligned16(t) || !aligned16(blocks) || !aligned16(scales) || ((uintptr_t)act_hi & 3u) ||
+      ((uintptr_t)act_lo & 3u))
     return MOE_ERR_ALIGN;
-  return moe_launch_expert_gemv(t, 0, indptr, sorted_pairs, (int)k, 0, 1, blocks, scales, bias,
-                                (int)E, (int)(2 * I), (int)H, 1, alpha, limit, act, (int)I,
-                                as_stream(stream));
+  return moe_launch_expert_gemv(t, nullptr, (int)H, indptr, sorted_pairs, (int)k, 0, 1, blocks,
+                                scales, bias, (int)E, (int)(2 * I), (int)H, (int)n, 1, alpha, limit,
+                                act_hi, act_lo, (int)I, as_stream(stream));
 }
 
-int moe_mlp2(const float* act, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
-             int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
-             const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream) {
+int moe_mlp2(const uint16_t* act_hi, const uint16_t* act_lo, const int32_t* indptr,
+             const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
+             const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, float* y,
+             moe_stream_t stream) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (n == 0) return MOE_OK;
-  if (!act || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y) return MOE_ERR_NULL;
-  if (!aligned16(act) || !aligned16(blocks) || !aligned16(scales) || !aligned16(y))
+  if (!act_hi || !act_lo || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y)
+    return MOE_ERR_NULL;
+  if (!aligned16(act_hi) || !aligned16(act_lo) || !aligned16(blocks) || !aligned16(scales) ||
+      !aligned16(y))
     return MOE_ERR_ALIGN;
-  return moe_launch_expert_gemv(act, 1, indptr, sorted_pairs, (int)k, 2, 0, blocks, scales, bias,
-                                (int)E, (int)H, (int)I, 0, 0.f, 0.f, y, (int)H, as_stream(stream));
+  return moe_launch_expert_gemv(act_hi, act_lo, (int)I, indptr, sorted_pairs, (int)k, 2, 0, blocks,
+                                scales, bias, (int)E, (int)H, (int)I, (int)n, 0, 0.f, 0.f, y, nullptr,
+                                (int)H, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -221,13 +243,13 @@ int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, float limit
 
 size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
   if (check_dims(n, E, k, H, I)) return 0;
-  size_t off[10], total;
+  size_t off[kNumRegions], total;
   layout(n, E, k, H, I, off, &total);
   return total;
 }
 
 int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                         size_t offsets[10]) {
+                         size_t offsets[11]) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (!offsets) return MOE_ERR_NULL;
@@ -253,7 +275,7 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
       !aligned16(mlp1_scales) || !aligned16(mlp2_blocks) || !aligned16(mlp2_scales) ||
       ((uintptr_t)out & 7u) || ((uintptr_t)workspace & 255u))
     return MOE_ERR_ALIGN;
-  size_t off[10], total;
+  size_t off[kNumRegions], total;
   layout(n, E, k, H, I, off, &total);
   if (workspace_bytes < total) return MOE_ERR_WORKSPACE;
   char* ws = (char*)workspace;
@@ -265,20 +287,22 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   int32_t* ti = (int32_t*)(ws + off[5]);
   int32_t* ei = (int32_t*)(ws + off[6]);
   int32_t* pp = (int32_t*)(ws + off[7]);
-  float* act = (float*)(ws + off[8]);
-  float* y = (float*)(ws + off[9]);
+  uint16_t* act_hi = (uint16_t*)(ws + off[8]);
+  uint16_t* act_lo = (uint16_t*)(ws + off[9]);
+  float* y = (float*)(ws + off[10]);
   hipStream_t s = as_stream(stream);
   const int nk = (int)(n * k);
   if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
                               idx, w, s)))
     return rc;
   if ((rc = moe_launch_permute(idx, nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s))) return rc;
-  if ((rc = moe_launch_expert_gemv(t, 0, indptr, sp, (int)k, 0, 1, mlp1_blocks, mlp1_scales,
-                                   mlp1_bias, (int)E, (int)(2 * I), (int)H, 1, alpha, limit, act,
-                                   (int)I, s)))
+  if ((rc = moe_launch_expert_gemv(t, nullptr, (int)H, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+                                   mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, 1,
+                                   alpha, limit, act_hi, act_lo, (int)I, s)))
     return rc;
-  if ((rc = moe_launch_expert_gemv(act, 1, indptr, sp, (int)k, 2, 0, mlp2_blocks, mlp2_scales,
-                                   mlp2_bias, (int)E, (int)H, (int)I, 0, 0.f, 0.f, y, (int)H, s)))
+  if ((rc = moe_launch_expert_gemv(act_hi, act_lo, (int)I, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                                   mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, 0, 0.f, 0.f,
+                                   y, nullptr, (int)H, s)))
     return rc;
   return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
 }

@@ -18,12 +18,23 @@ __global__ __launch_bounds__(256) void moe_gating_kernel(const float* __restrict
   const int tok = blockIdx.y;
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= N) return;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int r = 0; r < k; ++r) {
-    const float wr = bf2f(w[(size_t)tok * k + r]);
-    const f32x4 v = *(const f32x4*)(y + ((size_t)tok * k + r) * N + c);
+  // all k loads first (k <= 8), then the in-order sum
+  f32x4 v[8];
+  float wr[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], wr));
+  for (int r = 0; r < 8; ++r) {
+    if (r < k) {
+      v[r] = *(const f32x4*)(y + ((size_t)tok * k + r) * N + c);
+      wr[r] = bf2f(w[(size_t)tok * k + r]);
+    }
+  }
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (r < k) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[r][i], wr[r]));
+    }
   }
   uint16_t o[4];
 #pragma unroll

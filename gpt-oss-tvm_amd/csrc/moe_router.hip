@@ -19,59 +19,79 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
   }
 }
 
-// One workgroup of 256 threads routes TB tokens.
+// One workgroup of 1024 threads (16 waves) routes TB <= 16 tokens.
 //  phase 1  one wave per token: fp64 sum of squares, r = fp32(1/sqrt(ss/H+eps)),
 //           t = bf16(x*r*w) to HBM and to LDS;
-//  phase 2  256/E threads per expert, each a strided set of 16-byte chunks of
+//  phase 2  1024/E threads per expert, each a strided set of 16-byte chunks of
 //           the expert's gate row, fp64 partial dots for all TB tokens; the
 //           partials are summed in a fixed order, rounded fp64->fp32->bf16, the
 //           bias added in fp32 and rounded to bf16 again;
 //  phase 3  one wave per token: k rounds of a wave arg-max under the order
 //           (logit descending, expert ascending), then an fp64 softmax.
+// Loads are issued in unconditional batches (indices clamped in range) so that
+// each thread has one batch of requests in flight instead of a chain.
+constexpr int kRouterThreads = 1024;
+constexpr int kRouterWaves = kRouterThreads / 64;
+
 template <int TB>
-__global__ __launch_bounds__(256) void moe_router_kernel(
+__global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
     int k, float eps, uint16_t* __restrict__ t_out, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out) {
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* t_lds = (uint16_t*)smem;                              // [TB][H]
-  double* part = (double*)(smem + (size_t)TB * H * 2);            // [256][TB]
-  float* logit = (float*)((unsigned char*)part + 256 * TB * 8);   // [TB][E]
+  uint16_t* t_lds = (uint16_t*)smem;                                      // [TB][H]
+  double* part = (double*)(smem + (size_t)TB * H * 2);                    // [1024][TB]
+  float* logit = (float*)((unsigned char*)part + kRouterThreads * TB * 8);  // [TB][E]
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int tok0 = blockIdx.x * TB;
   const int H8 = H >> 3;
 
-  for (int tb = wave; tb < TB; tb += 4) {
+  constexpr int kMaxChunks = 8;  // H <= 4096: at most 8 16-byte chunks per lane
+  for (int tb = wave; tb < TB; tb += kRouterWaves) {
     const int tok = tok0 + tb;
     u32x4* trow_lds = (u32x4*)(t_lds + (size_t)tb * H);
     if (tok < n) {
       const u32x4* xr = (const u32x4*)(x + (size_t)tok * H);
-      double ss = 0.0;
-      for (int c = lane; c < H8; c += kWave) {
-        float f[8];
-        unpack8(xr[c], f);
+      const u32x4* wr = (const u32x4*)norm_w;
+      u32x4 xv[kMaxChunks], wv[kMaxChunks];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fma((double)f[i], (double)f[i], ss);
+      for (int i = 0; i < kMaxChunks; ++i) {
+        const int c = min(lane + kWave * i, H8 - 1);
+        xv[i] = xr[c];
+        wv[i] = wr[c];
+      }
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < kMaxChunks; ++i) {
+        if (lane + kWave * i < H8) {
+          float f[8];
+          unpack8(xv[i], f);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+        }
       }
       ss = wave_sum(ss);
       const float r = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
       u32x4* trow = (u32x4*)(t_out + (size_t)tok * H);
-      const u32x4* wr = (const u32x4*)norm_w;
-      for (int c = lane; c < H8; c += kWave) {
-        float f[8], g[8];
-        unpack8(xr[c], f);
-        unpack8(wr[c], g);
-        u32x4 o;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], r), g[2 * d]));
-          const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], r), g[2 * d + 1]));
-          o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+      for (int i = 0; i < kMaxChunks; ++i) {
+        const int c = lane + kWave * i;
+        if (c < H8) {
+          float f[8], g[8];
+          unpack8(xv[i], f);
+          unpack8(wv[i], g);
+          u32x4 o;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], r), g[2 * d]));
+            const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], r), g[2 * d + 1]));
+            o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+          }
+          trow[c] = o;
+          trow_lds[c] = o;
         }
-        trow[c] = o;
-        trow_lds[c] = o;
       }
     } else {
       for (int c = lane; c < H8; c += kWave) trow_lds[c] = u32x4{0u, 0u, 0u, 0u};
@@ -79,23 +99,33 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
   }
   __syncthreads();
 
-  const int ks = 256 / E;  // threads per expert
+  const int ks = kRouterThreads / E;  // threads per expert
   {
     const int e = tid / ks, s = tid - (tid / ks) * ks;
     double acc[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[tb] = 0.0;
     if (e < E) {
+      constexpr int kBatch = 12;
       const u32x4* wr = (const u32x4*)(gate_w + (size_t)e * H);
-      for (int c = s; c < H8; c += ks) {
-        float wf[8];
-        unpack8(wr[c], wf);
+      for (int c0 = s; c0 < H8; c0 += kBatch * ks) {
+        u32x4 wv[kBatch];
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          float tf[8];
-          unpack8(((const u32x4*)(t_lds + (size_t)tb * H))[c], tf);
+        for (int u = 0; u < kBatch; ++u) wv[u] = wr[min(c0 + u * ks, H8 - 1)];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[tb] = fma((double)tf[i], (double)wf[i], acc[tb]);
+        for (int u = 0; u < kBatch; ++u) {
+          const int c = c0 + u * ks;
+          if (c < H8) {
+            float wf[8];
+            unpack8(wv[u], wf);
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+              float tf[8];
+              unpack8(((const u32x4*)(t_lds + (size_t)tb * H))[c], tf);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) acc[tb] = fma((double)tf[i], (double)wf[i], acc[tb]);
+            }
+          }
         }
       }
     }
@@ -103,7 +133,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
     for (int tb = 0; tb < TB; ++tb) part[tid * TB + tb] = acc[tb];
   }
   __syncthreads();
-  for (int pi = tid; pi < E * TB; pi += 256) {
+  for (int pi = tid; pi < E * TB; pi += kRouterThreads) {
     const int e = pi / TB, tb = pi - (pi / TB) * TB;
     double sum = 0.0;
     for (int s = 0; s < ks; ++s) sum += part[(e * ks + s) * TB + tb];
@@ -112,7 +142,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
   }
   __syncthreads();
 
-  for (int tb = wave; tb < TB; tb += 4) {
+  for (int tb = wave; tb < TB; tb += kRouterWaves) {
     const int tok = tok0 + tb;
     if (tok >= n) continue;
     float v[4];
@@ -246,13 +276,14 @@ extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* 
   int32_t* pi = (int32_t*)idx_out;
   // One token per workgroup while that fills the chip; four once the gate
   // matrix re-reads (one per workgroup) start to cost more than latency.
+  constexpr int NT = moe::kRouterThreads;
   if (n <= 512) {
-    const size_t lds = (size_t)1 * H * 2 + 256 * 1 * 8 + (size_t)1 * E * 4;
-    hipLaunchKernelGGL(moe::moe_router_kernel<1>, dim3(n), dim3(256), lds, stream, px, pn, pg, pb,
+    const size_t lds = (size_t)1 * H * 2 + NT * 1 * 8 + (size_t)1 * E * 4;
+    hipLaunchKernelGGL(moe::moe_router_kernel<1>, dim3(n), dim3(NT), lds, stream, px, pn, pg, pb,
                        n, H, E, k, eps, pt, pi, pw);
   } else {
-    const size_t lds = (size_t)4 * H * 2 + 256 * 4 * 8 + (size_t)4 * E * 4;
-    hipLaunchKernelGGL(moe::moe_router_kernel<4>, dim3((n + 3) / 4), dim3(256), lds, stream, px, pn,
+    const size_t lds = (size_t)4 * H * 2 + NT * 4 * 8 + (size_t)4 * E * 4;
+    hipLaunchKernelGGL(moe::moe_router_kernel<4>, dim3((n + 3) / 4), dim3(NT), lds, stream, px, pn,
                        pg, pb, n, H, E, k, eps, pt, pi, pw);
   }
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;

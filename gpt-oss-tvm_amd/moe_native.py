@@ -37,11 +37,12 @@ _SIGS = {
     "moe_dequant_mxfp4_fast": ([_P, _P, _P, _I64, _P], _INT),
     "moe_router_topk": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P], _INT),
     "moe_permute": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P], _INT),
-    "moe_einsum_workspace_bytes": ([_I64, _I64, _I64], _SZ),
+    "moe_einsum_workspace_bytes": ([_I64, _I64, _I64, _I64, _INT], _SZ),
     "moe_einsum_fused": ([_P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P],
                          _INT),
-    "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P], _INT),
-    "moe_mlp2": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
+    "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P, _P],
+                        _INT),
+    "moe_mlp2": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
     "moe_gemv_gating": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _INT),
     "moe_swiglu": ([_P, _I64, _I64, _F, _F, _P, _P], _INT),
     "moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
@@ -159,7 +160,7 @@ def einsum_fused(x, expert_indices, blocks, scales, bias) -> torch.Tensor:
     _expect(scales, "weight_scales", torch.uint8, (E, N, G))
     _expect(bias, "bias", torch.bfloat16, (E, N))
     out = torch.empty((n, k, N), dtype=torch.float32, device=x.device)
-    wsb = _lib.moe_einsum_workspace_bytes(n, k, E)
+    wsb = _lib.moe_einsum_workspace_bytes(n, k, E, K, int(x3))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
     _check(_lib.moe_einsum_fused(_ptr(x), int(x3), _ptr(expert_indices), n, k, E, N, K, _ptr(blocks),
                                  _ptr(scales), _ptr(bias), _ptr(out), _ptr(ws), wsb, _stream()),
@@ -168,6 +169,7 @@ def einsum_fused(x, expert_indices, blocks, scales, bias) -> torch.Tensor:
 
 
 def mlp1_swiglu(t, indptr, sorted_pairs, k, blocks, scales, bias, alpha, limit, act=None):
+    """mlp1 + SwiGLU over grouped pairs -> (act_hi, act_lo) bf16 [n*k, I], act = hi + lo."""
     n, H = t.shape
     E, N2, G, _ = blocks.shape
     inter = N2 // 2
@@ -176,24 +178,26 @@ def mlp1_swiglu(t, indptr, sorted_pairs, k, blocks, scales, bias, alpha, limit, 
     _expect(scales, "mlp1_weight_scales", torch.uint8, (E, 2 * inter, H // 32))
     _expect(bias, "mlp1_bias", torch.bfloat16, (E, 2 * inter))
     if act is None:
-        act = torch.empty((n * k, inter), dtype=torch.float32, device=t.device)
+        act = torch.empty((2, n * k, inter), dtype=torch.bfloat16, device=t.device)
     _check(_lib.moe_mlp1_swiglu(_ptr(t), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
-                                _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit, _ptr(act),
-                                _stream()), "moe_mlp1_swiglu")
+                                _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit, _ptr(act[0]),
+                                _ptr(act[1]), _stream()), "moe_mlp1_swiglu")
     return act
 
 
 def mlp2(act, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
+    """mlp2 over grouped pairs; act = (hi, lo) planes [2, n*k, I] -> y fp32 [n*k, H] by pair."""
     E, H, G, _ = blocks.shape
     inter = G * 32
-    _expect(act, "act", torch.float32, (n * k, inter))
+    _expect(act, "act", torch.bfloat16, (2, n * k, inter))
     _expect(blocks, "mlp2_weight_blocks", torch.uint8, (E, H, G, 16))
     _expect(scales, "mlp2_weight_scales", torch.uint8, (E, H, G))
     _expect(bias, "mlp2_bias", torch.bfloat16, (E, H))
     if y is None:
         y = torch.empty((n * k, H), dtype=torch.float32, device=act.device)
-    _check(_lib.moe_mlp2(_ptr(act), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
-                         _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()), "moe_mlp2")
+    _check(_lib.moe_mlp2(_ptr(act[0]), _ptr(act[1]), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H,
+                         inter, _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()),
+           "moe_mlp2")
     return y
 
 
@@ -228,7 +232,7 @@ def workspace_bytes(n, E, k, H, inter) -> int:
 
 
 def workspace_layout(n, E, k, H, inter) -> list[int]:
-    offs = (_SZ * 10)()
+    offs = (_SZ * 11)()
     _check(_lib.moe_workspace_layout(n, E, k, H, inter, offs), "moe_workspace_layout")
     return list(offs)
 

@@ -110,37 +110,44 @@ MOE_API int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int
  * e = expert_indices[s, r], fp32 out [n, k, N].
  * Replaces: moe_einsum_fused, model/mlp.py:267-326 (MLPBlock.run_einsum, mlp.py:238-326).
  * x is bf16 [n, K] when x_is_3d_f32 == 0 (the mlp1 call, mlp.py:387) or fp32
- * [n, k, K] when 1 (the mlp2 call, mlp.py:395).  workspace holds the grouping:
- * at least moe_einsum_workspace_bytes(n, k, E) bytes.
+ * [n, k, K] when 1 (the mlp2 call, mlp.py:395).  workspace holds the grouping
+ * (and, for fp32 x, its bf16 hi/lo split): at least
+ * moe_einsum_workspace_bytes(n, k, E, K, x_is_3d_f32) bytes, 16-byte aligned.
  */
-MOE_API size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E);
-MOE_API int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indices, int64_t n,
-                     int64_t k, int64_t E, int64_t N, int64_t K, const uint8_t* blocks,
-                     const uint8_t* scales, const uint16_t* bias, float* out, void* workspace,
-                     size_t workspace_bytes, moe_stream_t stream);
+MOE_API size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K,
+                                          int x_is_3d_f32);
+MOE_API int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indices,
+                             int64_t n, int64_t k, int64_t E, int64_t N, int64_t K,
+                             const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias,
+                             float* out, void* workspace, size_t workspace_bytes,
+                             moe_stream_t stream);
 
 /*
  * mlp1 with the interleaved clamped SwiGLU epilogue, over grouped pairs.
  * Replaces: mxfp4_moe_mlp1_{prefill,decode}, model/mlp_optimized.py:214-571, with
  * the fp32 semantics of model/mlp.py:387-390 (run_einsum + swiglu(out_dtype=float32)).
  * t [n, H] bf16, indptr/sorted_pairs from moe_permute; weights [E, 2I, H/32, 16],
- * [E, 2I, H/32], bias [E, 2I] -> act [n*k, I] fp32, row = sorted position.
+ * [E, 2I, H/32], bias [E, 2I] -> the fp32 SwiGLU output as two bf16 planes
+ * act_hi, act_lo [n*k, I] (row = sorted position) with act = hi + lo to within
+ * 2^-17 relative: hi = bf16(act), lo = bf16(act - hi).
  */
 MOE_API int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
-                    int64_t n, int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
-                    const uint8_t* scales, const uint16_t* bias, float alpha, float limit,
-                    float* act, moe_stream_t stream);
+                            int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
+                            const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias,
+                            float alpha, float limit, uint16_t* act_hi, uint16_t* act_lo,
+                            moe_stream_t stream);
 
 /*
  * mlp2 over grouped pairs.
  * Replaces: mxfp4_moe_mlp2_{prefill,decode}, model/mlp_optimized.py:353-460, 573-660,
  * with the fp32 semantics of model/mlp.py:395.
- * act [n*k, I] fp32 (row = sorted position); weights [E, H, I/32, 16], [E, H, I/32],
- * bias [E, H] -> y [n*k, H] fp32, row = pair p = token*k + slot.
+ * act_hi, act_lo [n*k, I] bf16 (as written by moe_mlp1_swiglu); weights [E, H, I/32, 16],
+ * [E, H, I/32], bias [E, H] -> y [n*k, H] fp32, row = pair p = token*k + slot.
  */
-MOE_API int moe_mlp2(const float* act, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
-             int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
-             const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream);
+MOE_API int moe_mlp2(const uint16_t* act_hi, const uint16_t* act_lo, const int32_t* indptr,
+                     const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E, int64_t H,
+                     int64_t I, const uint8_t* blocks, const uint8_t* scales,
+                     const uint16_t* bias, float* y, moe_stream_t stream);
 
 /*
  * Gate-weighted sum of the k expert outputs, plus the residual when x != NULL.
@@ -169,9 +176,10 @@ MOE_API int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, flo
 MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I);
 
 /* Byte offsets of the intermediates inside the block workspace, in this order:
- * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos, act, y. */
+ * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos, act_hi,
+ * act_lo, y. */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                         size_t offsets[10]);
+                                 size_t offsets[11]);
 
 MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                       const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,

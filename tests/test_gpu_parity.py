@@ -190,7 +190,8 @@ def _check_block(blk, x, tr, staged=True):
         sp = host(st["perm"]["sorted_pairs"])
         k = tr.idx.shape[1]
         act_ref = tr.act.reshape(n * k, -1)[sp]
-        assert norm_rel(host(st["act"]), act_ref) <= 2e-5
+        act = host(st["act"][0].float()) + host(st["act"][1].float())  # hi + lo planes
+        assert norm_rel(act, act_ref) <= 2e-5
         y_ref = tr.y.reshape(n * k, -1)
         assert norm_rel(host(st["y"]), y_ref) <= 1e-4
     return m
