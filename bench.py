@@ -176,7 +176,7 @@ def main() -> int:
     # second pass: per-stage HIP events on the launch stream.  A spin kernel is
     # queued first so the host runs ahead of the GPU and the events time the
     # kernels, not gaps left by Python between launches.
-    stages = ("router", "permute", "mlp1", "mlp2", "combine")
+    stages = ("router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine")
     recs = []
     torch.cuda._sleep(int(2.4e9 * 0.4e-3 * args.steps))
     for i in range(args.steps):
@@ -198,7 +198,7 @@ def main() -> int:
     if not mfma_bound:
         alg = avg_touched * mlp1_weight_bytes + n * H * 2 + nk * I * 4
         achieved = alg / (stage_us["mlp1"] * 1e-6) / 1e9
-        roof = {"bound": "hbm", "kernel": "moe_expert_gemv_kernel<bf16,swiglu> (mlp1)",
+        roof = {"bound": "hbm", "kernel": "moe_mx_gemv_kernel<2,1,23> (mlp1)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(args.config),
                 "algorithmic_bytes": int(alg), "avg_us": round(stage_us["mlp1"], 2)}

@@ -14,12 +14,15 @@ int moe_launch_router(const void* x, const void* norm_w, const void* gate_w, con
                       void* w_out, hipStream_t stream);
 int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void* sorted_pairs,
                        void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
-int moe_launch_expert_gemv(const void* x, const void* x_lo, int x_ld, const void* indptr,
-                           const void* sorted_pairs, int k_top, int brow_mode, int orow_mode,
-                           const void* blocks, const void* scales, const void* bias, int E, int N,
-                           int K, int max_tokens, int swiglu, float alpha, float limit, void* out,
-                           void* out_lo, int out_ld, hipStream_t stream);
-int moe_launch_split(const void* x, int64_t count, void* hi, void* lo, hipStream_t stream);
+size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
+size_t moe_pieces_total_bytes(int64_t rows, int64_t K, int pieces);
+int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, void* packed,
+                      hipStream_t stream);
+int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* indptr,
+                       const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
+                       const void* blocks, const void* scales, const void* bias, int E, int N,
+                       int K, int max_tokens, int rows_active, int swiglu, float alpha,
+                       float limit, void* out, int out_ld, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -28,7 +31,7 @@ int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, vo
 
 namespace {
 
-constexpr int64_t kMaxK = 3072;  // reduction length limit (scale staging in LDS)
+constexpr int64_t kMaxK = 3072;  // reduction length limit (24 MFMA chunks of 128)
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -45,23 +48,26 @@ int check_dims(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-constexpr int kNumRegions = 11;
+constexpr int kNumRegions = 12;
+constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
+constexpr int kPiecesAct = 4;  // fp8 pieces of the fp32 SwiGLU output (~16 bits)
 
 void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kNumRegions],
             size_t* total) {
   const size_t nk = (size_t)n * (size_t)k;
   const size_t sizes[kNumRegions] = {
-      (size_t)n * H * 2,      // t       bf16 [n, H]
-      nk * 4,                 // idx     int32 [n, k]
-      nk * 2,                 // w       bf16 [n, k]
-      (size_t)(E + 1) * 4,    // indptr  int32 [E+1]
+      (size_t)n * H * 2,      // t        bf16 [n, H]
+      nk * 4,                 // idx      int32 [n, k]
+      nk * 2,                 // w        bf16 [n, k]
+      (size_t)(E + 1) * 4,    // indptr   int32 [E+1]
       nk * 4,                 // sorted_pairs
       nk * 4,                 // token_indices
       nk * 4,                 // expert_ids
       nk * 4,                 // pair_pos
-      nk * (size_t)I * 2,     // act_hi  bf16 [n*k, I]
-      nk * (size_t)I * 2,     // act_lo  bf16 [n*k, I]
-      nk * (size_t)H * 4,     // y       fp32 [n*k, H]
+      moe_pieces_total_bytes(n, H, kPiecesT),          // t_pieces
+      nk * (size_t)I * 4,                              // act      fp32 [n*k, I]
+      moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
+      nk * (size_t)H * 4,     // y        fp32 [n*k, H]
   };
   size_t o = 0;
   for (int i = 0; i < kNumRegions; ++i) {
@@ -134,17 +140,21 @@ int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int32_t* in
                             expert_ids, pair_pos, as_stream(stream));
 }
 
-size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K, int x_is_3d_f32) {
-  if (n < 0 || k < 1 || E < 1 || K < 0) return 0;
+static size_t einsum_grouping_bytes(int64_t n, int64_t k, int64_t E) {
   const size_t nk = (size_t)n * (size_t)k;
-  size_t b = round_up((size_t)(E + 1) * 4, 256) + 4 * round_up(nk * 4, 256);
-  if (x_is_3d_f32) b += 2 * round_up(nk * (size_t)K * 2, 256);
-  return b;
+  return round_up((size_t)(E + 1) * 4, 256) + 4 * round_up(nk * 4, 256);
 }
 
-// Rows per expert matmul must be a multiple of the 64-row wave tile.
+size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K, int x_is_3d_f32) {
+  if (n < 0 || k < 1 || E < 1 || K < 0) return 0;
+  const int64_t rows = x_is_3d_f32 ? n * k : n;
+  return einsum_grouping_bytes(n, k, E) +
+         moe_pieces_total_bytes(rows, K, x_is_3d_f32 ? kPiecesAct : kPiecesT);
+}
+
+// Output rows per expert matmul come in 16-row tiles.
 static int check_matmul(int64_t n, int64_t k, int64_t E, int64_t N, int64_t K) {
-  if (n < 0 || N <= 0 || K <= 0 || N % 64 || K % 32 || K > kMaxK) return MOE_ERR_SHAPE;
+  if (n < 0 || N <= 0 || K <= 0 || N % 16 || K % 32 || K > kMaxK) return MOE_ERR_SHAPE;
   if (k < 1 || k > 8 || E < k || E > 256) return MOE_ERR_UNSUPPORTED;
   if (n * k >= ((int64_t)1 << 31) || N * E >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
   return MOE_OK;
@@ -172,53 +182,62 @@ int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indic
   int32_t* ti = (int32_t*)(ws + seg);
   int32_t* ei = (int32_t*)(ws + 2 * seg);
   int32_t* pp = (int32_t*)(ws + 3 * seg);
+  void* packed = ws + 4 * seg;
   hipStream_t s = as_stream(stream);
   rc = moe_launch_permute(expert_indices, (int)nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s);
   if (rc) return rc;
-  if (!x_is_3d_f32)  // mlp1-style: bf16 rows per token
-    return moe_launch_expert_gemv(x, nullptr, (int)K, indptr, sp, (int)k, 0, 0, blocks, scales,
-                                  bias, (int)E, (int)N, (int)K, (int)n, 0, 0.f, 0.f, out, nullptr,
-                                  (int)N, s);
-  // mlp2-style: fp32 rows per pair, split into bf16 hi/lo planes first
-  void* hi = ws + 4 * seg;
-  void* lo = (char*)hi + round_up(nk * (size_t)K * 2, 256);
-  if ((rc = moe_launch_split(x, (int64_t)(nk * K), hi, lo, s))) return rc;
-  return moe_launch_expert_gemv(hi, lo, (int)K, indptr, sp, (int)k, 1, 0, blocks, scales, bias,
-                                (int)E, (int)N, (int)K, (int)n, 0, 0.f, 0.f, out, nullptr, (int)N, s);
+  // mlp1-style: bf16 rows per token; mlp2-style: fp32 rows per pair
+  const int rows = x_is_3d_f32 ? (int)nk : (int)n;
+  const int pieces = x_is_3d_f32 ? kPiecesAct : kPiecesT;
+  if ((rc = moe_launch_pieces(x, x_is_3d_f32, rows, (int)K, pieces, packed, s))) return rc;
+  return moe_launch_mx_gemv(packed, rows, pieces, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0, 0,
+                            blocks, scales, bias, (int)E, (int)N, (int)K, (int)nk, (int)nk, 0,
+                            0.f, 0.f, out, (int)N, s);
 }
 
-int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
+size_t moe_pieces_bytes(int64_t rows, int64_t K, int pieces) {
+  if (rows < 0 || K <= 0 || K % 32 || K > kMaxK || (pieces != 2 && pieces != 4)) return 0;
+  return moe_pieces_total_bytes(rows, K, pieces);
+}
+
+int moe_quantize_pieces(const void* x, int x_is_f32, int64_t rows, int64_t K, int pieces,
+                        void* packed, moe_stream_t stream) {
+  if (rows < 0 || K <= 0 || K % 32 || K > kMaxK || rows >= ((int64_t)1 << 31) / 96)
+    return MOE_ERR_SHAPE;
+  if (pieces != 2 && pieces != 4) return MOE_ERR_UNSUPPORTED;
+  if (rows == 0) return MOE_OK;
+  if (!x || !packed) return MOE_ERR_NULL;
+  if (!aligned16(x) || !aligned16(packed)) return MOE_ERR_ALIGN;
+  return moe_launch_pieces(x, x_is_f32, (int)rows, (int)K, pieces, packed, as_stream(stream));
+}
+
+int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr, const int32_t* sorted_pairs,
                     int64_t n, int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
                     const uint8_t* scales, const uint16_t* bias, float alpha, float limit,
-                    uint16_t* act_hi, uint16_t* act_lo, moe_stream_t stream) {
+                    float* act, moe_stream_t stream) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (n == 0) return MOE_OK;
-  if (!t || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act_hi || !act_lo)
+  if (!t_pieces || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act)
     return MOE_ERR_NULL;
-  if (!aligned16(t) || !aligned16(blocks) || !aligned16(scales) || ((uintptr_t)act_hi & 3u) ||
-      ((uintptr_t)act_lo & 3u))
-    return MOE_ERR_ALIGN;
-  return moe_launch_expert_gemv(t, nullptr, (int)H, indptr, sorted_pairs, (int)k, 0, 1, blocks,
-                                scales, bias, (int)E, (int)(2 * I), (int)H, (int)n, 1, alpha, limit,
-                                act_hi, act_lo, (int)I, as_stream(stream));
+  if (!aligned16(t_pieces) || !aligned16(blocks) || ((uintptr_t)act & 3u)) return MOE_ERR_ALIGN;
+  return moe_launch_mx_gemv(t_pieces, (int)n, kPiecesT, indptr, sorted_pairs, (int)k, 0, 1, blocks,
+                            scales, bias, (int)E, (int)(2 * I), (int)H, (int)(n * k), (int)(n * k),
+                            1, alpha, limit, act, (int)I, as_stream(stream));
 }
 
-int moe_mlp2(const uint16_t* act_hi, const uint16_t* act_lo, const int32_t* indptr,
-             const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
-             const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, float* y,
-             moe_stream_t stream) {
+int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
+             int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
+             const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (n == 0) return MOE_OK;
-  if (!act_hi || !act_lo || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y)
+  if (!act_pieces || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y)
     return MOE_ERR_NULL;
-  if (!aligned16(act_hi) || !aligned16(act_lo) || !aligned16(blocks) || !aligned16(scales) ||
-      !aligned16(y))
-    return MOE_ERR_ALIGN;
-  return moe_launch_expert_gemv(act_hi, act_lo, (int)I, indptr, sorted_pairs, (int)k, 2, 0, blocks,
-                                scales, bias, (int)E, (int)H, (int)I, (int)n, 0, 0.f, 0.f, y, nullptr,
-                                (int)H, as_stream(stream));
+  if (!aligned16(act_pieces) || !aligned16(blocks) || ((uintptr_t)y & 3u)) return MOE_ERR_ALIGN;
+  return moe_launch_mx_gemv(act_pieces, (int)(n * k), kPiecesAct, indptr, sorted_pairs, (int)k, 2,
+                            0, blocks, scales, bias, (int)E, (int)H, (int)I, (int)(n * k),
+                            (int)(n * k), 0, 0.f, 0.f, y, (int)H, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -249,7 +268,7 @@ size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I
 }
 
 int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                         size_t offsets[11]) {
+                         size_t offsets[12]) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (!offsets) return MOE_ERR_NULL;
@@ -287,22 +306,25 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   int32_t* ti = (int32_t*)(ws + off[5]);
   int32_t* ei = (int32_t*)(ws + off[6]);
   int32_t* pp = (int32_t*)(ws + off[7]);
-  uint16_t* act_hi = (uint16_t*)(ws + off[8]);
-  uint16_t* act_lo = (uint16_t*)(ws + off[9]);
-  float* y = (float*)(ws + off[10]);
+  void* t_pk = ws + off[8];
+  float* act = (float*)(ws + off[9]);
+  void* act_pk = ws + off[10];
+  float* y = (float*)(ws + off[11]);
   hipStream_t s = as_stream(stream);
   const int nk = (int)(n * k);
   if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
                               idx, w, s)))
     return rc;
   if ((rc = moe_launch_permute(idx, nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s))) return rc;
-  if ((rc = moe_launch_expert_gemv(t, nullptr, (int)H, indptr, sp, (int)k, 0, 1, mlp1_blocks,
-                                   mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, 1,
-                                   alpha, limit, act_hi, act_lo, (int)I, s)))
+  if ((rc = moe_launch_pieces(t, 0, (int)n, (int)H, kPiecesT, t_pk, s))) return rc;
+  if ((rc = moe_launch_mx_gemv(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+                               mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1,
+                               alpha, limit, act, (int)I, s)))
     return rc;
-  if ((rc = moe_launch_expert_gemv(act_hi, act_lo, (int)I, indptr, sp, (int)k, 2, 0, mlp2_blocks,
-                                   mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, 0, 0.f, 0.f,
-                                   y, nullptr, (int)H, s)))
+  if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
+  if ((rc = moe_launch_mx_gemv(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                               mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f,
+                               0.f, y, (int)H, s)))
     return rc;
   return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
 }

@@ -78,6 +78,50 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// fp8 e4m3 (OCP: bias 7, no infinities, max 448) by construction, round to
+// nearest even.  |y| must be < 448.
+__device__ __forceinline__ uint32_t e4m3_encode(float y) {
+  const uint32_t sign = __float_as_uint(y) >> 31;
+  const float a = fabsf(y);
+  uint32_t code;
+  const int e = (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127;
+  if (e < -6) {
+    code = (uint32_t)__builtin_rintf(a * 512.0f);         // subnormal steps of 2^-9 (8 -> 0x08 = 2^-6)
+  } else {
+    const float mant = a * __uint_as_float((uint32_t)(127 - e + 3) << 23);  // a / 2^e * 8 in [8, 16)
+    uint32_t mq = (uint32_t)__builtin_rintf(mant);
+    int ee = e;
+    if (mq == 16u) { mq = 8u; ++ee; }
+    code = ((uint32_t)(ee + 7) << 3) | (mq - 8u);
+  }
+  return code | (sign << 7);
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  const float mag = e == 0 ? (float)m * 0.001953125f                          // m * 2^-9
+                           : __uint_as_float((e + 120u) << 23) * (1.0f + 0.125f * (float)m);
+  return (c & 0x80u) ? -mag : mag;
+}
+
+// E8M0 exponent byte for a group whose largest magnitude is amax: the smallest
+// scale 2^(s-127) with amax / scale < 256, i.e. s = floor(log2(amax)) - 7 + 127
+// (s = 0 when amax is zero or tiny), so the group's codes stay below 256.
+__device__ __forceinline__ uint32_t e8m0_for_amax(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu);  // biased exponent of amax
+  const int s = e - 7;
+  return (uint32_t)(s < 0 ? 0 : s);
+}
+
+// v_mfma_scale_f32_16x16x128_f8f6f4, A = fp4 e2m1 (cbsz 4), B = fp8 e4m3
+// (blgp 0), one E8M0 byte per lane for each operand (byte 0 of the VGPR).
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
+__device__ __forceinline__ f32x4 mfma_mx(const i32x8& a, const i32x8& b, f32x4 c, int sa,
+                                         int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll

@@ -1,0 +1,466 @@
+// Expert matmuls on gfx950's block-scaled matrix instruction
+// v_mfma_scale_f32_16x16x128_f8f6f4: the MXFP4 weights enter the MFMA as
+// they lie in the checkpoint (e2m1 nibbles + one E8M0 byte per 32), so no
+// dequantisation runs on the vector ALUs at all.
+//
+// Reference operators: moe_einsum_fused (model/mlp.py:238-326) for the plain
+// epilogue and mxfp4_moe_mlp1_* / mxfp4_moe_mlp2_* (model/mlp_optimized.py:
+// 214-660) for the grouped-pair forms, with the fp32 semantics of
+// model/mlp.py:387-395: out = bias + sum_k x[k] * W[c, k].
+//
+// Activations as fp8 pieces.  The instruction's other operand is fp8 e4m3
+// with its own E8M0 scale per 32 elements.  An activation row x is written
+// as a sum of P pieces x = sum_p q_p * 2^(s_p - 127) + residual, each piece
+// one e4m3 code per element and one scale per 32-element block, chosen
+// greedily (the piece quantises what the earlier pieces left).  Two pieces
+// carry the 8-bit significand of a bf16 value (mlp1's normalised tokens);
+// four carry the fp32 SwiGLU output to about 16 bits.  The pieces of one
+// token occupy P of the 16 MFMA rows, so each output lane holds all pieces
+// of a token and sums them in registers.
+//
+// Operand layout of the 16x16x128 instruction (A = fp8 activations, B = fp4
+// weights, D = fp32), per 128-wide K chunk, lane l = 16 * g + r:
+//   A  row r, bytes 0..15  -> k = 16 g + 0..15, bytes 16..31 -> k = 64 + 16 g + 0..15
+//   B  column r (a weight row), nibble i (low nibble first) -> k = 32 g + i,
+//      i.e. one whole MXFP4 block: block 4 * chunk + g of that row
+//   scale_a / scale_b of lane (r, g) = the E8M0 of K block g of row / column r
+//   D  column r (weight row), elements i = 0..3 -> rows 4 g + i
+#include <cstdlib>
+#include <type_traits>
+
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int kMxMaxChunks = 24;                           // K <= 3072
+constexpr int kMxSclRun = 28;                              // scale bytes per (row, lane group)
+constexpr int kMxSclRow = 4 * kMxSclRun;                   // 112 scale bytes per piece row
+constexpr int kMxMaxGroups = 3;
+constexpr int kLdsBytes = 160 * 1024;                      // per CU
+constexpr int kNumCUs = 256;                               // MI355X
+
+// LDS bytes per staged activation row and per 16-row A operand group for a
+// kernel that runs NCT chunks (the 16-byte pad spreads the 16 rows of one
+// lane group over distinct banks).
+__host__ __device__ constexpr int mx_row_stride(int nct) { return nct * 128 + 16; }
+__host__ __device__ constexpr int mx_group_bytes(int nct) {
+  return 16 * mx_row_stride(nct) + 16 * kMxSclRow;
+}
+
+template <int S, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (S < E) {
+    f(std::integral_constant<int, S>{});
+    static_for<S + 1, E>(f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pieces.  Packed layout for `rows` rows of length K, NC = ceil(K / 128):
+//   q  [rows][P][NC * 128]   e4m3 codes, zero beyond K
+//   qs [rows][P][4][28]      qs[.., g, c] = E8M0 of block 4c + g (0 past K)
+// One thread per (row, 32-element block).
+template <int P, bool kF32>
+__global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict__ x, int rows,
+                                                         int K, int NC, uint8_t* __restrict__ q,
+                                                         uint8_t* __restrict__ qs) {
+  const int nblk = 4 * NC;
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (int64_t)rows * nblk) return;
+  const int row = (int)(id / nblk), blk = (int)(id - (int64_t)row * nblk);
+  const int c = blk >> 2, g = blk & 3;
+  const int Kp = NC * 128;
+  float r[32];
+  if (blk * 32 < K) {
+    if constexpr (kF32) {
+      const f32x4* src = (const f32x4*)((const float*)x + (size_t)row * K + blk * 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f32x4 v = src[i];
+        r[4 * i] = v[0]; r[4 * i + 1] = v[1]; r[4 * i + 2] = v[2]; r[4 * i + 3] = v[3];
+      }
+    } else {
+      const u32x4* src = (const u32x4*)((const uint16_t*)x + (size_t)row * K + blk * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = src[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          r[8 * i + 2 * j] = __uint_as_float(v[j] << 16);
+          r[8 * i + 2 * j + 1] = __uint_as_float(v[j] & 0xFFFF0000u);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) r[i] = 0.0f;
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(r[i]));
+    const uint32_t s = e8m0_for_amax(amax);
+    const float inv = __uint_as_float((254u - s) << 23);                       // 2^(127 - s)
+    const float sc = s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u);  // 2^(s - 127)
+    uint32_t pk[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pk[i] = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t code = e4m3_encode(r[i] * inv);
+      r[i] -= e4m3_decode(code) * sc;   // exact: the code's value is a rounding of r[i]
+      pk[i >> 2] |= code << (8 * (i & 3));
+    }
+    const size_t prow = (size_t)row * P + p;
+    u32x4* dst = (u32x4*)(q + prow * Kp + blk * 32);
+    dst[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    dst[1] = u32x4{pk[4], pk[5], pk[6], pk[7]};
+    uint8_t* run = qs + prow * kMxSclRow + g * kMxSclRun;
+    run[c] = (uint8_t)s;
+    if (c == NC - 1)
+      for (int z = NC; z < kMxSclRun; ++z) run[z] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped expert GEMV.  Grid (S, E): workgroup (s, e) serves expert e and the
+// 16-row weight tiles [s * tiles_per_wg, (s + 1) * tiles_per_wg), dealt
+// round-robin to its waves.  Per batch of at most `groups_cap` * 16/P of the
+// expert's tokens it stages their pieces in LDS; each wave then takes its
+// tiles one at a time: the NCT scale bytes and NCT weight loads of the tile's
+// 16 rows x K (MFMA-native: lane (r, g) reads block 4c + g of row r, 16 B, for
+// chunk c) are issued together, scales first, so MFMA c waits only for the
+// loads up to chunk c; every token group then runs NCT MFMAs over them.  The
+// first tile's loads are issued before the LDS staging, so they overlap it.
+//
+// arow_mode: piece row of sorted position j: 0 = sorted_pairs[j] / k_top
+// (token), 1 = sorted_pairs[j] (pair), 2 = j.  orow_mode: output row: 0 =
+// sorted_pairs[j], 1 = j.  kEpi: 0 = store y (N columns), 1 = interleaved
+// SwiGLU (N/2 columns).
+template <int P, int kEpi, int NCT>
+__global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
+    const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
+    int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
+    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G,
+    int tiles_per_wg, int groups_cap, float alpha, float limit, float* __restrict__ out,
+    int out_ld) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int TPG = 16 / P;  // tokens per 16-row operand group
+  constexpr int kMxRowStride = mx_row_stride(NCT);
+  constexpr int kMxGroupBytes = mx_group_bytes(NCT);
+  const int e = blockIdx.y;
+  const int start = indptr[e];
+  const int cnt = indptr[e + 1] - start;
+  if (cnt <= 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int t_begin = blockIdx.x * tiles_per_wg;
+  const int t_end = min(t_begin + tiles_per_wg, N >> 4);
+  const int tpb = groups_cap * TPG;
+
+  u32x4 w[NCT];
+  float bn = 0.0f;
+  // This wave's staging area for the scale bytes of its current tile.
+  uint8_t* const sstage = lds + groups_cap * kMxGroupBytes + wave * (16 * G);
+  // Block index of chunk c for this lane: 4c + g.  Past K the lane re-reads
+  // block G-1 (finite data; its A operand bytes are zero).  With NCT == 23
+  // (89 <= G <= 92) only the last chunk can pass K, so the others address
+  // from one base with immediate offsets.  The opaque copy of g keeps the
+  // compiler from hoisting 2*NCT per-chunk offsets out of the tile loop.
+  // The tile's 16 x G scale bytes are contiguous and 16-byte aligned: two
+  // 16-byte loads per lane fetch them (G <= 96 units), issued before the
+  // weights so they land first; they pass through LDS to reach the lane that
+  // needs each byte.
+  auto issue = [&](int tile) {
+    int gl = g;
+    asm volatile("" : "+v"(gl));
+    const size_t row0 = (size_t)e * N + (tile << 4);
+    const size_t wrow = row0 + r;
+    const uint8_t* wp = blocks + wrow * G * 16;
+    const uint8_t* st = scales + row0 * G;
+    const u32x4 s0 = *(const u32x4*)(st + min(lane, G - 1) * 16);
+    const u32x4 s1 = *(const u32x4*)(st + min(lane + 64, G - 1) * 16);
+    bn = bf2f(bias[wrow]);
+    static_for<0, NCT>([&](auto cv) {
+      constexpr int c = decltype(cv)::value;
+      const int blk = (NCT == 23 && c < 22) ? 4 * c + gl : min(4 * c + gl, G - 1);
+      w[c] = *(const u32x4*)(wp + blk * 16);
+    });
+    if (lane < G) *(u32x4*)(sstage + lane * 16) = s0;
+    if (lane + 64 < G) *(u32x4*)(sstage + (lane + 64) * 16) = s1;
+  };
+  // Scale byte of chunk c for this lane, read from the staging area.
+  auto scale_b = [&](int c) -> uint32_t {
+    const int blk = (NCT == 23 && c < 22) ? 4 * c + g : min(4 * c + g, G - 1);
+    return sstage[r * G + blk];
+  };
+  if (t_begin + wave < t_end) issue(t_begin + wave);
+
+  if (NCT * 128 > Kp) {  // zero the K tail of every staged row once
+    const int tail16 = (NCT * 128 - Kp) >> 4;
+    for (int u = threadIdx.x; u < groups_cap * 16 * tail16; u += blockDim.x) {
+      const int row = u / tail16, c = u - row * tail16;
+      *(u32x4*)(lds + (row >> 4) * kMxGroupBytes + (row & 15) * kMxRowStride + Kp + c * 16) =
+          u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  for (int b0 = 0; b0 < cnt; b0 += tpb) {
+    const int nb = min(tpb, cnt - b0);
+    if (b0) __syncthreads();  // the previous batch's operands are no longer read
+    {
+      // Stage the batch: 16-byte units, kFill loads in flight per thread.
+      // Units past the end repeat the last one (same data to the same place).
+      constexpr int kFill = NCT == 23 ? 8 : 4;
+      const int row16 = Kp >> 4;
+      const int units = row16 + kMxSclRow / 16;
+      const int total = nb * P * units;
+      for (int u0 = threadIdx.x; u0 < total; u0 += kFill * blockDim.x) {
+        u32x4 v[kFill];
+        uint32_t dst[kFill];
+#pragma unroll
+        for (int i = 0; i < kFill; ++i) {
+          const int u = min(u0 + i * (int)blockDim.x, total - 1);
+          const int rp = u / units, c = u - rp * units;
+          const int tt = rp / P, p = rp - tt * P;
+          const int j = start + b0 + tt;
+          const int row = arow_mode == 0 ? sorted_pairs[j] / k_top
+                          : arow_mode == 1 ? sorted_pairs[j] : j;
+          const int gi = tt / TPG, m = (tt - gi * TPG) * P + p;
+          const size_t prow = (size_t)row * P + p;
+          if (c < row16) {
+            v[i] = *(const u32x4*)(q + prow * Kp + c * 16);
+            dst[i] = gi * kMxGroupBytes + m * kMxRowStride + c * 16;
+          } else {
+            v[i] = *(const u32x4*)(qs + prow * kMxSclRow + (c - row16) * 16);
+            dst[i] = gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + (c - row16) * 16;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kFill; ++i) *(u32x4*)(lds + dst[i]) = v[i];
+      }
+    }
+    __syncthreads();
+    const int ngroups = (nb + TPG - 1) / TPG;
+
+    for (int it = 0;; ++it) {
+      const int tile = t_begin + wave + nwaves * it;
+      if (tile >= t_end) break;
+      if (it > 0 || b0 > 0) issue(tile);
+      const int r0 = tile << 4;
+
+      for (int gi = 0; gi < ngroups; ++gi) {
+        const uint8_t* ar = lds + gi * kMxGroupBytes + r * kMxRowStride + 16 * g;
+        const uint8_t* as = lds + gi * kMxGroupBytes + 16 * kMxRowStride + r * kMxSclRow +
+                            g * kMxSclRun;
+        // A operands stream from LDS one chunk ahead of the MFMA chain; the
+        // scheduling barrier after each MFMA keeps at most two chunks live.
+        auto load_a = [&](int c) {
+          const u32x4 a0 = *(const u32x4*)(ar + 128 * c);
+          const u32x4 a1 = *(const u32x4*)(ar + 128 * c + 64);
+          return i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                       (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+        };
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t sa = *(const uint32_t*)as;
+        uint32_t sb = scale_b(0);
+        i32x8 acur = load_a(0);
+        static_for<0, NCT>([&](auto cv) {
+          constexpr int c = decltype(cv)::value;
+          i32x8 anext;
+          uint32_t sa_next = 0, sb_next = 0;
+          if constexpr (c + 1 < NCT) {
+            anext = load_a(c + 1);
+            sb_next = scale_b(c + 1);
+          }
+          if constexpr ((c & 3) == 3 && c + 1 < NCT) sa_next = *(const uint32_t*)(as + c + 1);
+          const i32x8 B = {(int)w[c][0], (int)w[c][1], (int)w[c][2], (int)w[c][3], 0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(acur, B, acc, 0, 4, c & 3, (int)sa,
+                                                                 0, (int)sb);
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (c + 1 < NCT) {
+            acur = anext;
+            sb = sb_next;
+          }
+          if constexpr ((c & 3) == 3 && c + 1 < NCT) sa = sa_next;
+        });
+        // The MFMAs combine operands of all 64 lanes, so they must run with the
+        // full wave active.  Their results are only stored under per-lane
+        // conditions below; without this barrier the compiler may sink the
+        // whole chain into that divergent branch.
+        asm volatile("" : "+v"(acc));
+        // lane (r, g): weight row r0 + r; operand rows 4g + i hold token
+        // (4g + i) / P, piece (4g + i) % P of this group
+        if constexpr (P == 4) {
+          const int tt = gi * TPG + g;
+          const float y = (((acc[3] + acc[2]) + acc[1]) + acc[0]) + bn;
+          if (tt < nb) {
+            const int j = start + b0 + tt;
+            const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+            out[(size_t)orow * out_ld + r0 + r] = y;
+          }
+        } else {
+          const float y0 = (acc[1] + acc[0]) + bn;
+          const float y1 = (acc[3] + acc[2]) + bn;
+          const int tt0 = gi * TPG + 2 * g;
+          if constexpr (kEpi == 1) {
+            const float l0 = __shfl_xor(y0, 1, kWave);  // odd rows hold the linear half
+            const float l1 = __shfl_xor(y1, 1, kWave);
+            if ((r & 1) == 0) {
+              const float yy[2] = {y0, y1}, ll[2] = {l0, l1};
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                if (tt0 + h < nb) {
+                  const int j = start + b0 + tt0 + h;
+                  const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+                  const float xg = fminf(yy[h], limit);
+                  const float xl = fminf(fmaxf(ll[h], -limit), limit);
+                  const float z = __fmul_rn(alpha, xg);
+                  const float sig = 1.0f / (1.0f + expf(-z));
+                  out[(size_t)orow * out_ld + ((r0 + r) >> 1)] =
+                      __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+                }
+              }
+            }
+          } else {
+            const float yy[2] = {y0, y1};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              if (tt0 + h < nb) {
+                const int j = start + b0 + tt0 + h;
+                const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+                out[(size_t)orow * out_ld + r0 + r] = yy[h];
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int P, int kEpi>
+int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const uint8_t* q,
+              const uint8_t* qs, int Kp, const int* indptr, const int* sp, int k_top, int arow,
+              int orow, const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, int N,
+              int G, int tpwg, int gcap, float alpha, float limit, float* out, int out_ld) {
+  static const bool lds_ok = [] {  // allow more than 64 KB of dynamic LDS, once per kernel
+    const int bytes = kLdsBytes;
+    return hipFuncSetAttribute((const void*)moe_mx_gemv_kernel<P, kEpi, 23>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess &&
+           hipFuncSetAttribute((const void*)moe_mx_gemv_kernel<P, kEpi, kMxMaxChunks>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+  }();
+  if (!lds_ok) return kErrLaunch;
+  if (NC == 23)
+    hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, 23>), grid, block, lds, stream, q, qs, Kp,
+                       indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, tpwg, gcap, alpha,
+                       limit, out, out_ld);
+  else
+    hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, kMxMaxChunks>), grid, block, lds, stream, q,
+                       qs, Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, tpwg, gcap,
+                       alpha, limit, out, out_ld);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace moe
+
+extern "C" {
+
+// Packed pieces of `rows` rows of length K: q bytes then (256-aligned) qs bytes.
+size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces) {
+  const int64_t nc = (K + 127) / 128;
+  return (size_t)(((rows * pieces * nc * 128) + 255) / 256 * 256);
+}
+
+size_t moe_pieces_total_bytes(int64_t rows, int64_t K, int pieces) {
+  return moe_pieces_q_bytes(rows, K, pieces) +
+         (size_t)((rows * pieces * moe::kMxSclRow + 255) / 256 * 256);
+}
+
+int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, void* packed,
+                      hipStream_t stream) {
+  if (rows == 0) return moe::kOk;
+  const int NC = (K + 127) / 128;
+  uint8_t* q = (uint8_t*)packed;
+  uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
+  const int64_t threads = (int64_t)rows * 4 * NC;
+  const dim3 grid((uint32_t)((threads + 255) / 256));
+#define MOE_PIECES(P, F)                                                                       \
+  hipLaunchKernelGGL((moe::moe_pieces_kernel<P, F>), grid, dim3(256), 0, stream, x, rows, K, NC, \
+                     q, qs)
+  if (pieces == 2 && !x_is_f32) MOE_PIECES(2, false);
+  else if (pieces == 2) MOE_PIECES(2, true);
+  else if (pieces == 4 && !x_is_f32) MOE_PIECES(4, false);
+  else if (pieces == 4) MOE_PIECES(4, true);
+  else return moe::kErrUnsupported;
+#undef MOE_PIECES
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}
+
+// packed: pieces of the activation rows (moe_launch_pieces); max_tokens bounds
+// the tokens of one expert (sizes the LDS batch); rows_active bounds the pairs
+// (and so the experts that hold any).
+int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* indptr,
+                       const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
+                       const void* blocks, const void* scales, const void* bias, int E, int N,
+                       int K, int max_tokens, int rows_active, int swiglu, float alpha,
+                       float limit, void* out, int out_ld, hipStream_t stream) {
+  if (max_tokens <= 0) return moe::kOk;
+  const int NC = (K + 127) / 128, Kp = NC * 128, G = K / 32;
+  const uint8_t* q = (const uint8_t*)packed;
+  const uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
+  // Waves per workgroup and workgroups per CU targeted by the split of each
+  // expert's rows; MOE_MX_WAVES / MOE_MX_WG_PER_CU override (tuning runs).
+  static const int waves = [] {
+    const char* v = getenv("MOE_MX_WAVES");
+    const int w = v ? atoi(v) : 11;
+    return w < 1 ? 1 : w > 12 ? 12 : w;
+  }();
+  static const int wg_per_cu = [] {
+    const char* v = getenv("MOE_MX_WG_PER_CU");
+    const int t = v ? atoi(v) : 1;
+    return t < 1 ? 1 : t;
+  }();
+  const int tpg = 16 / pieces;
+  const int gbytes = moe::mx_group_bytes(NC == 23 ? 23 : moe::kMxMaxChunks);
+  const int stage = waves * 16 * G;
+  const int gfit = (moe::kLdsBytes - stage) / gbytes;
+  const int gcap = min(min(moe::kMxMaxGroups, gfit), (max_tokens + tpg - 1) / tpg);
+  if (gcap < 1) return moe::kErrUnsupported;
+  const size_t lds = (size_t)gcap * gbytes + stage;
+  const int ntiles = N / 16;
+  // Split each expert's tiles so that the experts that can be active fill the
+  // chip: at most min(E, rows) experts hold pairs.
+  const int active = max(1, min(E, rows_active));
+  const int target = moe::kNumCUs * wg_per_cu;
+  int split = min(ntiles, max(1, (target + active - 1) / active));
+  const int tiles_per_wg = (ntiles + split - 1) / split;
+  split = (ntiles + tiles_per_wg - 1) / tiles_per_wg;
+  const dim3 grid(split, E);
+  const dim3 block(64 * waves);
+  const int* ip = (const int*)indptr;
+  const int* sp = (const int*)sorted_pairs;
+  const uint8_t* b = (const uint8_t*)blocks;
+  const uint8_t* s = (const uint8_t*)scales;
+  const uint16_t* bi = (const uint16_t*)bias;
+  float* o = (float*)out;
+  if (pieces == 2 && swiglu)
+    return moe::launch_mx<2, 1>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                out_ld);
+  if (pieces == 2)
+    return moe::launch_mx<2, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                out_ld);
+  if (pieces == 4 && !swiglu)
+    return moe::launch_mx<4, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                out_ld);
+  return moe::kErrUnsupported;
+}
+
+}  // extern "C"

@@ -175,7 +175,7 @@ class MLPBlock(torch.nn.Module):
 
         ``events`` (optional) maps stage names to (start, end) torch.cuda.Event
         pairs recorded around that stage on the current stream; the stages are
-        "router", "permute", "mlp1", "mlp2", "combine".
+        "router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine".
         """
         b, seq_len, dim = x.shape
         n = b * seq_len
@@ -192,14 +192,20 @@ class MLPBlock(torch.nn.Module):
         rec("permute", 0)
         perm = _native.permute(idx, self.num_experts)
         rec("permute", 1)
+        rec("pieces_t", 0)
+        t_pk = _native.quantize_pieces(t, 2)
+        rec("pieces_t", 1)
         rec("mlp1", 0)
-        act = _native.mlp1_swiglu(t, perm["indptr"], perm["sorted_pairs"], k,
+        act = _native.mlp1_swiglu(t_pk, n, dim, perm["indptr"], perm["sorted_pairs"], k,
                                   self.mlp1_weight_blocks, self.mlp1_weight_scales, self.mlp1_bias,
                                   SWIGLU_ALPHA, self.swiglu_limit)
         rec("mlp1", 1)
+        rec("pieces_act", 0)
+        act_pk = _native.quantize_pieces(act, 4)
+        rec("pieces_act", 1)
         rec("mlp2", 0)
-        y = _native.mlp2(act, perm["indptr"], perm["sorted_pairs"], n, k, self.mlp2_weight_blocks,
-                         self.mlp2_weight_scales, self.mlp2_bias)
+        y = _native.mlp2(act_pk, perm["indptr"], perm["sorted_pairs"], n, k,
+                         self.mlp2_weight_blocks, self.mlp2_weight_scales, self.mlp2_bias)
         rec("mlp2", 1)
         rec("combine", 0)
         out = _native.gemv_gating(y.view(n, k, self.hidden_size), w, x2)

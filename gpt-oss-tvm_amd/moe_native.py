@@ -40,9 +40,11 @@ _SIGS = {
     "moe_einsum_workspace_bytes": ([_I64, _I64, _I64, _I64, _INT], _SZ),
     "moe_einsum_fused": ([_P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P],
                          _INT),
-    "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P, _P],
+    "moe_pieces_bytes": ([_I64, _I64, _INT], _SZ),
+    "moe_quantize_pieces": ([_P, _INT, _I64, _I64, _INT, _P, _P], _INT),
+    "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P],
                         _INT),
-    "moe_mlp2": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
+    "moe_mlp2": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
     "moe_gemv_gating": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _INT),
     "moe_swiglu": ([_P, _I64, _I64, _F, _F, _P, _P], _INT),
     "moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
@@ -168,36 +170,82 @@ def einsum_fused(x, expert_indices, blocks, scales, bias) -> torch.Tensor:
     return out
 
 
-def mlp1_swiglu(t, indptr, sorted_pairs, k, blocks, scales, bias, alpha, limit, act=None):
-    """mlp1 + SwiGLU over grouped pairs -> (act_hi, act_lo) bf16 [n*k, I], act = hi + lo."""
-    n, H = t.shape
+def pieces_bytes(rows: int, K: int, pieces: int) -> int:
+    return int(_lib.moe_pieces_bytes(rows, K, pieces))
+
+
+def quantize_pieces(x: torch.Tensor, pieces: int, packed: torch.Tensor | None = None) -> torch.Tensor:
+    """x [rows, K] bf16 or fp32 -> packed fp8 pieces (u8 buffer of pieces_bytes(rows, K, pieces)).
+
+    Layout: q [rows, pieces, ceil(K/128)*128] e4m3 codes, then (256-byte aligned)
+    qs [rows, pieces, 4, 28] E8M0 bytes with qs[.., g, c] the scale of block 4c + g.
+    """
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x: expected bfloat16 or float32, got {x.dtype}")
+    _expect(x, "x", x.dtype)
+    if x.dim() != 2:
+        raise ValueError(f"x: expected [rows, K], got shape {tuple(x.shape)}")
+    rows, K = x.shape
+    nbytes = pieces_bytes(rows, K, pieces)
+    if nbytes == 0 and rows > 0:
+        raise ValueError(f"quantize_pieces: unsupported K={K} or pieces={pieces}")
+    if packed is None:
+        packed = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    elif packed.numel() < nbytes:
+        raise ValueError(f"packed: need {nbytes} bytes, got {packed.numel()}")
+    _check(_lib.moe_quantize_pieces(_ptr(x), int(x.dtype == torch.float32), rows, K, pieces,
+                                    _ptr(packed), _stream()), "moe_quantize_pieces")
+    return packed
+
+
+def unpack_pieces(packed: torch.Tensor, rows: int, K: int, pieces: int):
+    """Views (q [rows, pieces, Kp] u8, qs [rows, pieces, 4, 28] u8) of a packed buffer."""
+    kp = (K + 127) // 128 * 128
+    qb = (rows * pieces * kp + 255) // 256 * 256
+    q = packed[: rows * pieces * kp].view(rows, pieces, kp)
+    qs = packed[qb: qb + rows * pieces * 112].view(rows, pieces, 4, 28)
+    return q, qs
+
+
+def mlp1_swiglu(t_pieces, n, H, indptr, sorted_pairs, k, blocks, scales, bias, alpha, limit,
+                act=None):
+    """mlp1 + SwiGLU over grouped pairs -> act fp32 [n*k, I] (row = sorted position).
+
+    t_pieces: quantize_pieces(t, 2) of the normalised tokens t [n, H].
+    """
     E, N2, G, _ = blocks.shape
     inter = N2 // 2
-    _expect(t, "t", torch.bfloat16)
+    _expect(t_pieces, "t_pieces", torch.uint8)
+    if t_pieces.numel() < pieces_bytes(n, H, 2):
+        raise ValueError("t_pieces: buffer smaller than pieces_bytes(n, H, 2)")
     _expect(blocks, "mlp1_weight_blocks", torch.uint8, (E, 2 * inter, H // 32, 16))
     _expect(scales, "mlp1_weight_scales", torch.uint8, (E, 2 * inter, H // 32))
     _expect(bias, "mlp1_bias", torch.bfloat16, (E, 2 * inter))
     if act is None:
-        act = torch.empty((2, n * k, inter), dtype=torch.bfloat16, device=t.device)
-    _check(_lib.moe_mlp1_swiglu(_ptr(t), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
-                                _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit, _ptr(act[0]),
-                                _ptr(act[1]), _stream()), "moe_mlp1_swiglu")
+        act = torch.empty((n * k, inter), dtype=torch.float32, device=blocks.device)
+    _check(_lib.moe_mlp1_swiglu(_ptr(t_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H,
+                                inter, _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit,
+                                _ptr(act), _stream()), "moe_mlp1_swiglu")
     return act
 
 
-def mlp2(act, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
-    """mlp2 over grouped pairs; act = (hi, lo) planes [2, n*k, I] -> y fp32 [n*k, H] by pair."""
+def mlp2(act_pieces, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
+    """mlp2 over grouped pairs -> y fp32 [n*k, H] by pair.
+
+    act_pieces: quantize_pieces(act, 4) of mlp1_swiglu's output (sorted rows).
+    """
     E, H, G, _ = blocks.shape
     inter = G * 32
-    _expect(act, "act", torch.bfloat16, (2, n * k, inter))
+    _expect(act_pieces, "act_pieces", torch.uint8)
+    if act_pieces.numel() < pieces_bytes(n * k, inter, 4):
+        raise ValueError("act_pieces: buffer smaller than pieces_bytes(n*k, I, 4)")
     _expect(blocks, "mlp2_weight_blocks", torch.uint8, (E, H, G, 16))
     _expect(scales, "mlp2_weight_scales", torch.uint8, (E, H, G))
     _expect(bias, "mlp2_bias", torch.bfloat16, (E, H))
     if y is None:
-        y = torch.empty((n * k, H), dtype=torch.float32, device=act.device)
-    _check(_lib.moe_mlp2(_ptr(act[0]), _ptr(act[1]), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H,
-                         inter, _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()),
-           "moe_mlp2")
+        y = torch.empty((n * k, H), dtype=torch.float32, device=blocks.device)
+    _check(_lib.moe_mlp2(_ptr(act_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
+                         _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()), "moe_mlp2")
     return y
 
 
@@ -232,7 +280,7 @@ def workspace_bytes(n, E, k, H, inter) -> int:
 
 
 def workspace_layout(n, E, k, H, inter) -> list[int]:
-    offs = (_SZ * 11)()
+    offs = (_SZ * 12)()
     _check(_lib.moe_workspace_layout(n, E, k, H, inter, offs), "moe_workspace_layout")
     return list(offs)
 

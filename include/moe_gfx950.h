@@ -111,8 +111,9 @@ MOE_API int moe_permute(const int32_t* idx, int64_t n, int64_t k, int64_t E, int
  * Replaces: moe_einsum_fused, model/mlp.py:267-326 (MLPBlock.run_einsum, mlp.py:238-326).
  * x is bf16 [n, K] when x_is_3d_f32 == 0 (the mlp1 call, mlp.py:387) or fp32
  * [n, k, K] when 1 (the mlp2 call, mlp.py:395).  workspace holds the grouping
- * (and, for fp32 x, its bf16 hi/lo split): at least
- * moe_einsum_workspace_bytes(n, k, E, K, x_is_3d_f32) bytes, 16-byte aligned.
+ * and the fp8 pieces of x (2 for bf16 x, 4 for fp32 x, see moe_quantize_pieces):
+ * at least moe_einsum_workspace_bytes(n, k, E, K, x_is_3d_f32) bytes, 16-byte
+ * aligned.  N % 16 == 0, K % 32 == 0, K <= 3072.
  */
 MOE_API size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K,
                                           int x_is_3d_f32);
@@ -123,31 +124,49 @@ MOE_API int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expe
                              moe_stream_t stream);
 
 /*
+ * Activation operand encoding of the expert matmuls ("pieces").  No reference
+ * counterpart: the reference multiplies bf16 activations by dequantised bf16
+ * weights (model/mlp_optimized.py:324-331); here the weights stay MXFP4 and
+ * the matmul is gfx950's block-scaled fp4 x fp8 MFMA, whose activation
+ * operand is fp8 e4m3 with one E8M0 scale per 32 elements.  Each row of x is
+ * written as the sum of `pieces` fp8 rows, each quantising (round to nearest
+ * even) what the earlier ones left, with the smallest scale that keeps the
+ * block's codes below 256.  pieces = 2 reproduces bf16 input to within
+ * 2^-14 of each 32-block's largest magnitude (exactly when a block spans at
+ * most 6 binades); pieces = 4 carries fp32 input to about 16 significant bits.
+ * x [rows, K] bf16 (x_is_f32 == 0) or fp32; packed: moe_pieces_bytes(rows, K,
+ * pieces) bytes, 16-byte aligned.  K % 32 == 0, K <= 3072, pieces 2 or 4.
+ */
+MOE_API size_t moe_pieces_bytes(int64_t rows, int64_t K, int pieces);
+MOE_API int moe_quantize_pieces(const void* x, int x_is_f32, int64_t rows, int64_t K, int pieces,
+                                void* packed, moe_stream_t stream);
+
+/*
  * mlp1 with the interleaved clamped SwiGLU epilogue, over grouped pairs.
  * Replaces: mxfp4_moe_mlp1_{prefill,decode}, model/mlp_optimized.py:214-571, with
  * the fp32 semantics of model/mlp.py:387-390 (run_einsum + swiglu(out_dtype=float32)).
- * t [n, H] bf16, indptr/sorted_pairs from moe_permute; weights [E, 2I, H/32, 16],
- * [E, 2I, H/32], bias [E, 2I] -> the fp32 SwiGLU output as two bf16 planes
- * act_hi, act_lo [n*k, I] (row = sorted position) with act = hi + lo to within
- * 2^-17 relative: hi = bf16(act), lo = bf16(act - hi).
+ * t_pieces: moe_quantize_pieces(t, 0, n, H, 2) of the normalised tokens t [n, H];
+ * indptr/sorted_pairs from moe_permute; weights [E, 2I, H/32, 16], [E, 2I, H/32],
+ * bias [E, 2I] -> act [n*k, I] fp32, row = sorted position.
  */
-MOE_API int moe_mlp1_swiglu(const uint16_t* t, const int32_t* indptr, const int32_t* sorted_pairs,
-                            int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
-                            const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias,
-                            float alpha, float limit, uint16_t* act_hi, uint16_t* act_lo,
+MOE_API int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr,
+                            const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E,
+                            int64_t H, int64_t I, const uint8_t* blocks, const uint8_t* scales,
+                            const uint16_t* bias, float alpha, float limit, float* act,
                             moe_stream_t stream);
 
 /*
  * mlp2 over grouped pairs.
  * Replaces: mxfp4_moe_mlp2_{prefill,decode}, model/mlp_optimized.py:353-460, 573-660,
  * with the fp32 semantics of model/mlp.py:395.
- * act_hi, act_lo [n*k, I] bf16 (as written by moe_mlp1_swiglu); weights [E, H, I/32, 16],
- * [E, H, I/32], bias [E, H] -> y [n*k, H] fp32, row = pair p = token*k + slot.
+ * act_pieces: moe_quantize_pieces(act, 1, n*k, I, 4) of moe_mlp1_swiglu's output;
+ * weights [E, H, I/32, 16], [E, H, I/32], bias [E, H] -> y [n*k, H] fp32,
+ * row = pair p = token*k + slot.
  */
-MOE_API int moe_mlp2(const uint16_t* act_hi, const uint16_t* act_lo, const int32_t* indptr,
-                     const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E, int64_t H,
-                     int64_t I, const uint8_t* blocks, const uint8_t* scales,
-                     const uint16_t* bias, float* y, moe_stream_t stream);
+MOE_API int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorted_pairs,
+                     int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
+                     const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias,
+                     float* y, moe_stream_t stream);
 
 /*
  * Gate-weighted sum of the k expert outputs, plus the residual when x != NULL.
@@ -176,10 +195,10 @@ MOE_API int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, flo
 MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I);
 
 /* Byte offsets of the intermediates inside the block workspace, in this order:
- * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos, act_hi,
- * act_lo, y. */
+ * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
+ * t_pieces, act, act_pieces, y. */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                                 size_t offsets[11]);
+                                 size_t offsets[12]);
 
 MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                       const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,

@@ -153,8 +153,10 @@ def test_einsum_fused(native, E, N, K, n, three_d):
         xd = bf16_dev(xb)
     ref = O.einsum_fused(x, idx, blocks, scales, bias)
     out = host(native.einsum_fused(xd, i32_dev(idx), u8_dev(blocks), u8_dev(scales), bf16_dev(bias)))
-    # bf16 input: exact products, fp32 sums; fp32 input: split-bf16 products (2^-17)
-    assert norm_rel(out, ref) <= (5e-5 if three_d else 1e-5), norm_rel(out, ref)
+    # x enters the MFMA as fp8 pieces: 2 for bf16 x (exact to 2^-14 of each
+    # 32-block's maximum), 4 for fp32 x (to 2^-16 of it); sums in fp32.  A
+    # dropped piece or a wrong block scale is off by 4e-3 or more.
+    assert norm_rel(out, ref) <= 5e-5, norm_rel(out, ref)
 
 
 def test_many_tokens_per_expert(native):
@@ -169,6 +171,34 @@ def test_many_tokens_per_expert(native):
     out = host_bf16(blk(bf16_dev(x).view(1, n, H)).view(n, H))
     m = O.compare_outputs(out, tr.out)
     assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
+
+
+# ---------------------------------------------------------------------------
+# fp8 pieces of the activations (the scaled-MFMA operand), bit-exact
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,K,pieces,f32", [(64, 2880, 2, False), (256, 2880, 4, True),
+                                               (5, 96, 2, False), (7, 160, 4, True),
+                                               (3, 3072, 4, False), (1, 32, 2, True)])
+def test_quantize_pieces_bit_exact(native, rows, K, pieces, f32):
+    import pieces_model as PM
+    rng = np.random.default_rng(rows * K + pieces)
+    x = (rng.standard_normal((rows, K)) * np.exp(2 * rng.standard_normal((rows, K)))).astype(np.float32)
+    x[0, :32] = 0.0                         # all-zero block
+    if K >= 96:
+        x[0, 32:64] = np.float32(3e-39)     # fp32 subnormals
+        x[-1, 64:96] *= np.float32(1e20)    # large block
+    if f32:
+        xd = f32_dev(x)
+    else:
+        xb = O.f32_to_bf16(x)
+        x = O.bf16_to_f32(xb)
+        xd = bf16_dev(xb)
+    packed = host(native.quantize_pieces(xd, pieces))
+    q, qs = PM.unpack(packed, rows, K, pieces)
+    rq, rqs = PM.quantize_pieces(x, pieces)
+    assert np.array_equal(qs, rqs), np.argwhere(qs != rqs)[:4]
+    assert np.array_equal(q, rq), np.argwhere(q != rq)[:4]
 
 
 # ---------------------------------------------------------------------------
@@ -190,7 +220,7 @@ def _check_block(blk, x, tr, staged=True):
         sp = host(st["perm"]["sorted_pairs"])
         k = tr.idx.shape[1]
         act_ref = tr.act.reshape(n * k, -1)[sp]
-        act = host(st["act"][0].float()) + host(st["act"][1].float())  # hi + lo planes
+        act = host(st["act"])
         assert norm_rel(act, act_ref) <= 2e-5
         y_ref = tr.y.reshape(n * k, -1)
         assert norm_rel(host(st["y"]), y_ref) <= 1e-4
