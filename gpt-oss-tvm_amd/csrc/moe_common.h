@@ -84,18 +84,16 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ uint32_t e4m3_encode(float y) {
   const uint32_t sign = __float_as_uint(y) >> 31;
   const float a = fabsf(y);
-  uint32_t code;
-  const int e = (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127;
-  if (e < -6) {
-    code = (uint32_t)__builtin_rintf(a * 512.0f);         // subnormal steps of 2^-9 (8 -> 0x08 = 2^-6)
-  } else {
-    const float mant = a * __uint_as_float((uint32_t)(127 - e + 3) << 23);  // a / 2^e * 8 in [8, 16)
-    uint32_t mq = (uint32_t)__builtin_rintf(mant);
-    int ee = e;
-    if (mq == 16u) { mq = 8u; ++ee; }
-    code = ((uint32_t)(ee + 7) << 3) | (mq - 8u);
-  }
-  return code | (sign << 7);
+  const int e = (int)(__float_as_uint(a) >> 23) - 127;  // a in [2^e, 2^(e+1)) when normal
+  // normal codes (e >= -6): 3 mantissa bits, a / 2^e * 8 rounded in [8, 16]
+  const int en = e < -6 ? -6 : e;
+  const float mant = a * __uint_as_float((uint32_t)(127 - en + 3) << 23);
+  const uint32_t mq = (uint32_t)__builtin_rintf(mant);
+  const uint32_t carry = mq >> 4;  // rounded up to 16: next binade, mantissa 0
+  const uint32_t code_n = ((uint32_t)(en + 7 + (int)carry) << 3) | ((mq - 8u) & 7u);
+  // subnormal codes (e < -6): steps of 2^-9 (8 steps reach 0x08 = 2^-6)
+  const uint32_t code_s = (uint32_t)__builtin_rintf(a * 512.0f);
+  return (e < -6 ? code_s : code_n) | (sign << 7);
 }
 
 __device__ __forceinline__ float e4m3_decode(uint32_t c) {

@@ -58,81 +58,89 @@ __device__ __forceinline__ void static_for(F&& f) {
 // ---------------------------------------------------------------------------
 // Pieces.  Packed layout for `rows` rows of length K, NC = ceil(K / 128):
 //   q  [rows][P][NC * 128]   e4m3 codes, zero beyond K
-//   qs [rows][P][4][28]      qs[.., g, c] = E8M0 of block 4c + g (0 past K)
-// One thread per (row, 32-element block).
+//   qs [rows][P][4][28]      qs[.., g, c] = E8M0 of block 4c + g (0 past NC)
+// Four adjacent threads share one (row, 32-element block), 8 elements each;
+// the block maximum is combined over the four with two lane exchanges.
 template <int P, bool kF32>
 __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict__ x, int rows,
                                                          int K, int NC, uint8_t* __restrict__ q,
                                                          uint8_t* __restrict__ qs) {
   const int nblk = 4 * NC;
   const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (id >= (int64_t)rows * nblk) return;
-  const int row = (int)(id / nblk), blk = (int)(id - (int64_t)row * nblk);
+  const int64_t nthreads = (int64_t)rows * nblk * 4;
+  // Whole quads lie past the end (nthreads and 256 are multiples of 4); they
+  // compute on block 0 so every lane takes part in the exchanges, and store
+  // nothing.
+  const bool valid = id < nthreads;
+  const int64_t idc = valid ? id : (id & 3);
+  const int quarter = (int)(idc & 3);
+  const int64_t rb = idc >> 2;
+  const int row = (int)(rb / nblk), blk = (int)(rb - (int64_t)row * nblk);
   const int c = blk >> 2, g = blk & 3;
   const int Kp = NC * 128;
-  float r[32];
+  const int k0 = blk * 32 + quarter * 8;
+  float r[8];
   if (blk * 32 < K) {
     if constexpr (kF32) {
-      const f32x4* src = (const f32x4*)((const float*)x + (size_t)row * K + blk * 32);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const f32x4 v = src[i];
-        r[4 * i] = v[0]; r[4 * i + 1] = v[1]; r[4 * i + 2] = v[2]; r[4 * i + 3] = v[3];
-      }
+      const f32x4* src = (const f32x4*)((const float*)x + (size_t)row * K + k0);
+      const f32x4 v0 = src[0], v1 = src[1];
+      r[0] = v0[0]; r[1] = v0[1]; r[2] = v0[2]; r[3] = v0[3];
+      r[4] = v1[0]; r[5] = v1[1]; r[6] = v1[2]; r[7] = v1[3];
     } else {
-      const u32x4* src = (const u32x4*)((const uint16_t*)x + (size_t)row * K + blk * 32);
+      const u32x4 v = *(const u32x4*)((const uint16_t*)x + (size_t)row * K + k0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4 v = src[i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          r[8 * i + 2 * j] = __uint_as_float(v[j] << 16);
-          r[8 * i + 2 * j + 1] = __uint_as_float(v[j] & 0xFFFF0000u);
-        }
+      for (int j = 0; j < 4; ++j) {
+        r[2 * j] = __uint_as_float(v[j] << 16);
+        r[2 * j + 1] = __uint_as_float(v[j] & 0xFFFF0000u);
       }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) r[i] = 0.0f;
+    for (int i = 0; i < 8; ++i) r[i] = 0.0f;
   }
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(r[i]));
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(r[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
     const uint32_t s = e8m0_for_amax(amax);
-    const float inv = __uint_as_float((254u - s) << 23);                       // 2^(127 - s)
+    const float inv = __uint_as_float((254u - s) << 23);                           // 2^(127 - s)
     const float sc = s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u);  // 2^(s - 127)
-    uint32_t pk[8];
+    uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pk[i] = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const uint32_t code = e4m3_encode(r[i] * inv);
-      r[i] -= e4m3_decode(code) * sc;   // exact: the code's value is a rounding of r[i]
-      pk[i >> 2] |= code << (8 * (i & 3));
+      r[i] -= e4m3_decode(code) * sc;  // exact: the code's value is a rounding of r[i]
+      if (i < 4) lo |= code << (8 * i); else hi |= code << (8 * (i - 4));
     }
     const size_t prow = (size_t)row * P + p;
-    u32x4* dst = (u32x4*)(q + prow * Kp + blk * 32);
-    dst[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-    dst[1] = u32x4{pk[4], pk[5], pk[6], pk[7]};
-    uint8_t* run = qs + prow * kMxSclRow + g * kMxSclRun;
-    run[c] = (uint8_t)s;
-    if (c == NC - 1)
-      for (int z = NC; z < kMxSclRun; ++z) run[z] = 0;
+    if (!valid) continue;
+    *(uint2*)(q + prow * Kp + k0) = make_uint2(lo, hi);
+    if (quarter == 0) {
+      uint8_t* run = qs + prow * kMxSclRow + g * kMxSclRun;
+      run[c] = (uint8_t)s;
+      if (c == NC - 1)
+        for (int z = NC; z < kMxSclRun; ++z) run[z] = 0;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Grouped expert GEMV.  Grid (S, E): workgroup (s, e) serves expert e and the
-// 16-row weight tiles [s * tiles_per_wg, (s + 1) * tiles_per_wg), dealt
-// round-robin to its waves.  Per batch of at most `groups_cap` * 16/P of the
-// expert's tokens it stages their pieces in LDS; each wave then takes its
-// tiles one at a time: the NCT scale bytes and NCT weight loads of the tile's
-// 16 rows x K (MFMA-native: lane (r, g) reads block 4c + g of row r, 16 B, for
-// chunk c) are issued together, scales first, so MFMA c waits only for the
-// loads up to chunk c; every token group then runs NCT MFMAs over them.  The
-// first tile's loads are issued before the LDS staging, so they overlap it.
+// Grouped expert GEMV.  Work is counted in units: one unit = one 16-row
+// weight tile of one expert for one batch of that expert's tokens (a batch is
+// at most `groups_cap` * 16/P tokens, the pieces that fit in LDS).  Every
+// workgroup scans the per-expert unit counts from indptr and takes an equal
+// contiguous share of all units, so experts with many tokens (several
+// batches) are spread over the chip like the rest.  A share splits into
+// segments of one (expert, batch); for each segment the workgroup stages that
+// batch's pieces in LDS and its waves take the segment's tiles round-robin:
+// the tile's scale bytes and NCT weight loads (MFMA-native: lane (r, g) reads
+// block 4c + g of row r, 16 B, for chunk c) are issued together, scales
+// first, so MFMA c waits only for the loads up to chunk c; every token group
+// of the batch then runs NCT MFMAs over them.  Each wave's first tile is
+// issued before the first staging, so its loads overlap it.
 //
 // arow_mode: piece row of sorted position j: 0 = sorted_pairs[j] / k_top
 // (token), 1 = sorted_pairs[j] (pair), 2 = j.  orow_mode: output row: 0 =
@@ -143,28 +151,54 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
     int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
-    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G,
-    int tiles_per_wg, int groups_cap, float alpha, float limit, float* __restrict__ out,
-    int out_ld) {
+    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
+    int groups_cap, float alpha, float limit, float* __restrict__ out, int out_ld) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
-  const int e = blockIdx.y;
-  const int start = indptr[e];
-  const int cnt = indptr[e + 1] - start;
-  if (cnt <= 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nwaves = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int t_begin = blockIdx.x * tiles_per_wg;
-  const int t_end = min(t_begin + tiles_per_wg, N >> 4);
+  const int ntiles = N >> 4;
   const int tpb = groups_cap * TPG;
+  // LDS: [groups_cap A operand groups][per-wave scale staging][E+1 unit prefix]
+  uint8_t* const sstage = lds + groups_cap * kMxGroupBytes + wave * (16 * G);
+  int* const pre = (int*)(lds + groups_cap * kMxGroupBytes + nwaves * (16 * G));
+
+  // Exclusive prefix of the unit counts: ceil(cnt_e / tpb) * ntiles.
+  if (wave == 0) {
+    int carry = 0;
+    if (lane == 0) pre[0] = 0;
+    for (int b = 0; b < E; b += 64) {
+      const int i = b + lane;
+      int v = 0;
+      if (i < E) v = (indptr[i + 1] - indptr[i] + tpb - 1) / tpb * ntiles;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, kWave);
+        if (lane >= o) v += t;
+      }
+      if (i < E) pre[i + 1] = carry + v;
+      carry += __shfl(v, 63, kWave);
+    }
+  }
+  __syncthreads();
+  const int64_t total = pre[E];
+  const int ubeg = (int)(total * blockIdx.x / gridDim.x);
+  const int uend = (int)(total * (blockIdx.x + 1) / gridDim.x);
+  if (ubeg >= uend) return;
+  auto expert_of = [&](int u) {  // largest e with pre[e] <= u
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= u) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
 
   u32x4 w[NCT];
   float bn = 0.0f;
-  // This wave's staging area for the scale bytes of its current tile.
-  uint8_t* const sstage = lds + groups_cap * kMxGroupBytes + wave * (16 * G);
   // Block index of chunk c for this lane: 4c + g.  Past K the lane re-reads
   // block G-1 (finite data; its A operand bytes are zero).  With NCT == 23
   // (89 <= G <= 92) only the last chunk can pass K, so the others address
@@ -174,7 +208,7 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
   // 16-byte loads per lane fetch them (G <= 96 units), issued before the
   // weights so they land first; they pass through LDS to reach the lane that
   // needs each byte.
-  auto issue = [&](int tile) {
+  auto issue = [&](int e, int tile) {
     int gl = g;
     asm volatile("" : "+v"(gl));
     const size_t row0 = (size_t)e * N + (tile << 4);
@@ -197,7 +231,14 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     const int blk = (NCT == 23 && c < 22) ? 4 * c + g : min(4 * c + g, G - 1);
     return sstage[r * G + blk];
   };
-  if (t_begin + wave < t_end) issue(t_begin + wave);
+
+  {  // this wave's first tile, in flight during the first staging
+    const int e = expert_of(ubeg);
+    const int off = ubeg - pre[e];
+    const int t0 = off % ntiles;
+    const int len = min(uend - ubeg, ntiles - t0);
+    if (wave < len) issue(e, t0 + wave);
+  }
 
   if (NCT * 128 > Kp) {  // zero the K tail of every staged row once
     const int tail16 = (NCT * 128 - Kp) >> 4;
@@ -208,23 +249,30 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     }
   }
 
-  for (int b0 = 0; b0 < cnt; b0 += tpb) {
-    const int nb = min(tpb, cnt - b0);
-    if (b0) __syncthreads();  // the previous batch's operands are no longer read
+  for (int u = ubeg; u < uend;) {
+    const int e = expert_of(u);
+    const int off = u - pre[e];
+    const int b0 = off / ntiles * tpb;
+    const int t0 = off % ntiles;
+    const int len = min(uend - u, ntiles - t0);
+    const int start = indptr[e];
+    const int nb = min(tpb, indptr[e + 1] - start - b0);
+    const bool first = u == ubeg;
+    if (!first) __syncthreads();  // the previous segment's operands are no longer read
     {
       // Stage the batch: 16-byte units, kFill loads in flight per thread.
       // Units past the end repeat the last one (same data to the same place).
       constexpr int kFill = NCT == 23 ? 8 : 4;
       const int row16 = Kp >> 4;
       const int units = row16 + kMxSclRow / 16;
-      const int total = nb * P * units;
-      for (int u0 = threadIdx.x; u0 < total; u0 += kFill * blockDim.x) {
+      const int total_units = nb * P * units;
+      for (int u0 = threadIdx.x; u0 < total_units; u0 += kFill * blockDim.x) {
         u32x4 v[kFill];
         uint32_t dst[kFill];
 #pragma unroll
         for (int i = 0; i < kFill; ++i) {
-          const int u = min(u0 + i * (int)blockDim.x, total - 1);
-          const int rp = u / units, c = u - rp * units;
+          const int uu = min(u0 + i * (int)blockDim.x, total_units - 1);
+          const int rp = uu / units, c = uu - rp * units;
           const int tt = rp / P, p = rp - tt * P;
           const int j = start + b0 + tt;
           const int row = arow_mode == 0 ? sorted_pairs[j] / k_top
@@ -247,9 +295,10 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     const int ngroups = (nb + TPG - 1) / TPG;
 
     for (int it = 0;; ++it) {
-      const int tile = t_begin + wave + nwaves * it;
-      if (tile >= t_end) break;
-      if (it > 0 || b0 > 0) issue(tile);
+      const int tl = wave + nwaves * it;
+      if (tl >= len) break;
+      const int tile = t0 + tl;
+      if (!first || it > 0) issue(e, tile);
       const int r0 = tile << 4;
 
       for (int gi = 0; gi < ngroups; ++gi) {
@@ -339,6 +388,7 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
         }
       }
     }
+    u += len;
   }
 }
 
@@ -346,7 +396,7 @@ template <int P, int kEpi>
 int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const uint8_t* q,
               const uint8_t* qs, int Kp, const int* indptr, const int* sp, int k_top, int arow,
               int orow, const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, int N,
-              int G, int tpwg, int gcap, float alpha, float limit, float* out, int out_ld) {
+              int G, int E, int gcap, float alpha, float limit, float* out, int out_ld) {
   static const bool lds_ok = [] {  // allow more than 64 KB of dynamic LDS, once per kernel
     const int bytes = kLdsBytes;
     return hipFuncSetAttribute((const void*)moe_mx_gemv_kernel<P, kEpi, 23>,
@@ -357,11 +407,11 @@ int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, con
   if (!lds_ok) return kErrLaunch;
   if (NC == 23)
     hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, 23>), grid, block, lds, stream, q, qs, Kp,
-                       indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, tpwg, gcap, alpha,
+                       indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, gcap, alpha,
                        limit, out, out_ld);
   else
     hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, kMxMaxChunks>), grid, block, lds, stream, q,
-                       qs, Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, tpwg, gcap,
+                       qs, Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, gcap,
                        alpha, limit, out, out_ld);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
@@ -387,7 +437,7 @@ int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, 
   const int NC = (K + 127) / 128;
   uint8_t* q = (uint8_t*)packed;
   uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
-  const int64_t threads = (int64_t)rows * 4 * NC;
+  const int64_t threads = (int64_t)rows * 4 * NC * 4;
   const dim3 grid((uint32_t)((threads + 255) / 256));
 #define MOE_PIECES(P, F)                                                                       \
   hipLaunchKernelGGL((moe::moe_pieces_kernel<P, F>), grid, dim3(256), 0, stream, x, rows, K, NC, \
@@ -413,8 +463,8 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   const int NC = (K + 127) / 128, Kp = NC * 128, G = K / 32;
   const uint8_t* q = (const uint8_t*)packed;
   const uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
-  // Waves per workgroup and workgroups per CU targeted by the split of each
-  // expert's rows; MOE_MX_WAVES / MOE_MX_WG_PER_CU override (tuning runs).
+  // Waves per workgroup and workgroups per CU of the persistent grid;
+  // MOE_MX_WAVES / MOE_MX_WG_PER_CU override (tuning runs).
   static const int waves = [] {
     const char* v = getenv("MOE_MX_WAVES");
     const int w = v ? atoi(v) : 11;
@@ -427,20 +477,21 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   }();
   const int tpg = 16 / pieces;
   const int gbytes = moe::mx_group_bytes(NC == 23 ? 23 : moe::kMxMaxChunks);
-  const int stage = waves * 16 * G;
-  const int gfit = (moe::kLdsBytes - stage) / gbytes;
+  const int fixed = waves * 16 * G + (E + 1) * 4;  // scale staging + unit prefix
+  const int gfit = (moe::kLdsBytes - fixed) / gbytes;
   const int gcap = min(min(moe::kMxMaxGroups, gfit), (max_tokens + tpg - 1) / tpg);
   if (gcap < 1) return moe::kErrUnsupported;
-  const size_t lds = (size_t)gcap * gbytes + stage;
+  const size_t lds = (size_t)gcap * gbytes + fixed;
+  // Upper bound of the work units (16-row tiles x token batches) over the
+  // experts that can hold pairs; the grid never exceeds it.
   const int ntiles = N / 16;
-  // Split each expert's tiles so that the experts that can be active fill the
-  // chip: at most min(E, rows) experts hold pairs.
-  const int active = max(1, min(E, rows_active));
-  const int target = moe::kNumCUs * wg_per_cu;
-  int split = min(ntiles, max(1, (target + active - 1) / active));
-  const int tiles_per_wg = (ntiles + split - 1) / split;
-  split = (ntiles + tiles_per_wg - 1) / tiles_per_wg;
-  const dim3 grid(split, E);
+  const int64_t tpb = (int64_t)gcap * tpg;
+  const int64_t units_max =
+      (int64_t)ntiles * ((int64_t)max(1, min(E, rows_active)) + (int64_t)rows_active / tpb);
+  if (units_max >= ((int64_t)1 << 31)) return moe::kErrUnsupported;  // int unit indices
+  const int64_t target = (int64_t)moe::kNumCUs * wg_per_cu;
+  const int nwg = (int)(units_max < target ? (units_max < 1 ? 1 : units_max) : target);
+  const dim3 grid(nwg);
   const dim3 block(64 * waves);
   const int* ip = (const int*)indptr;
   const int* sp = (const int*)sorted_pairs;
@@ -450,15 +501,15 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   float* o = (float*)out;
   if (pieces == 2 && swiglu)
     return moe::launch_mx<2, 1>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
-                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld);
   if (pieces == 2)
     return moe::launch_mx<2, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
-                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld);
   if (pieces == 4 && !swiglu)
     return moe::launch_mx<4, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
-                                orow_mode, b, s, bi, N, G, tiles_per_wg, gcap, alpha, limit, o,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld);
   return moe::kErrUnsupported;
 }
