@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict_
 // sorted_pairs[j], 1 = j.  kEpi: 0 = store y (N columns), 1 = interleaved
 // SwiGLU (N/2 columns).
 template <int P, int kEpi, int NCT>
-__global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
+__global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
     int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
@@ -157,7 +157,9 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // wave index in a scalar register: branches on it are uniform
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int ntiles = N >> 4;
@@ -197,48 +199,71 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     return lo;
   };
 
-  u32x4 w[NCT];
-  float bn = 0.0f;
+  // Two-stage pipeline per wave: a tile's weights come in two halves of
+  // H0 and H1 chunks held in wa / wb.  While one half's MFMAs run, the other
+  // half's loads (or the next tile's first half) are in flight.
+  constexpr int H0 = (NCT + 1) / 2, H1 = NCT - H0;
+  u32x4 wa[H0], wb[H1];
+  u32x4 sc0, sc1;          // the tile's scale bytes, staged in LDS at compute time
+  float bn = 0.0f, bn_next = 0.0f;
   // Block index of chunk c for this lane: 4c + g.  Past K the lane re-reads
   // block G-1 (finite data; its A operand bytes are zero).  With NCT == 23
   // (89 <= G <= 92) only the last chunk can pass K, so the others address
   // from one base with immediate offsets.  The opaque copy of g keeps the
   // compiler from hoisting 2*NCT per-chunk offsets out of the tile loop.
-  // The tile's 16 x G scale bytes are contiguous and 16-byte aligned: two
-  // 16-byte loads per lane fetch them (G <= 96 units), issued before the
-  // weights so they land first; they pass through LDS to reach the lane that
-  // needs each byte.
-  auto issue = [&](int e, int tile) {
+  auto blk_of = [&](int c, int gl) {
+    return (NCT == 23 && c < 22) ? 4 * c + gl : min(4 * c + gl, G - 1);
+  };
+  // First half: the tile's 16 x G scale bytes (contiguous, 16-byte aligned,
+  // G <= 96 units: two 16-byte loads per lane), its bias and chunks 0..H0-1.
+  auto issue_h0 = [&](int e, int tile) {
     int gl = g;
     asm volatile("" : "+v"(gl));
     const size_t row0 = (size_t)e * N + (tile << 4);
-    const size_t wrow = row0 + r;
-    const uint8_t* wp = blocks + wrow * G * 16;
     const uint8_t* st = scales + row0 * G;
-    const u32x4 s0 = *(const u32x4*)(st + min(lane, G - 1) * 16);
-    const u32x4 s1 = *(const u32x4*)(st + min(lane + 64, G - 1) * 16);
-    bn = bf2f(bias[wrow]);
-    static_for<0, NCT>([&](auto cv) {
+    sc0 = *(const u32x4*)(st + min(lane, G - 1) * 16);
+    sc1 = *(const u32x4*)(st + min(lane + 64, G - 1) * 16);
+    bn_next = bf2f(bias[row0 + r]);
+    const uint8_t* wp = blocks + (row0 + r) * G * 16;
+    static_for<0, H0>([&](auto cv) {
       constexpr int c = decltype(cv)::value;
-      const int blk = (NCT == 23 && c < 22) ? 4 * c + gl : min(4 * c + gl, G - 1);
-      w[c] = *(const u32x4*)(wp + blk * 16);
+      wa[c] = *(const u32x4*)(wp + blk_of(c, gl) * 16);
     });
-    if (lane < G) *(u32x4*)(sstage + lane * 16) = s0;
-    if (lane + 64 < G) *(u32x4*)(sstage + (lane + 64) * 16) = s1;
   };
-  // Scale byte of chunk c for this lane, read from the staging area.
-  auto scale_b = [&](int c) -> uint32_t {
-    const int blk = (NCT == 23 && c < 22) ? 4 * c + g : min(4 * c + g, G - 1);
-    return sstage[r * G + blk];
+  auto issue_h1 = [&](int e, int tile) {
+    int gl = g;
+    asm volatile("" : "+v"(gl));
+    const uint8_t* wp = blocks + ((size_t)e * N + (tile << 4) + r) * G * 16;
+    static_for<0, H1>([&](auto cv) {
+      constexpr int c = decltype(cv)::value;
+      wb[c] = *(const u32x4*)(wp + blk_of(H0 + c, gl) * 16);
+    });
+  };
+  // The scale bytes pass through LDS to reach the lane that needs each one.
+  auto stage_scales = [&]() {
+    if (lane < G) *(u32x4*)(sstage + lane * 16) = sc0;
+    if (lane + 64 < G) *(u32x4*)(sstage + (lane + 64) * 16) = sc1;
+  };
+  const uint32_t sstage_off = groups_cap * kMxGroupBytes + wave * (16 * G) + r * G;
+  auto scale_b = [&](uint32_t ss, int c) -> uint32_t { return lds[ss + blk_of(c, g)]; };
+
+  struct Seg {
+    int e, b0, t0, len;
+  };
+  auto seg_at = [&](int u) {
+    Seg sgm;
+    sgm.e = expert_of(u);
+    const int off = u - pre[sgm.e];
+    sgm.b0 = off / ntiles * tpb;
+    sgm.t0 = off % ntiles;
+    sgm.len = min(uend - u, ntiles - sgm.t0);
+    return sgm;
   };
 
-  {  // this wave's first tile, in flight during the first staging
-    const int e = expert_of(ubeg);
-    const int off = ubeg - pre[e];
-    const int t0 = off % ntiles;
-    const int len = min(uend - ubeg, ntiles - t0);
-    if (wave < len) issue(e, t0 + wave);
-  }
+  Seg sg = seg_at(ubeg);
+  // in flight during the first staging (a wave without a tile in the first
+  // segment loads the segment's first tile; it is replaced before use)
+  issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
 
   if (NCT * 128 > Kp) {  // zero the K tail of every staged row once
     const int tail16 = (NCT * 128 - Kp) >> 4;
@@ -250,15 +275,10 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
   }
 
   for (int u = ubeg; u < uend;) {
-    const int e = expert_of(u);
-    const int off = u - pre[e];
-    const int b0 = off / ntiles * tpb;
-    const int t0 = off % ntiles;
-    const int len = min(uend - u, ntiles - t0);
+    const int e = sg.e, b0 = sg.b0, t0 = sg.t0, len = sg.len;
     const int start = indptr[e];
     const int nb = min(tpb, indptr[e + 1] - start - b0);
-    const bool first = u == ubeg;
-    if (!first) __syncthreads();  // the previous segment's operands are no longer read
+    if (u != ubeg) __syncthreads();  // the previous segment's operands are no longer read
     {
       // Stage the batch: 16-byte units, kFill loads in flight per thread.
       // Units past the end repeat the last one (same data to the same place).
@@ -293,102 +313,147 @@ __global__ __launch_bounds__(768) void moe_mx_gemv_kernel(
     }
     __syncthreads();
     const int ngroups = (nb + TPG - 1) / TPG;
+    const int u_next = u + len;
+    Seg nx = {-1, 0, 0, 0};
+    if (u_next < uend) nx = seg_at(u_next);
+
+    // MFMAs of chunks [C0, C0 + NH) of one operand group, from register half w.
+    auto run_half = [&](auto c0v, auto nhv, const u32x4* w, int gi, f32x4& acc) {
+      constexpr int C0 = decltype(c0v)::value, NH = decltype(nhv)::value;
+      const uint32_t ar = gi * kMxGroupBytes + r * kMxRowStride + 16 * g;
+      const uint8_t* as = lds + gi * kMxGroupBytes + 16 * kMxRowStride + r * kMxSclRow +
+                          g * kMxSclRun;
+      // A operands stream from LDS one chunk ahead of the MFMA chain.  Each
+      // chunk's offset passes through an opaque asm, so its reads cannot be
+      // hoisted ahead of the chain (which would hold all chunks in registers);
+      // the scheduling barrier after each MFMA keeps at most two chunks live.
+      auto load_a = [&](int c) {
+        uint32_t o = ar + 128 * c;
+        asm volatile("" : "+v"(o));
+        const u32x4 a0 = *(const u32x4*)(lds + o);
+        const u32x4 a1 = *(const u32x4*)(lds + o + 64);
+        return i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                     (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+      };
+      // An opaque copy of this lane's staged scale row offset keeps the
+      // compiler from hoisting the per-chunk reads out of the group loop.
+      uint32_t ss = sstage_off;
+      asm volatile("" : "+v"(ss));
+      uint32_t sa = *(const uint32_t*)(as + (C0 & ~3));
+      uint32_t sb = scale_b(ss, C0);
+      i32x8 acur = load_a(C0);
+      static_for<0, NH>([&](auto jv) {
+        constexpr int j = decltype(jv)::value;
+        constexpr int c = C0 + j;
+        i32x8 anext;
+        uint32_t sa_next = 0, sb_next = 0;
+        if constexpr (j + 1 < NH) {
+          anext = load_a(c + 1);
+          sb_next = scale_b(ss, c + 1);
+          if constexpr ((c & 3) == 3) sa_next = *(const uint32_t*)(as + c + 1);
+        }
+        const i32x8 B = {(int)w[j][0], (int)w[j][1], (int)w[j][2], (int)w[j][3], 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(acur, B, acc, 0, 4, c & 3, (int)sa,
+                                                               0, (int)sb);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (j + 1 < NH) {
+          acur = anext;
+          sb = sb_next;
+          if constexpr ((c & 3) == 3) sa = sa_next;
+        }
+      });
+    };
 
     for (int it = 0;; ++it) {
       const int tl = wave + nwaves * it;
       if (tl >= len) break;
       const int tile = t0 + tl;
-      if (!first || it > 0) issue(e, tile);
       const int r0 = tile << 4;
-
-      for (int gi = 0; gi < ngroups; ++gi) {
-        const uint8_t* ar = lds + gi * kMxGroupBytes + r * kMxRowStride + 16 * g;
-        const uint8_t* as = lds + gi * kMxGroupBytes + 16 * kMxRowStride + r * kMxSclRow +
-                            g * kMxSclRun;
-        // A operands stream from LDS one chunk ahead of the MFMA chain; the
-        // scheduling barrier after each MFMA keeps at most two chunks live.
-        auto load_a = [&](int c) {
-          const u32x4 a0 = *(const u32x4*)(ar + 128 * c);
-          const u32x4 a1 = *(const u32x4*)(ar + 128 * c + 64);
-          return i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
-                       (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-        };
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        uint32_t sa = *(const uint32_t*)as;
-        uint32_t sb = scale_b(0);
-        i32x8 acur = load_a(0);
-        static_for<0, NCT>([&](auto cv) {
-          constexpr int c = decltype(cv)::value;
-          i32x8 anext;
-          uint32_t sa_next = 0, sb_next = 0;
-          if constexpr (c + 1 < NCT) {
-            anext = load_a(c + 1);
-            sb_next = scale_b(c + 1);
+      issue_h1(e, tile);
+      stage_scales();
+      bn = bn_next;
+      // One operand group: both halves and the epilogue.  The last group
+      // issues the next tile's first half between its halves; it is peeled
+      // out of the loop so the current first half is dead by then.
+      auto do_group = [&](int gi, auto lastv) {
+        constexpr bool last = decltype(lastv)::value;
+          f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+          run_half(std::integral_constant<int, 0>{}, std::integral_constant<int, H0>{}, wa, gi, acc);
+          // keeps the first-half MFMAs ahead of the (uniform) prefetch branch
+          asm volatile("" : "+v"(acc));
+          if constexpr (last) {
+            // next first half: this segment's next tile, else this wave's first
+            // tile of the next segment, else (nothing left) this tile again.
+            // Issued unconditionally: a branch here would make the waits of
+            // the second half below count the new loads too.
+            int ne = e, nt = tile;
+            if (tl + nwaves < len) {
+              nt = tile + nwaves;
+            } else if (nx.e >= 0 && wave < nx.len) {
+              ne = nx.e;
+              nt = nx.t0 + wave;
+            }
+            issue_h0(ne, nt);
           }
-          if constexpr ((c & 3) == 3 && c + 1 < NCT) sa_next = *(const uint32_t*)(as + c + 1);
-          const i32x8 B = {(int)w[c][0], (int)w[c][1], (int)w[c][2], (int)w[c][3], 0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(acur, B, acc, 0, 4, c & 3, (int)sa,
-                                                                 0, (int)sb);
-          __builtin_amdgcn_sched_barrier(0);
-          if constexpr (c + 1 < NCT) {
-            acur = anext;
-            sb = sb_next;
-          }
-          if constexpr ((c & 3) == 3 && c + 1 < NCT) sa = sa_next;
-        });
-        // The MFMAs combine operands of all 64 lanes, so they must run with the
-        // full wave active.  Their results are only stored under per-lane
-        // conditions below; without this barrier the compiler may sink the
-        // whole chain into that divergent branch.
-        asm volatile("" : "+v"(acc));
-        // lane (r, g): weight row r0 + r; operand rows 4g + i hold token
-        // (4g + i) / P, piece (4g + i) % P of this group
-        if constexpr (P == 4) {
-          const int tt = gi * TPG + g;
-          const float y = (((acc[3] + acc[2]) + acc[1]) + acc[0]) + bn;
-          if (tt < nb) {
-            const int j = start + b0 + tt;
-            const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
-            out[(size_t)orow * out_ld + r0 + r] = y;
-          }
-        } else {
-          const float y0 = (acc[1] + acc[0]) + bn;
-          const float y1 = (acc[3] + acc[2]) + bn;
-          const int tt0 = gi * TPG + 2 * g;
-          if constexpr (kEpi == 1) {
-            const float l0 = __shfl_xor(y0, 1, kWave);  // odd rows hold the linear half
-            const float l1 = __shfl_xor(y1, 1, kWave);
-            if ((r & 1) == 0) {
-              const float yy[2] = {y0, y1}, ll[2] = {l0, l1};
-#pragma unroll
+          run_half(std::integral_constant<int, H0>{}, std::integral_constant<int, H1>{}, wb, gi, acc);
+          // The MFMAs combine operands of all 64 lanes, so they must run with the
+          // full wave active.  Their results are only stored under per-lane
+          // conditions below; without this barrier the compiler may sink the
+          // chains into those divergent branches.
+          asm volatile("" : "+v"(acc));
+          // lane (r, g): weight row r0 + r; operand rows 4g + i hold token
+          // (4g + i) / P, piece (4g + i) % P of this group
+          if constexpr (P == 4) {
+            const int tt = gi * TPG + g;
+            const float y = (((acc[3] + acc[2]) + acc[1]) + acc[0]) + bn;
+            if (tt < nb) {
+              const int j = start + b0 + tt;
+              const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+              out[(size_t)orow * out_ld + r0 + r] = y;
+            }
+          } else {
+            const float y0 = (acc[1] + acc[0]) + bn;
+            const float y1 = (acc[3] + acc[2]) + bn;
+            const int tt0 = gi * TPG + 2 * g;
+            if constexpr (kEpi == 1) {
+              const float l0 = __shfl_xor(y0, 1, kWave);  // odd rows hold the linear half
+              const float l1 = __shfl_xor(y1, 1, kWave);
+              if ((r & 1) == 0) {
+                const float yy[2] = {y0, y1}, ll[2] = {l0, l1};
+  #pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  if (tt0 + h < nb) {
+                    const int j = start + b0 + tt0 + h;
+                    const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+                    const float xg = fminf(yy[h], limit);
+                    const float xl = fminf(fmaxf(ll[h], -limit), limit);
+                    const float z = __fmul_rn(alpha, xg);
+                    const float sig = 1.0f / (1.0f + expf(-z));
+                    out[(size_t)orow * out_ld + ((r0 + r) >> 1)] =
+                        __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+                  }
+                }
+              }
+            } else {
+              const float yy[2] = {y0, y1};
+  #pragma unroll
               for (int h = 0; h < 2; ++h) {
                 if (tt0 + h < nb) {
                   const int j = start + b0 + tt0 + h;
                   const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
-                  const float xg = fminf(yy[h], limit);
-                  const float xl = fminf(fmaxf(ll[h], -limit), limit);
-                  const float z = __fmul_rn(alpha, xg);
-                  const float sig = 1.0f / (1.0f + expf(-z));
-                  out[(size_t)orow * out_ld + ((r0 + r) >> 1)] =
-                      __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+                  out[(size_t)orow * out_ld + r0 + r] = yy[h];
                 }
               }
             }
-          } else {
-            const float yy[2] = {y0, y1};
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              if (tt0 + h < nb) {
-                const int j = start + b0 + tt0 + h;
-                const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
-                out[(size_t)orow * out_ld + r0 + r] = yy[h];
-              }
-            }
           }
-        }
-      }
+      };
+      for (int gi = 0; gi < ngroups - 1; ++gi) do_group(gi, std::false_type{});
+      do_group(ngroups - 1, std::true_type{});
     }
-    u += len;
+    // a wave without tiles in this segment starts its next-segment tile now
+    if (wave >= len && nx.e >= 0) issue_h0(nx.e, nx.t0 + (wave < nx.len ? wave : 0));
+    u = u_next;
+    sg = nx;
   }
 }
 
@@ -465,11 +530,13 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   const uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
   // Waves per workgroup and workgroups per CU of the persistent grid;
   // MOE_MX_WAVES / MOE_MX_WG_PER_CU override (tuning runs).
-  static const int waves = [] {
+  static const int waves_env = [] {
     const char* v = getenv("MOE_MX_WAVES");
     const int w = v ? atoi(v) : 11;
     return w < 1 ? 1 : w > 12 ? 12 : w;
   }();
+  // the generic (24-chunk) kernel is built for at most 8 waves
+  const int waves = NC == 23 ? waves_env : min(waves_env, 8);
   static const int wg_per_cu = [] {
     const char* v = getenv("MOE_MX_WG_PER_CU");
     const int t = v ? atoi(v) : 1;
