@@ -12,6 +12,10 @@ int moe_launch_dequant(const void* blocks, const void* scales, void* out, int64_
 int moe_launch_router(const void* x, const void* norm_w, const void* gate_w, const void* gate_b,
                       int n, int H, int E, int k, float eps, void* t_out, void* idx_out,
                       void* w_out, hipStream_t stream);
+int moe_launch_router_pieces(const void* x, const void* norm_w, const void* gate_w,
+                             const void* gate_b, int n, int H, int E, int k, float eps,
+                             void* t_out, void* idx_out, void* w_out, void* pq, void* pqs,
+                             hipStream_t stream);
 int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void* sorted_pairs,
                        void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
 size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
@@ -312,11 +316,18 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   float* y = (float*)(ws + off[11]);
   hipStream_t s = as_stream(stream);
   const int nk = (int)(n * k);
-  if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
-                              idx, w, s)))
+  // decode sizes: router and the pieces of t in one kernel
+  rc = moe_launch_router_pieces(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
+                                idx, w, t_pk, (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT), s);
+  if (rc == MOE_ERR_UNSUPPORTED) {
+    if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
+                                idx, w, s)))
+      return rc;
+    if ((rc = moe_launch_pieces(t, 0, (int)n, (int)H, kPiecesT, t_pk, s))) return rc;
+  } else if (rc) {
     return rc;
+  }
   if ((rc = moe_launch_permute(idx, nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s))) return rc;
-  if ((rc = moe_launch_pieces(t, 0, (int)n, (int)H, kPiecesT, t_pk, s))) return rc;
   if ((rc = moe_launch_mx_gemv(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
                                mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1,
                                alpha, limit, act, (int)I, s)))

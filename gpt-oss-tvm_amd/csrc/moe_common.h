@@ -26,12 +26,8 @@ enum Status : int {
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// fp32 -> bf16 round-to-nearest-even on the bit pattern (NaN -> quiet NaN).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // E8M0 byte -> fp32 2^(s-127); s = 0 is the fp32 subnormal 2^-127 and s = 255
 // is +inf, as exp2(float(s - 127)) gives (model/mlp.py:297-298).
@@ -79,28 +75,35 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------
-// fp8 e4m3 (OCP: bias 7, no infinities, max 448) by construction, round to
-// nearest even.  |y| must be < 448.
-__device__ __forceinline__ uint32_t e4m3_encode(float y) {
-  const uint32_t sign = __float_as_uint(y) >> 31;
-  const float a = fabsf(y);
-  const int e = (int)(__float_as_uint(a) >> 23) - 127;  // a in [2^e, 2^(e+1)) when normal
-  // normal codes (e >= -6): 3 mantissa bits, a / 2^e * 8 rounded in [8, 16]
-  const int en = e < -6 ? -6 : e;
-  const float mant = a * __uint_as_float((uint32_t)(127 - en + 3) << 23);
-  const uint32_t mq = (uint32_t)__builtin_rintf(mant);
-  const uint32_t carry = mq >> 4;  // rounded up to 16: next binade, mantissa 0
-  const uint32_t code_n = ((uint32_t)(en + 7 + (int)carry) << 3) | ((mq - 8u) & 7u);
-  // subnormal codes (e < -6): steps of 2^-9 (8 steps reach 0x08 = 2^-6)
-  const uint32_t code_s = (uint32_t)__builtin_rintf(a * 512.0f);
-  return (e < -6 ? code_s : code_n) | (sign << 7);
+// fp8 e4m3 (OCP: bias 7, no infinities, max 448), through gfx950's
+// conversions: v_cvt_pk_fp8_f32 rounds to nearest even (subnormals included),
+// v_cvt_f32_fp8 is exact.  Four values -> four codes, value j in byte j.
+__device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
-__device__ __forceinline__ float e4m3_decode(uint32_t c) {
-  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-  const float mag = e == 0 ? (float)m * 0.001953125f                          // m * 2^-9
-                           : __uint_as_float((e + 120u) << 23) * (1.0f + 0.125f * (float)m);
-  return (c & 0x80u) ? -mag : mag;
+// Value of byte J of a word of e4m3 codes.
+template <int J>
+__device__ __forceinline__ float e4m3_byte(uint32_t w) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)w, J);
+}
+
+// Eight values r (each |r| * inv < 256) -> eight e4m3 codes of r * inv in
+// (lo, hi), and r minus the value each code stands for (times sc = 1 / inv;
+// exact: the code's value is a rounding of r * inv).
+__device__ __forceinline__ void e4m3_piece8(float* r, float inv, float sc, uint32_t& lo,
+                                            uint32_t& hi) {
+  lo = e4m3_pack4(r[0] * inv, r[1] * inv, r[2] * inv, r[3] * inv);
+  hi = e4m3_pack4(r[4] * inv, r[5] * inv, r[6] * inv, r[7] * inv);
+  r[0] -= e4m3_byte<0>(lo) * sc;
+  r[1] -= e4m3_byte<1>(lo) * sc;
+  r[2] -= e4m3_byte<2>(lo) * sc;
+  r[3] -= e4m3_byte<3>(lo) * sc;
+  r[4] -= e4m3_byte<0>(hi) * sc;
+  r[5] -= e4m3_byte<1>(hi) * sc;
+  r[6] -= e4m3_byte<2>(hi) * sc;
+  r[7] -= e4m3_byte<3>(hi) * sc;
 }
 
 // E8M0 exponent byte for a group whose largest magnitude is amax: the smallest

@@ -108,13 +108,8 @@ __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict_
     const uint32_t s = e8m0_for_amax(amax);
     const float inv = __uint_as_float((254u - s) << 23);                           // 2^(127 - s)
     const float sc = s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u);  // 2^(s - 127)
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t code = e4m3_encode(r[i] * inv);
-      r[i] -= e4m3_decode(code) * sc;  // exact: the code's value is a rounding of r[i]
-      if (i < 4) lo |= code << (8 * i); else hi |= code << (8 * (i - 4));
-    }
+    uint32_t lo, hi;
+    e4m3_piece8(r, inv, sc, lo, hi);
     const size_t prow = (size_t)row * P + p;
     if (!valid) continue;
     *(uint2*)(q + prow * Kp + k0) = make_uint2(lo, hi);

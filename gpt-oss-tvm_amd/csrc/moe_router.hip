@@ -4,6 +4,7 @@
 // variant's gating_softmax_topk call is model/mlp_optimized.py:187.
 // Grouping: mlc-llm moe_cumsum / get_indices / get_indptr / moe_expand_indptr
 // as called at model/mlp_optimized.py:119-148.
+#include <algorithm>
 #include <climits>
 
 #include "moe_common.h"
@@ -193,6 +194,185 @@ __global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(
   }
 }
 
+// Decode router: one token per workgroup of four waves.  Wave w owns experts
+// e = w, w + 4, ... and needs no other wave until the top-k:
+//  1  every lane issues its loads at once: chunks c = lane + 64 i (i < S) of
+//     x and the norm weight, and the first kDecExp gate rows it owns;
+//  2  fp64 sum of squares per lane, fixed-order wave tree (each wave computes
+//     the norm of the whole token itself); r = fp32(1 / sqrt(ss / H + eps));
+//     t = bf16(x * r * w), kept packed;
+//  3  wave 0 writes t; the waves share the t pieces by chunk slot (i % 4 ==
+//     w): the four lanes of a 32-element block share its maximum by lane
+//     exchange (same encoding as moe_pieces_kernel);
+//  4  per owned expert, fp64 dot of t and the gate row: per lane, then a
+//     fixed-order wave tree (the next batch's rows load meanwhile);
+//     logit = bf16(bf16(dot) + bias) into LDS;
+//  5  wave 0: lane e ranks logit e by (value descending, expert ascending)
+//     against all others; the k winners' fp64 exponentials are summed in rank
+//     order and normalised.
+constexpr int kDecWaves = 4;
+constexpr int kDecExp = 4;  // gate rows per lane per load batch
+
+template <bool kPieces, int S>
+__global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+    const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int H, int E, int k,
+    float eps, uint16_t* __restrict__ t_out, int32_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out, uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs) {
+  __shared__ float logit[256];
+  __shared__ double topv[8];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int W = kDecWaves;
+  const int tok = blockIdx.x;
+  const int H8 = H >> 3;
+  const int NC = (H + 127) >> 7;
+  const u32x4* xr = (const u32x4*)(x + (size_t)tok * H);
+  const u32x4* nr = (const u32x4*)norm_w;
+
+  u32x4 xv[S], wv[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int c = min(lane + 64 * i, H8 - 1);
+    xv[i] = xr[c];
+    wv[i] = nr[c];
+  }
+  const int nown = (E - wave + W - 1) / W;  // experts owned by this wave
+  u32x4 gv[kDecExp][S];
+  auto load_gate = [&](int eb) {
+#pragma unroll
+    for (int b = 0; b < kDecExp; ++b) {
+      // a wave owning no expert (E < 4) still issues the batch: row 0
+      const int e = max(0, min(wave + W * min(eb + b, nown - 1), E - 1));
+      const u32x4* gr = (const u32x4*)(gate_w + (size_t)e * H);
+#pragma unroll
+      for (int i = 0; i < S; ++i) gv[b][i] = gr[min(lane + 64 * i, H8 - 1)];
+    }
+  };
+  load_gate(0);  // in flight during the norm
+
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (lane + 64 * i < H8) {
+      float f[8];
+      unpack8(xv[i], f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float rn = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
+
+  u32x4 tp[S];  // t, packed bf16 (zero past H)
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int c = lane + 64 * i;
+    float f[8], g[8];
+    unpack8(xv[i], f);
+    unpack8(wv[i], g);
+    u32x4 o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], rn), g[2 * d]));
+      const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], rn), g[2 * d + 1]));
+      o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    const bool in = c < H8;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) tp[i][d] = in ? o[d] : 0u;
+    if (wave == 0 && in) ((u32x4*)(t_out + (size_t)tok * H))[c] = o;
+    if constexpr (kPieces) {
+      // a quad (32-element block) lies wholly inside or outside [0, 16 * NC)
+      // because H % 32 == 0
+      if (i % W == wave && c < 16 * NC) {
+        const int blk = c >> 2, quarter = c & 3;
+        const int ch = blk >> 2, gg = blk & 3;
+        const int Kp = NC * 128;
+        float rr[8];
+        unpack8(tp[i], rr);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          float amax = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
+          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+          const uint32_t sc = e8m0_for_amax(amax);
+          const float inv = __uint_as_float((254u - sc) << 23);
+          const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+          uint32_t lo, hi;
+          e4m3_piece8(rr, inv, scf, lo, hi);
+          const size_t prow = (size_t)tok * 2 + p;
+          *(uint2*)(pq + prow * Kp + c * 8) = make_uint2(lo, hi);
+          if (quarter == 0) {
+            uint8_t* run = pqs + prow * 112 + gg * 28;
+            run[ch] = (uint8_t)sc;
+            if (ch == NC - 1)
+              for (int z = NC; z < 28; ++z) run[z] = 0;
+          }
+        }
+      }
+    }
+  }
+
+  for (int eb = 0; eb < nown; eb += kDecExp) {
+    double acc[kDecExp];
+#pragma unroll
+    for (int b = 0; b < kDecExp; ++b) {
+      acc[b] = 0.0;
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        float tf[8], gf[8];
+        unpack8(tp[i], tf);
+        unpack8(gv[b][i], gf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[b] = fma((double)tf[q], (double)gf[q], acc[b]);
+      }
+    }
+    if (eb + kDecExp < nown) load_gate(eb + kDecExp);  // next rows load during the trees
+#pragma unroll
+    for (int b = 0; b < kDecExp; ++b) acc[b] = wave_sum(acc[b]);
+    if (lane < kDecExp && eb + lane < nown) {
+      double a = acc[0];
+#pragma unroll
+      for (int b = 1; b < kDecExp; ++b) a = lane == b ? acc[b] : a;
+      const int e = wave + W * (eb + lane);
+      const float d = bf2f(f2bf((float)a));
+      logit[e] = bf2f(f2bf(__fadd_rn(d, bf2f(gate_b[e]))));
+    }
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    // rank of each logit: how many others come first
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      if (e < E) {
+        const float v = logit[e];
+        int rank = 0;
+        for (int o = 0; o < E; ++o) {
+          const float ov = logit[o];
+          rank += (ov > v || (ov == v && o < e)) ? 1 : 0;
+        }
+        if (rank < k) {
+          idx_out[(size_t)tok * k + rank] = e;
+          topv[rank] = (double)v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    double ex = 0.0;
+    if (lane < k) ex = exp(topv[lane] - topv[0]);
+    // summed in rank order, as a single lane would
+    double sum = __shfl(ex, 0, kWave);
+    for (int j = 1; j < k; ++j) sum += __shfl(ex, j, kWave);
+    if (lane < k) w_out[(size_t)tok * k + lane] = f2bf((float)(ex / sum));
+  }
+}
+
 // Stable counting sort of the n*k (token, slot) pairs by expert, one
 // workgroup.  Totals come from LDS atomics (order-free); placement is
 // deterministic: within a round of 1024 pairs a pair's rank among same-expert
@@ -266,10 +446,41 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
 
 }  // namespace moe
 
+// t_pieces (optional, H % 32 == 0): the two fp8 pieces of t, packed as
+// moe_launch_pieces writes them.  Returns kErrUnsupported when the fused form
+// does not apply (n > kDecodeMax or H > 4096 with pieces requested).
+extern "C" int moe_launch_router_pieces(const void* x, const void* norm_w, const void* gate_w,
+                                        const void* gate_b, int n, int H, int E, int k, float eps,
+                                        void* t_out, void* idx_out, void* w_out, void* pq,
+                                        void* pqs, hipStream_t stream) {
+  if (n == 0) return moe::kOk;
+  if (n > 512 || H > 4096 || (pq && H % 32)) return moe::kErrUnsupported;
+  const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
+                 *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
+  const dim3 block(64 * moe::kDecWaves);
+  uint16_t* pt = (uint16_t*)t_out;
+  int32_t* pi = (int32_t*)idx_out;
+  uint16_t* pw = (uint16_t*)w_out;
+  uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
+#define MOE_DEC(PC, S)                                                                          \
+  hipLaunchKernelGGL((moe::moe_router_decode_kernel<PC, S>), dim3(n), block, 0, stream, px, pn, \
+                     pg, pb, H, E, k, eps, pt, pi, pw, q, qs)
+  if (H <= 64 * 6 * 8) {
+    if (pq) MOE_DEC(true, 6); else MOE_DEC(false, 6);
+  } else {
+    if (pq) MOE_DEC(true, 8); else MOE_DEC(false, 8);
+  }
+#undef MOE_DEC
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}
+
 extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* gate_w,
                                  const void* gate_b, int n, int H, int E, int k, float eps,
                                  void* t_out, void* idx_out, void* w_out, hipStream_t stream) {
   if (n == 0) return moe::kOk;
+  if (n <= 512)
+    return moe_launch_router_pieces(x, norm_w, gate_w, gate_b, n, H, E, k, eps, t_out, idx_out,
+                                    w_out, nullptr, nullptr, stream);
   const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
                  *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
   uint16_t *pt = (uint16_t*)t_out, *pw = (uint16_t*)w_out;

@@ -256,6 +256,23 @@ def test_block_20b_shape(native, block20b, n, seed):
     print(f"20B n={n}: {m}")
 
 
+def test_block_router_pieces_fused(native, block20b):
+    """The block's fused router writes the same t pieces as moe_quantize_pieces(t)."""
+    p, blk = block20b
+    n, H = 64, 2880
+    x = bf16_dev(O.make_input(15, n)).view(1, n, H)
+    blk(x)
+    torch.cuda.synchronize()
+    ws = blk._workspace(n, x.device)
+    offs = native.workspace_layout(n, p.num_experts, 4, H, 2880)
+    t = ws[offs[0]: offs[0] + n * H * 2].view(torch.bfloat16).view(n, H)
+    assert np.array_equal(host_bf16(t), O.rms_norm(O.make_input(15, n), p.norm_w))
+    nb = native.pieces_bytes(n, H, 2)
+    fused = host(ws[offs[8]: offs[8] + nb])
+    ref = host(native.quantize_pieces(t.contiguous(), 2))
+    assert np.array_equal(fused, ref), np.argwhere(fused != ref)[:4]
+
+
 def test_block_120b_shape(native):
     p = O.make_params(seed=3, num_experts=128)
     x = O.make_input(13, 48)
