@@ -238,6 +238,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
     wv[i] = nr[c];
   }
   const int nown = (E - wave + W - 1) / W;  // experts owned by this wave
+  if (threadIdx.x >= (unsigned)E && threadIdx.x < (unsigned)((E + 31) & ~31))
+    logit[threadIdx.x] = -INFINITY;
   u32x4 gv[kDecExp][S];
   auto load_gate = [&](int eb) {
 #pragma unroll
@@ -261,7 +263,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
       for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_f64(ss);
   const float rn = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
 
   u32x4 tp[S];  // t, packed bf16 (zero past H)
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
     }
     if (eb + kDecExp < nown) load_gate(eb + kDecExp);  // next rows load during the trees
 #pragma unroll
-    for (int b = 0; b < kDecExp; ++b) acc[b] = wave_sum(acc[b]);
+    for (int b = 0; b < kDecExp; ++b) acc[b] = wave_sum_f64(acc[b]);
     if (lane < kDecExp && eb + lane < nown) {
       double a = acc[0];
 #pragma unroll
@@ -345,20 +347,23 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
   __syncthreads();
 
   if (wave == 0) {
-    // rank of each logit: how many others come first
+    // rank of each logit: how many others come first (logits past E are
+    // -inf and never do)
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + lane;
-      if (e < E) {
-        const float v = logit[e];
-        int rank = 0;
-        for (int o = 0; o < E; ++o) {
-          const float ov = logit[o];
-          rank += (ov > v || (ov == v && o < e)) ? 1 : 0;
-        }
-        if (rank < k) {
-          idx_out[(size_t)tok * k + rank] = e;
-          topv[rank] = (double)v;
-        }
+      const float v = e < E ? logit[e] : 0.0f;
+      int rank = 0;
+      for (int o0 = 0; o0 < E; o0 += 32) {
+        float ov[32];
+#pragma unroll
+        for (int o = 0; o < 32; ++o) ov[o] = logit[o0 + o];
+#pragma unroll
+        for (int o = 0; o < 32; ++o)
+          rank += (ov[o] > v || (ov[o] == v && o0 + o < e)) ? 1 : 0;
+      }
+      if (e < E && rank < k) {
+        idx_out[(size_t)tok * k + rank] = e;
+        topv[rank] = (double)v;
       }
     }
   }
@@ -367,8 +372,14 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
     double ex = 0.0;
     if (lane < k) ex = exp(topv[lane] - topv[0]);
     // summed in rank order, as a single lane would
-    double sum = __shfl(ex, 0, kWave);
-    for (int j = 1; j < k; ++j) sum += __shfl(ex, j, kWave);
+    auto lane_f64 = [&](int j) {
+      const uint64_t u = __builtin_bit_cast(uint64_t, ex);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, j);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+      return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+    };
+    double sum = lane_f64(0);
+    for (int j = 1; j < k; ++j) sum += lane_f64(j);
     if (lane < k) w_out[(size_t)tok * k + lane] = f2bf((float)(ex / sum));
   }
 }
@@ -395,14 +406,24 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
     if (v >= 0 && v < E) atomicAdd(&cnt[v], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      base[e] = run;
-      indptr[e] = run;
-      run += cnt[e];
+  if (wave == 0) {  // exclusive prefix of the counts, 64 experts per step
+    int carry = 0;
+    for (int b = 0; b < E; b += 64) {
+      const int e = b + lane;
+      const int c = e < E ? cnt[e] : 0;
+      int v = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+      }
+      if (e < E) {
+        base[e] = carry + v - c;
+        indptr[e] = carry + v - c;
+      }
+      carry += __shfl(v, 63, 64);
     }
-    indptr[E] = run;
+    if (lane == 0) indptr[E] = carry;
   }
   __syncthreads();
 
