@@ -131,6 +131,9 @@ def main() -> int:
     ap.add_argument("--weight-sets", type=int, default=3)
     ap.add_argument("--cpu-tokens", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 device copies of 512 MiB (the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -138,6 +141,15 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calibration:
+        src = torch.ones(512 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 5 x 512 MiB device copies")
+        return 0
 
     from oracle import moe_oracle as O
 
