@@ -18,6 +18,13 @@ int moe_launch_router_pieces(const void* x, const void* norm_w, const void* gate
                              hipStream_t stream);
 int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void* sorted_pairs,
                        void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
+int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
+                             const void* gate_b, int n, int H, int E, float eps, void* t_out,
+                             float* logits, void* pq, void* pqs, hipStream_t stream);
+int moe_select_chunks(int n);
+int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out, void* w_out,
+                            void* counts, void* indptr, void* sorted_pairs, void* token_indices,
+                            void* expert_ids, void* pair_pos, hipStream_t stream);
 size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
 size_t moe_pieces_total_bytes(int64_t rows, int64_t K, int pieces);
 int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, void* packed,
@@ -52,7 +59,7 @@ int check_dims(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-constexpr int kNumRegions = 12;
+constexpr int kNumRegions = 14;
 constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
 constexpr int kPiecesAct = 4;  // fp8 pieces of the fp32 SwiGLU output (~16 bits)
 
@@ -72,6 +79,8 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       nk * (size_t)I * 4,                              // act      fp32 [n*k, I]
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
       nk * (size_t)H * 4,     // y        fp32 [n*k, H]
+      (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
+      (size_t)moe_select_chunks((int)n) * E * 4,  // counts int32 [chunks of 64 tokens, E]
   };
   size_t o = 0;
   for (int i = 0; i < kNumRegions; ++i) {
@@ -272,7 +281,7 @@ size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I
 }
 
 int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                         size_t offsets[12]) {
+                         size_t offsets[14]) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (!offsets) return MOE_ERR_NULL;
@@ -316,18 +325,16 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   float* y = (float*)(ws + off[11]);
   hipStream_t s = as_stream(stream);
   const int nk = (int)(n * k);
-  // decode sizes: router and the pieces of t in one kernel
-  rc = moe_launch_router_pieces(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
-                                idx, w, t_pk, (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT), s);
-  if (rc == MOE_ERR_UNSUPPORTED) {
-    if ((rc = moe_launch_router(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps, t,
-                                idx, w, s)))
-      return rc;
-    if ((rc = moe_launch_pieces(t, 0, (int)n, (int)H, kPiecesT, t_pk, s))) return rc;
-  } else if (rc) {
+  float* logits = (float*)(ws + off[12]);
+  int32_t* counts = (int32_t*)(ws + off[13]);
+  // norm, t, its pieces and the logits; then top-k, softmax and grouping
+  if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
+                                     logits, t_pk,
+                                     (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT), s)))
     return rc;
-  }
-  if ((rc = moe_launch_permute(idx, nk, (int)k, (int)E, indptr, sp, ti, ei, pp, s))) return rc;
+  if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
+                                    ei, pp, s)))
+    return rc;
   if ((rc = moe_launch_mx_gemv(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
                                mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1,
                                alpha, limit, act, (int)I, s)))

@@ -38,6 +38,7 @@ constexpr int kMxSclRow = 4 * kMxSclRun;                   // 112 scale bytes pe
 constexpr int kMxMaxGroups = 3;
 constexpr int kLdsBytes = 160 * 1024;                      // per CU
 constexpr int kNumCUs = 256;                               // MI355X
+constexpr int kNumXcds = 8;                                // 8 XCDs of 32 CUs, one L2 each
 
 // LDS bytes per staged activation row and per 16-row A operand group for a
 // kernel that runs NCT chunks (the 16-byte pad spreads the 16 rows of one
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
     int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
     const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
-    int groups_cap, float alpha, float limit, float* __restrict__ out, int out_ld) {
+    int groups_cap, float alpha, float limit, float* __restrict__ out, int out_ld, int xcds) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
@@ -182,8 +183,14 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   }
   __syncthreads();
   const int64_t total = pre[E];
-  const int ubeg = (int)(total * blockIdx.x / gridDim.x);
-  const int uend = (int)(total * (blockIdx.x + 1) / gridDim.x);
+  // Workgroups go to the XCDs round-robin (workgroup b on XCD b % xcds).
+  // Numbering them XCD-major hands each XCD one contiguous run of unit
+  // ranges, so the workgroups that stage an expert's activations share an L2.
+  const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
+                                (int)(blockIdx.x / xcds)
+                          : (int)blockIdx.x;
+  const int ubeg = (int)(total * vb / gridDim.x);
+  const int uend = (int)(total * (vb + 1) / gridDim.x);
   if (ubeg >= uend) return;
   auto expert_of = [&](int u) {  // largest e with pre[e] <= u
     int lo = 0, hi = E - 1;
@@ -456,7 +463,7 @@ template <int P, int kEpi>
 int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const uint8_t* q,
               const uint8_t* qs, int Kp, const int* indptr, const int* sp, int k_top, int arow,
               int orow, const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, int N,
-              int G, int E, int gcap, float alpha, float limit, float* out, int out_ld) {
+              int G, int E, int gcap, float alpha, float limit, float* out, int out_ld, int xcds) {
   static const bool lds_ok = [] {  // allow more than 64 KB of dynamic LDS, once per kernel
     const int bytes = kLdsBytes;
     return hipFuncSetAttribute((const void*)moe_mx_gemv_kernel<P, kEpi, 23>,
@@ -468,11 +475,11 @@ int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, con
   if (NC == 23)
     hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, 23>), grid, block, lds, stream, q, qs, Kp,
                        indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, gcap, alpha,
-                       limit, out, out_ld);
+                       limit, out, out_ld, xcds);
   else
     hipLaunchKernelGGL((moe_mx_gemv_kernel<P, kEpi, kMxMaxChunks>), grid, block, lds, stream, q,
                        qs, Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, gcap,
-                       alpha, limit, out, out_ld);
+                       alpha, limit, out, out_ld, xcds);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -555,6 +562,11 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   const int nwg = (int)(units_max < target ? (units_max < 1 ? 1 : units_max) : target);
   const dim3 grid(nwg);
   const dim3 block(64 * waves);
+  static const bool xcd_env = [] {
+    const char* v = getenv("MOE_MX_XCD");
+    return !(v && atoi(v) == 0);
+  }();
+  const int xcds = (xcd_env && nwg % moe::kNumXcds == 0) ? moe::kNumXcds : 1;
   const int* ip = (const int*)indptr;
   const int* sp = (const int*)sorted_pairs;
   const uint8_t* b = (const uint8_t*)blocks;
@@ -564,15 +576,15 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   if (pieces == 2 && swiglu)
     return moe::launch_mx<2, 1>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
-                                out_ld);
+                                out_ld, xcds);
   if (pieces == 2)
     return moe::launch_mx<2, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
-                                out_ld);
+                                out_ld, xcds);
   if (pieces == 4 && !swiglu)
     return moe::launch_mx<4, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
-                                out_ld);
+                                out_ld, xcds);
   return moe::kErrUnsupported;
 }
 

@@ -20,357 +20,216 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
   }
 }
 
-// One workgroup of 1024 threads (16 waves) routes TB <= 16 tokens.
-//  phase 1  one wave per token: fp64 sum of squares, r = fp32(1/sqrt(ss/H+eps)),
-//           t = bf16(x*r*w) to HBM and to LDS;
-//  phase 2  1024/E threads per expert, each a strided set of 16-byte chunks of
-//           the expert's gate row, fp64 partial dots for all TB tokens; the
-//           partials are summed in a fixed order, rounded fp64->fp32->bf16, the
-//           bias added in fp32 and rounded to bf16 again;
-//  phase 3  one wave per token: k rounds of a wave arg-max under the order
-//           (logit descending, expert ascending), then an fp64 softmax.
-// Loads are issued in unconditional batches (indices clamped in range) so that
-// each thread has one batch of requests in flight instead of a chain.
-constexpr int kRouterThreads = 1024;
-constexpr int kRouterWaves = kRouterThreads / 64;
-
-template <int TB>
-__global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(
+// Router: TT consecutive tokens per workgroup of W waves.  Wave w owns experts
+// e = w, w + W, ... and needs no other wave until the top-k:
+//  1  every lane issues its loads at once: chunks c = lane + 64 i (i < S) of
+//     the TT token rows and the norm weight, and the first KE gate rows it
+//     owns;
+//  2  per token, fp64 sum of squares per lane, fixed-order wave tree (each
+//     wave computes the norms itself); r = fp32(1 / sqrt(ss / H + eps));
+//     t = bf16(x * r * w), kept packed; wave 0 writes t;
+//  3  the (token, chunk slot) pairs are shared out over the waves for the
+//     two fp8 pieces of t: the four lanes of a 32-element block share its
+//     maximum by lane exchange (same encoding as moe_pieces_kernel);
+//  4  per owned expert and token, the dot of t and the gate row: every
+//     product of two bf16 values is exact in fp32 and is added in fp64, per
+//     lane, then by a fixed-order wave tree (the next batch of gate rows loads
+//     meanwhile); logit = bf16(bf16(fp32(dot)) + bias) into LDS;
+//  5  wave j < TT ranks token j's logits by (value descending, expert
+//     ascending); the k winners' fp64 exponentials are summed in rank order
+//     and normalised.
+// A product below 2^-126 in magnitude is rounded to an fp32 subnormal; no
+// logit above 2^-100 can change by it.
+template <bool kPieces, int S, int W, int TT, int KE>
+__global__ __launch_bounds__(64 * W) void moe_router_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
     int k, float eps, uint16_t* __restrict__ t_out, int32_t* __restrict__ idx_out,
-    uint16_t* __restrict__ w_out) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* t_lds = (uint16_t*)smem;                                      // [TB][H]
-  double* part = (double*)(smem + (size_t)TB * H * 2);                    // [1024][TB]
-  float* logit = (float*)((unsigned char*)part + kRouterThreads * TB * 8);  // [TB][E]
-
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int tok0 = blockIdx.x * TB;
-  const int H8 = H >> 3;
-
-  constexpr int kMaxChunks = 8;  // H <= 4096: at most 8 16-byte chunks per lane
-  for (int tb = wave; tb < TB; tb += kRouterWaves) {
-    const int tok = tok0 + tb;
-    u32x4* trow_lds = (u32x4*)(t_lds + (size_t)tb * H);
-    if (tok < n) {
-      const u32x4* xr = (const u32x4*)(x + (size_t)tok * H);
-      const u32x4* wr = (const u32x4*)norm_w;
-      u32x4 xv[kMaxChunks], wv[kMaxChunks];
-#pragma unroll
-      for (int i = 0; i < kMaxChunks; ++i) {
-        const int c = min(lane + kWave * i, H8 - 1);
-        xv[i] = xr[c];
-        wv[i] = wr[c];
-      }
-      double ss = 0.0;
-#pragma unroll
-      for (int i = 0; i < kMaxChunks; ++i) {
-        if (lane + kWave * i < H8) {
-          float f[8];
-          unpack8(xv[i], f);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
-        }
-      }
-      ss = wave_sum(ss);
-      const float r = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
-      u32x4* trow = (u32x4*)(t_out + (size_t)tok * H);
-#pragma unroll
-      for (int i = 0; i < kMaxChunks; ++i) {
-        const int c = lane + kWave * i;
-        if (c < H8) {
-          float f[8], g[8];
-          unpack8(xv[i], f);
-          unpack8(wv[i], g);
-          u32x4 o;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], r), g[2 * d]));
-            const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], r), g[2 * d + 1]));
-            o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
-          }
-          trow[c] = o;
-          trow_lds[c] = o;
-        }
-      }
-    } else {
-      for (int c = lane; c < H8; c += kWave) trow_lds[c] = u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  __syncthreads();
-
-  const int ks = kRouterThreads / E;  // threads per expert
-  {
-    const int e = tid / ks, s = tid - (tid / ks) * ks;
-    double acc[TB];
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) acc[tb] = 0.0;
-    if (e < E) {
-      constexpr int kBatch = 12;
-      const u32x4* wr = (const u32x4*)(gate_w + (size_t)e * H);
-      for (int c0 = s; c0 < H8; c0 += kBatch * ks) {
-        u32x4 wv[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) wv[u] = wr[min(c0 + u * ks, H8 - 1)];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int c = c0 + u * ks;
-          if (c < H8) {
-            float wf[8];
-            unpack8(wv[u], wf);
-#pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
-              float tf[8];
-              unpack8(((const u32x4*)(t_lds + (size_t)tb * H))[c], tf);
-#pragma unroll
-              for (int i = 0; i < 8; ++i) acc[tb] = fma((double)tf[i], (double)wf[i], acc[tb]);
-            }
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) part[tid * TB + tb] = acc[tb];
-  }
-  __syncthreads();
-  for (int pi = tid; pi < E * TB; pi += kRouterThreads) {
-    const int e = pi / TB, tb = pi - (pi / TB) * TB;
-    double sum = 0.0;
-    for (int s = 0; s < ks; ++s) sum += part[(e * ks + s) * TB + tb];
-    const float dot = bf2f(f2bf((float)sum));
-    logit[tb * E + e] = bf2f(f2bf(__fadd_rn(dot, bf2f(gate_b[e]))));
-  }
-  __syncthreads();
-
-  for (int tb = wave; tb < TB; tb += kRouterWaves) {
-    const int tok = tok0 + tb;
-    if (tok >= n) continue;
-    float v[4];
-    bool taken[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + 64 * j;
-      v[j] = e < E ? logit[tb * E + e] : 0.0f;
-      taken[j] = e >= E;
-    }
-    double sel_v[8];
-    int sel_i[8];
-    for (int j = 0; j < k; ++j) {
-      float bv = -INFINITY;
-      int bi = INT_MAX;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int e = lane + 64 * jj;
-        if (!taken[jj] && (v[jj] > bv || (v[jj] == bv && e < bi))) {
-          bv = v[jj];
-          bi = e;
-        }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, kWave);
-        const int oi = __shfl_xor(bi, off, kWave);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      if (bi < E && (bi & 63) == lane) taken[bi >> 6] = true;
-      sel_v[j] = (double)bv;
-      sel_i[j] = bi < E ? bi : 0;
-    }
-    if (lane == 0) {
-      double ex[8], sum = 0.0;
-      for (int j = 0; j < k; ++j) {
-        ex[j] = exp(sel_v[j] - sel_v[0]);
-        sum = j == 0 ? ex[0] : sum + ex[j];
-      }
-      for (int j = 0; j < k; ++j) {
-        idx_out[(size_t)tok * k + j] = sel_i[j];
-        w_out[(size_t)tok * k + j] = f2bf((float)(ex[j] / sum));
-      }
-    }
-  }
-}
-
-// Decode router: one token per workgroup of four waves.  Wave w owns experts
-// e = w, w + 4, ... and needs no other wave until the top-k:
-//  1  every lane issues its loads at once: chunks c = lane + 64 i (i < S) of
-//     x and the norm weight, and the first kDecExp gate rows it owns;
-//  2  fp64 sum of squares per lane, fixed-order wave tree (each wave computes
-//     the norm of the whole token itself); r = fp32(1 / sqrt(ss / H + eps));
-//     t = bf16(x * r * w), kept packed;
-//  3  wave 0 writes t; the waves share the t pieces by chunk slot (i % 4 ==
-//     w): the four lanes of a 32-element block share its maximum by lane
-//     exchange (same encoding as moe_pieces_kernel);
-//  4  per owned expert, fp64 dot of t and the gate row: per lane, then a
-//     fixed-order wave tree (the next batch's rows load meanwhile);
-//     logit = bf16(bf16(dot) + bias) into LDS;
-//  5  wave 0: lane e ranks logit e by (value descending, expert ascending)
-//     against all others; the k winners' fp64 exponentials are summed in rank
-//     order and normalised.
-constexpr int kDecWaves = 4;
-constexpr int kDecExp = 4;  // gate rows per lane per load batch
-
-template <bool kPieces, int S>
-__global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
-    const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int H, int E, int k,
-    float eps, uint16_t* __restrict__ t_out, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out, uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs) {
-  __shared__ float logit[256];
-  __shared__ double topv[8];
+  __shared__ float logit[TT][256];
+  __shared__ double topv[TT][8];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  constexpr int W = kDecWaves;
-  const int tok = blockIdx.x;
+  const int tok0 = blockIdx.x * TT;
+  const int ntok = min(TT, n - tok0);
   const int H8 = H >> 3;
   const int NC = (H + 127) >> 7;
-  const u32x4* xr = (const u32x4*)(x + (size_t)tok * H);
   const u32x4* nr = (const u32x4*)norm_w;
 
-  u32x4 xv[S], wv[S];
+  // rows past n repeat the last token (computed, never stored)
+  u32x4 xv[TT][S], wv[S];
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const int c = min(lane + 64 * i, H8 - 1);
-    xv[i] = xr[c];
-    wv[i] = nr[c];
+  for (int i = 0; i < S; ++i) wv[i] = nr[min(lane + 64 * i, H8 - 1)];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const u32x4* xr = (const u32x4*)(x + (size_t)min(tok0 + tt, n - 1) * H);
+#pragma unroll
+    for (int i = 0; i < S; ++i) xv[tt][i] = xr[min(lane + 64 * i, H8 - 1)];
   }
-  const int nown = (E - wave + W - 1) / W;  // experts owned by this wave
-  if (threadIdx.x >= (unsigned)E && threadIdx.x < (unsigned)((E + 31) & ~31))
-    logit[threadIdx.x] = -INFINITY;
-  u32x4 gv[kDecExp][S];
+  const int nown = (E - wave + W - 1) / W;  // experts owned by this wave (may be 0)
+  const int Epad = (E + 31) & ~31;
+  for (int u = threadIdx.x; u < TT * 256; u += 64 * W) {
+    const int e = u & 255;
+    if (e >= E && e < Epad) logit[u >> 8][e] = -INFINITY;
+  }
+  u32x4 gv[KE][S];
   auto load_gate = [&](int eb) {
 #pragma unroll
-    for (int b = 0; b < kDecExp; ++b) {
-      // a wave owning no expert (E < 4) still issues the batch: row 0
+    for (int b = 0; b < KE; ++b) {
+      // a wave owning no expert still issues the batch (a valid row)
       const int e = max(0, min(wave + W * min(eb + b, nown - 1), E - 1));
       const u32x4* gr = (const u32x4*)(gate_w + (size_t)e * H);
 #pragma unroll
       for (int i = 0; i < S; ++i) gv[b][i] = gr[min(lane + 64 * i, H8 - 1)];
     }
   };
-  load_gate(0);  // in flight during the norm
+  load_gate(0);  // in flight during the norms
 
-  double ss = 0.0;
+  u32x4 tp[TT][S];  // t, packed bf16 (zero past H)
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    if (lane + 64 * i < H8) {
-      float f[8];
-      unpack8(xv[i], f);
+  for (int tt = 0; tt < TT; ++tt) {
+    double ss = 0.0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+    for (int i = 0; i < S; ++i) {
+      if (lane + 64 * i < H8) {
+        float f[8];
+        unpack8(xv[tt][i], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+      }
     }
-  }
-  ss = wave_sum_f64(ss);
-  const float rn = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
-
-  u32x4 tp[S];  // t, packed bf16 (zero past H)
+    ss = wave_sum_f64(ss);
+    const float rn = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
+    const int tok = tok0 + tt;
+    // unpack x again below rather than holding 8 S floats across the tree
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const int c = lane + 64 * i;
-    float f[8], g[8];
-    unpack8(xv[i], f);
-    unpack8(wv[i], g);
-    u32x4 o;
+    for (int i = 0; i < S; ++i) asm volatile("" : "+v"(xv[tt][i]));
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], rn), g[2 * d]));
-      const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], rn), g[2 * d + 1]));
-      o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
-    }
-    const bool in = c < H8;
+    for (int i = 0; i < S; ++i) {
+      const int c = lane + 64 * i;
+      float f[8], g[8];
+      unpack8(xv[tt][i], f);
+      unpack8(wv[i], g);
+      u32x4 o;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) tp[i][d] = in ? o[d] : 0u;
-    if (wave == 0 && in) ((u32x4*)(t_out + (size_t)tok * H))[c] = o;
-    if constexpr (kPieces) {
-      // a quad (32-element block) lies wholly inside or outside [0, 16 * NC)
-      // because H % 32 == 0
-      if (i % W == wave && c < 16 * NC) {
-        const int blk = c >> 2, quarter = c & 3;
-        const int ch = blk >> 2, gg = blk & 3;
-        const int Kp = NC * 128;
-        float rr[8];
-        unpack8(tp[i], rr);
+      for (int d = 0; d < 4; ++d) {
+        const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], rn), g[2 * d]));
+        const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], rn), g[2 * d + 1]));
+        o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+      }
+      const bool in = c < H8;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          float amax = 0.0f;
+      for (int d = 0; d < 4; ++d) tp[tt][i][d] = in ? o[d] : 0u;
+      if (wave == 0 && in && tt < ntok) ((u32x4*)(t_out + (size_t)tok * H))[c] = o;
+      if constexpr (kPieces) {
+        // a quad (32-element block) lies wholly inside or outside [0, 16 * NC)
+        // because H % 32 == 0
+        if ((tt * S + i) % W == wave && tt < ntok && c < 16 * NC) {
+          const int blk = c >> 2, quarter = c & 3;
+          const int ch = blk >> 2, gg = blk & 3;
+          const int Kp = NC * 128;
+          float rr[8];
+          unpack8(tp[tt][i], rr);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
-          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
-          const uint32_t sc = e8m0_for_amax(amax);
-          const float inv = __uint_as_float((254u - sc) << 23);
-          const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
-          uint32_t lo, hi;
-          e4m3_piece8(rr, inv, scf, lo, hi);
-          const size_t prow = (size_t)tok * 2 + p;
-          *(uint2*)(pq + prow * Kp + c * 8) = make_uint2(lo, hi);
-          if (quarter == 0) {
-            uint8_t* run = pqs + prow * 112 + gg * 28;
-            run[ch] = (uint8_t)sc;
-            if (ch == NC - 1)
-              for (int z = NC; z < 28; ++z) run[z] = 0;
+          for (int p = 0; p < 2; ++p) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            const uint32_t sc = e8m0_for_amax(amax);
+            const float inv = __uint_as_float((254u - sc) << 23);
+            const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+            uint32_t lo, hi;
+            e4m3_piece8(rr, inv, scf, lo, hi);
+            const size_t prow = (size_t)tok * 2 + p;
+            *(uint2*)(pq + prow * Kp + c * 8) = make_uint2(lo, hi);
+            if (quarter == 0) {
+              uint8_t* run = pqs + prow * 112 + gg * 28;
+              run[ch] = (uint8_t)sc;
+              if (ch == NC - 1)
+                for (int z = NC; z < 28; ++z) run[z] = 0;
+            }
           }
         }
       }
     }
   }
 
-  for (int eb = 0; eb < nown; eb += kDecExp) {
-    double acc[kDecExp];
+  for (int eb = 0; eb < nown; eb += KE) {
+    // t stays packed: the opaque copy keeps its unpacking inside the loop
 #pragma unroll
-    for (int b = 0; b < kDecExp; ++b) {
-      acc[b] = 0.0;
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int i = 0; i < S; ++i) asm volatile("" : "+v"(tp[tt][i]));
+    double acc[KE][TT];
+#pragma unroll
+    for (int b = 0; b < KE; ++b) {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = 0.0;
 #pragma unroll
       for (int i = 0; i < S; ++i) {
-        float tf[8], gf[8];
-        unpack8(tp[i], tf);
+        float gf[8];
         unpack8(gv[b][i], gf);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[b] = fma((double)tf[q], (double)gf[q], acc[b]);
+        for (int tt = 0; tt < TT; ++tt) {
+          float tf[8];
+          unpack8(tp[tt][i], tf);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[b][tt] += (double)__fmul_rn(tf[q], gf[q]);
+        }
       }
     }
-    if (eb + kDecExp < nown) load_gate(eb + kDecExp);  // next rows load during the trees
+    if (eb + KE < nown) load_gate(eb + KE);  // next rows load during the trees
 #pragma unroll
-    for (int b = 0; b < kDecExp; ++b) acc[b] = wave_sum_f64(acc[b]);
-    if (lane < kDecExp && eb + lane < nown) {
-      double a = acc[0];
+    for (int b = 0; b < KE; ++b)
 #pragma unroll
-      for (int b = 1; b < kDecExp; ++b) a = lane == b ? acc[b] : a;
-      const int e = wave + W * (eb + lane);
-      const float d = bf2f(f2bf((float)a));
-      logit[e] = bf2f(f2bf(__fadd_rn(d, bf2f(gate_b[e]))));
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = wave_sum_f64(acc[b][tt]);
+    // lane b * TT + tt stores expert (eb + b)'s logit for token tt
+    if (lane < KE * TT) {
+      const int b = lane / TT, tt = lane - b * TT;
+      double a = acc[0][0];
+#pragma unroll
+      for (int bb = 0; bb < KE; ++bb)
+#pragma unroll
+        for (int t2 = 0; t2 < TT; ++t2) a = lane == bb * TT + t2 ? acc[bb][t2] : a;
+      if (eb + b < nown) {
+        const int e = wave + W * (eb + b);
+        const float d = bf2f(f2bf((float)a));
+        logit[tt][e] = bf2f(f2bf(__fadd_rn(d, bf2f(gate_b[e]))));
+      }
     }
   }
   __syncthreads();
 
-  if (wave == 0) {
+  if (wave < ntok) {
+    const int tok = tok0 + wave;
+    const float* lg = logit[wave];
     // rank of each logit: how many others come first (logits past E are
     // -inf and never do)
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + lane;
-      const float v = e < E ? logit[e] : 0.0f;
+      const float v = e < E ? lg[e] : 0.0f;
       int rank = 0;
       for (int o0 = 0; o0 < E; o0 += 32) {
         float ov[32];
 #pragma unroll
-        for (int o = 0; o < 32; ++o) ov[o] = logit[o0 + o];
+        for (int o = 0; o < 32; ++o) ov[o] = lg[o0 + o];
 #pragma unroll
         for (int o = 0; o < 32; ++o)
           rank += (ov[o] > v || (ov[o] == v && o0 + o < e)) ? 1 : 0;
       }
       if (e < E && rank < k) {
         idx_out[(size_t)tok * k + rank] = e;
-        topv[rank] = (double)v;
+        topv[wave][rank] = (double)v;
       }
     }
   }
   __syncthreads();
-  if (wave == 0) {
+  if (wave < ntok) {
+    const int tok = tok0 + wave;
     double ex = 0.0;
-    if (lane < k) ex = exp(topv[lane] - topv[0]);
+    if (lane < k) ex = exp(topv[wave][lane] - topv[wave][0]);
     // summed in rank order, as a single lane would
     auto lane_f64 = [&](int j) {
       const uint64_t u = __builtin_bit_cast(uint64_t, ex);
@@ -384,53 +243,243 @@ __global__ __launch_bounds__(64 * kDecWaves) void moe_router_decode_kernel(
   }
 }
 
-// Stable counting sort of the n*k (token, slot) pairs by expert, one
-// workgroup.  Totals come from LDS atomics (order-free); placement is
-// deterministic: within a round of 1024 pairs a pair's rank among same-expert
-// pairs comes from ballots, so pairs keep flattened (token, slot) order inside
-// each expert, exactly as np.argsort(kind="stable").  Pairs whose expert id is
-// out of range are not placed (pair_pos = -1).
-__global__ __launch_bounds__(1024) void moe_permute_kernel(
-    const int32_t* __restrict__ idx, int nk, int k, int E, int32_t* __restrict__ indptr,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
-  __shared__ int cnt[256];
-  __shared__ int base[256];
-  __shared__ int wcnt[16 * 256];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+// Router logits: workgroup (bx, by) of W waves computes the logits of tokens
+// [TT bx, TT bx + TT) for experts [W by, W by + W), one expert per wave.
+//  1  the threads load the token rows and the norm weight cooperatively (one
+//     16-byte chunk per thread and token); each wave loads its gate row;
+//  2  per token, fp64 sum of squares: per thread, fixed-order wave tree, then
+//     the waves' sums in wave order; r = fp32(1 / sqrt(ss / H + eps));
+//     t = bf16(x * r * w) into LDS; workgroups with by == 0 also write t and
+//     its two fp8 pieces (the four threads of a 32-element block share its
+//     maximum by lane exchange, the encoding of moe_pieces_kernel);
+//  3  per token, the dot of t and the wave's gate row: every product of two
+//     bf16 values is exact in fp32 and is added in fp64, per lane, then by a
+//     fixed-order wave tree; logit = bf16(bf16(fp32(dot)) + bias), stored as
+//     fp32.
+// A product below 2^-126 in magnitude is rounded to an fp32 subnormal; no
+// logit above 2^-100 can change by it.
+template <bool kPieces, int S, int W, int TT>
+__global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+    const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
+    float eps, uint16_t* __restrict__ t_out, float* __restrict__ logits,
+    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs) {
+  constexpr int kChunks = 64 * S;                // 16-byte chunks of a row, at most
+  constexpr int J = (kChunks + 64 * W - 1) / (64 * W);  // chunks per thread and token
+  __shared__ u32x4 t_lds[TT][kChunks];
+  __shared__ double ss_part[W][TT];
+  __shared__ float rn_lds[TT];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tok0 = blockIdx.x * TT;
+  const int ntok = min(TT, n - tok0);
+  const int e = blockIdx.y * W + wave;
+  const bool own = e < E;  // wave-uniform
+  const int H8 = H >> 3;
+  const int NC = (H + 127) >> 7;
 
-  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
-  __syncthreads();
-  for (int p = tid; p < nk; p += 1024) {
-    const int v = idx[p];
-    if (v >= 0 && v < E) atomicAdd(&cnt[v], 1);
-  }
-  __syncthreads();
-  if (wave == 0) {  // exclusive prefix of the counts, 64 experts per step
-    int carry = 0;
-    for (int b = 0; b < E; b += 64) {
-      const int e = b + lane;
-      const int c = e < E ? cnt[e] : 0;
-      int v = c;
+  u32x4 gv[S];
+  {
+    const u32x4* gr = (const u32x4*)(gate_w + (size_t)min(e, E - 1) * H);
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(v, o, 64);
-        if (lane >= o) v += t;
+    for (int i = 0; i < S; ++i) gv[i] = gr[min(lane + 64 * i, H8 - 1)];
+  }
+  // rows past n repeat the last token (computed, never stored)
+  u32x4 xv[TT][J], wv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) wv[j] = ((const u32x4*)norm_w)[min(tid + 64 * W * j, H8 - 1)];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const u32x4* xr = (const u32x4*)(x + (size_t)min(tok0 + tt, n - 1) * H);
+#pragma unroll
+    for (int j = 0; j < J; ++j) xv[tt][j] = xr[min(tid + 64 * W * j, H8 - 1)];
+  }
+
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (tid + 64 * W * j < H8) {
+        float f[8];
+        unpack8(xv[tt][j], f);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ss = fma((double)f[q], (double)f[q], ss);
       }
-      if (e < E) {
-        base[e] = carry + v - c;
-        indptr[e] = carry + v - c;
-      }
-      carry += __shfl(v, 63, 64);
     }
-    if (lane == 0) indptr[E] = carry;
+    ss = wave_sum_f64(ss);
+    if (lane == 0) ss_part[wave][tt] = ss;
+  }
+  __syncthreads();
+  if (tid < TT) {
+    double ss = ss_part[0][tid];
+    for (int w = 1; w < W; ++w) ss += ss_part[w][tid];
+    rn_lds[tid] = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
   }
   __syncthreads();
 
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const float rn = rn_lds[tt];
+    const int tok = tok0 + tt;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      // chunks in [H8, 16 NC) are the zero tail of the pieces' last 128
+      const int c = tid + 64 * W * j;
+      if (c >= (kPieces ? 16 * NC : H8)) continue;
+      u32x4 o = {0u, 0u, 0u, 0u};
+      if (c < H8) {
+        float f[8], g[8];
+        unpack8(xv[tt][j], f);
+        unpack8(wv[j], g);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint16_t lo = f2bf(__fmul_rn(__fmul_rn(f[2 * d], rn), g[2 * d]));
+          const uint16_t hi = f2bf(__fmul_rn(__fmul_rn(f[2 * d + 1], rn), g[2 * d + 1]));
+          o[d] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        t_lds[tt][c] = o;
+      }
+      if (blockIdx.y == 0 && tt < ntok) {
+        if (c < H8) ((u32x4*)(t_out + (size_t)tok * H))[c] = o;
+        if constexpr (kPieces) {
+          // the quad of a 32-element block is four consecutive threads of
+          // one wave, all below H8 or all in the tail (H % 32 == 0)
+          const int blk = c >> 2, quarter = c & 3;
+          const int ch = blk >> 2, gg = blk & 3;
+          const int Kp = NC * 128;
+          float rr[8];
+          unpack8(o, rr);
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            const uint32_t sc = e8m0_for_amax(amax);
+            const float inv = __uint_as_float((254u - sc) << 23);
+            const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+            uint32_t lo, hi;
+            e4m3_piece8(rr, inv, scf, lo, hi);
+            const size_t prow = (size_t)tok * 2 + p;
+            *(uint2*)(pq + prow * Kp + c * 8) = make_uint2(lo, hi);
+            if (quarter == 0) {
+              uint8_t* run = pqs + prow * 112 + gg * 28;
+              run[ch] = (uint8_t)sc;
+              if (ch == NC - 1)
+                for (int z = NC; z < 28; ++z) run[z] = 0;
+            }
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (!own) return;
+
+  double acc[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) acc[tt] = 0.0;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int c = lane + 64 * i;
+    if (c < H8) {
+      float gf[8];
+      unpack8(gv[i], gf);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        float tf[8];
+        unpack8(t_lds[tt][c], tf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[tt] += (double)__fmul_rn(tf[q], gf[q]);
+      }
+    }
+  }
+  const float bias = bf2f(gate_b[e]);
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const double a = wave_sum_f64(acc[tt]);
+    if (lane == 0 && tt < ntok) {
+      const float d = bf2f(f2bf((float)a));
+      logits[(size_t)(tok0 + tt) * E + e] = bf2f(f2bf(__fadd_rn(d, bias)));
+    }
+  }
+}
+
+// Ranking keys of bf16 logits: the order-preserving unsigned image of the
+// value in the high 16 bits, 0xFFFF - expert in the low 16, so that a larger
+// key means (value larger, or value equal and expert lower).  Logits are bf16
+// values (low 16 bits zero); -inf pads rank below every finite logit.
+__device__ __forceinline__ uint32_t rank_key(float v, int e) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (u & 0xFFFF0000u) | (uint32_t)(0xFFFF - e);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t hi = key & 0xFFFF0000u;
+  return __uint_as_float((hi & 0x80000000u) ? (hi ^ 0x80000000u) : (~hi & 0xFFFF0000u));
+}
+
+// Rank of one token's logits (LDS key row kr, padded to a multiple of 32),
+// one wave: lane e (and e + 64, ...) counts the keys above its own; the k
+// winners go to topi / topv (LDS) at their rank.
+__device__ __forceinline__ void rank_wave(const uint32_t* kr, int E, int k, int* topi,
+                                          float* topv) {
+  const int lane = threadIdx.x & 63;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const uint32_t key = kr[min(e, E - 1)];
+    int rank = 0;
+    for (int o0 = 0; o0 < E; o0 += 32) {
+      uint32_t ok[32];
+#pragma unroll
+      for (int o = 0; o < 32; ++o) ok[o] = kr[o0 + o];
+#pragma unroll
+      for (int o = 0; o < 32; ++o) rank += ok[o] > key ? 1 : 0;
+    }
+    if (e < E && rank < k) {
+      topi[rank] = e;
+      topv[rank] = key_value(key);
+    }
+  }
+}
+
+// Softmax of one token's k winners (model/mlp.py:382): fp64 exponentials
+// relative to the largest, summed in rank order, bf16 weights.  One thread.
+__device__ __forceinline__ void softmax_token(const float* topv, int k,
+                                              uint16_t* __restrict__ w) {
+  double ex[8], sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j < k) {
+      ex[j] = exp((double)topv[j] - (double)topv[0]);
+      sum = j == 0 ? ex[0] : sum + ex[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) w[j] = f2bf((float)(ex[j] / sum));
+}
+
+// Placement of pairs [p0, p1) of a stable counting sort by expert, given
+// base[e] (LDS) = the sorted position of the chunk's first pair of expert e.
+// Within a round of 1024 pairs a pair's rank among same-expert pairs comes
+// from ballots, so pairs keep flattened (token, slot) order inside each
+// expert, exactly as np.argsort(kind="stable").  Pairs whose expert id is out
+// of range are not placed (pair_pos = -1).  All 1024 threads call it.
+__device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, int k, int E,
+                                            int* base, int* wcnt,
+                                            int32_t* __restrict__ sorted_pairs,
+                                            int32_t* __restrict__ token_indices,
+                                            int32_t* __restrict__ expert_ids,
+                                            int32_t* __restrict__ pair_pos) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int round0 = 0; round0 < nk; round0 += 1024) {
+  for (int round0 = p0; round0 < p1; round0 += 1024) {
     const int p = round0 + tid;
-    const bool inb = p < nk;
+    const bool inb = p < p1;
     const int v = inb ? idx[p] : -1;
     const bool ok = inb && v >= 0 && v < E;
     for (int i = tid; i < 16 * E; i += 1024) wcnt[(i / E) * 256 + (i % E)] = 0;
@@ -465,58 +514,295 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
   }
 }
 
+// Exclusive prefix over experts of tot[e] (LDS), by wave 0: base[e] +=
+// prefix, and indptr (when given) = the prefix with indptr[E] = the total.
+__device__ __forceinline__ void expert_prefix(const int* tot, int E, int* base,
+                                              int32_t* __restrict__ indptr) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x >= 64) return;
+  int carry = 0;
+  for (int b = 0; b < E; b += 64) {
+    const int e = b + lane;
+    const int c = e < E ? tot[e] : 0;
+    int v = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, 64);
+      if (lane >= o) v += t;
+    }
+    if (e < E) {
+      base[e] += carry + v - c;
+      if (indptr) indptr[e] = carry + v - c;
+    }
+    carry += __shfl(v, 63, 64);
+  }
+  if (indptr && lane == 0) indptr[E] = carry;
+}
+
+// Ranking keys staged in LDS for the selection: 16 K keys (64 KB) per pass,
+// at most kSelTok tokens.
+constexpr int kSelLds = 16384;
+constexpr int kSelTok = 256;
+
+// Top-k + softmax of the tokens [t0, t0 + nt), in passes of up to
+// kSelLds / Ep tokens: the rows' ranking keys are staged in LDS (stride Ep,
+// padded with -inf); one wave ranks each token; then one thread per token
+// takes the softmax and writes slot j of idx and w.  ti (when given) receives
+// the indices at [t - t0][k]; expert counts go to hist (LDS).
+__device__ __forceinline__ void select_range(const float* __restrict__ logits, int t0, int nt,
+                                             int E, int k, uint32_t* keys, int* topi,
+                                             float* topv, int32_t* __restrict__ idx_out,
+                                             uint16_t* __restrict__ w_out, int* ti, int* hist) {
+  const int nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int Ep = (E + 31) & ~31;
+  const int per = min(kSelLds / Ep, kSelTok);
+  for (int b0 = 0; b0 < nt; b0 += per) {
+    const int nbt = min(per, nt - b0);
+    const float* src = logits + (size_t)(t0 + b0) * E;
+    __syncthreads();  // the previous pass's rows are no longer read
+    for (int i = threadIdx.x; i < nbt * Ep; i += blockDim.x) {
+      const int r = i / Ep, c = i - r * Ep;
+      keys[i] = rank_key(c < E ? src[r * E + c] : -INFINITY, c);
+    }
+    __syncthreads();
+    for (int r = wave; r < nbt; r += nw) rank_wave(keys + r * Ep, E, k, topi + r * 8, topv + r * 8);
+    __syncthreads();
+    for (int r = threadIdx.x; r < nbt; r += blockDim.x) {
+      const int t = t0 + b0 + r;
+      softmax_token(topv + r * 8, k, w_out + (size_t)t * k);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < k) {
+          const int e = topi[r * 8 + j];
+          idx_out[(size_t)t * k + j] = e;
+          if (ti) ti[(b0 + r) * k + j] = e;
+          atomicAdd(&hist[e], 1);
+        }
+      }
+    }
+  }
+}
+
+// Top-k + softmax of n <= 128 tokens and the grouping of their n*k pairs,
+// one workgroup (mlc-llm gating_softmax_topk + moe_cumsum / get_indices /
+// get_indptr, model/mlp_optimized.py:118-148).
+__global__ __launch_bounds__(1024) void moe_select_permute_kernel(
+    const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out, int32_t* __restrict__ indptr,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
+  __shared__ uint32_t keys[kSelLds];
+  __shared__ int topi[kSelTok * 8];
+  __shared__ float topv[kSelTok * 8];
+  __shared__ int idx_lds[4096];
+  __shared__ int cnt[256];
+  __shared__ int base[256];
+  __shared__ int wcnt[16 * 256];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) {
+    cnt[e] = 0;
+    base[e] = 0;
+  }
+  select_range(logits, 0, n, E, k, keys, topi, topv, idx_out, w_out, idx_lds, cnt);
+  __syncthreads();
+  expert_prefix(cnt, E, base, indptr);
+  __syncthreads();
+  place_pairs(idx_lds, 0, n * k, k, E, base, wcnt, sorted_pairs, token_indices, expert_ids,
+              pair_pos);
+}
+
+// Tokens per chunk of the large-n grouping.
+constexpr int kSelChunk = 64;
+
+// Large n, first pass: top-k + softmax of the kSelChunk tokens of chunk
+// blockIdx.x and the chunk's expert histogram, counts[chunk][E].
+__global__ __launch_bounds__(1024) void moe_select_count_kernel(
+    const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out, int32_t* __restrict__ counts) {
+  __shared__ uint32_t keys[kSelLds];
+  __shared__ int topi[kSelChunk * 8];
+  __shared__ float topv[kSelChunk * 8];
+  __shared__ int h[256];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) h[e] = 0;
+  const int t0 = blockIdx.x * kSelChunk;
+  select_range(logits, t0, min(kSelChunk, n - t0), E, k, keys, topi, topv, idx_out, w_out,
+               nullptr, h);
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) counts[(size_t)blockIdx.x * E + e] = h[e];
+}
+
+// Large n, second pass: workgroup c places the pairs of chunk c (kSelChunk
+// tokens' pairs).  Its base for expert e is the prefix over experts of the totals plus
+// the counts of expert e in the chunks before c; chunk 0 writes indptr.
+__global__ __launch_bounds__(1024) void moe_place_kernel(
+    const int32_t* __restrict__ idx, const int32_t* __restrict__ counts, int nchunks, int nk,
+    int k, int E, int32_t* __restrict__ indptr, int32_t* __restrict__ sorted_pairs,
+    int32_t* __restrict__ token_indices, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ pair_pos) {
+  __shared__ int tot[256];
+  __shared__ int base[256];
+  __shared__ int wcnt[16 * 256];  // first holds the partial sums below
+  const int tid = threadIdx.x, c = blockIdx.x;
+  // thread (part, e) sums chunks j = part, part + parts, ... of expert e
+  // (all of them, and those before c); the parts are then added in order
+  const int parts = 1024 / E;
+  {
+    const int e = tid % E, part = tid / E;
+    int s = 0, before = 0;
+    if (part < parts) {
+      for (int j = part; j < nchunks; j += parts) {
+        const int v = counts[(size_t)j * E + e];
+        s += v;
+        before += j < c ? v : 0;
+      }
+      wcnt[part * E + e] = s;
+      wcnt[2048 + part * E + e] = before;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    int s = 0, before = 0;
+    for (int part = 0; part < parts; ++part) {
+      s += wcnt[part * E + e];
+      before += wcnt[2048 + part * E + e];
+    }
+    tot[e] = s;
+    base[e] = before;
+  }
+  __syncthreads();
+  expert_prefix(tot, E, base, c == 0 ? indptr : nullptr);
+  __syncthreads();
+  const int p0 = c * kSelChunk * k;
+  place_pairs(idx, p0, min(nk, p0 + kSelChunk * k), k, E, base, wcnt, sorted_pairs,
+              token_indices, expert_ids, pair_pos);
+}
+
+// Stable counting sort of the n*k (token, slot) pairs by expert, one
+// workgroup.  Totals come from LDS atomics (order-free); placement follows
+// place_pairs.
+__global__ __launch_bounds__(1024) void moe_permute_kernel(
+    const int32_t* __restrict__ idx, int nk, int k, int E, int32_t* __restrict__ indptr,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
+  __shared__ int cnt[256];
+  __shared__ int base[256];
+  __shared__ int wcnt[16 * 256];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) {
+    cnt[e] = 0;
+    base[e] = 0;
+  }
+  __syncthreads();
+  for (int p = tid; p < nk; p += 1024) {
+    const int v = idx[p];
+    if (v >= 0 && v < E) atomicAdd(&cnt[v], 1);
+  }
+  __syncthreads();
+  expert_prefix(cnt, E, base, indptr);
+  __syncthreads();
+  place_pairs(idx, 0, nk, k, E, base, wcnt, sorted_pairs, token_indices, expert_ids, pair_pos);
+}
+
 }  // namespace moe
 
 // t_pieces (optional, H % 32 == 0): the two fp8 pieces of t, packed as
-// moe_launch_pieces writes them.  Returns kErrUnsupported when the fused form
-// does not apply (n > kDecodeMax or H > 4096 with pieces requested).
+// moe_launch_pieces writes them.  Up to 256 tokens run one per workgroup of
+// four waves; beyond, two tokens share a workgroup, so each gate row read
+// from L2 serves two tokens.
 extern "C" int moe_launch_router_pieces(const void* x, const void* norm_w, const void* gate_w,
                                         const void* gate_b, int n, int H, int E, int k, float eps,
                                         void* t_out, void* idx_out, void* w_out, void* pq,
                                         void* pqs, hipStream_t stream) {
   if (n == 0) return moe::kOk;
-  if (n > 512 || H > 4096 || (pq && H % 32)) return moe::kErrUnsupported;
+  if (H > 4096 || H % 8 || E > 256 || k > 8 || (pq && H % 32)) return moe::kErrUnsupported;
   const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
                  *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
-  const dim3 block(64 * moe::kDecWaves);
   uint16_t* pt = (uint16_t*)t_out;
   int32_t* pi = (int32_t*)idx_out;
   uint16_t* pw = (uint16_t*)w_out;
   uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
-#define MOE_DEC(PC, S)                                                                          \
-  hipLaunchKernelGGL((moe::moe_router_decode_kernel<PC, S>), dim3(n), block, 0, stream, px, pn, \
-                     pg, pb, H, E, k, eps, pt, pi, pw, q, qs)
-  if (H <= 64 * 6 * 8) {
-    if (pq) MOE_DEC(true, 6); else MOE_DEC(false, 6);
+#define MOE_RT(PC, S, W, TT, KE)                                                             \
+  hipLaunchKernelGGL((moe::moe_router_kernel<PC, S, W, TT, KE>), dim3((n + TT - 1) / TT),   \
+                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, k, eps, pt, pi, pw, q, qs)
+#define MOE_RT_S(PC, W, TT, KE)                 \
+  if (H <= 64 * 6 * 8) MOE_RT(PC, 6, W, TT, KE); \
+  else MOE_RT(PC, 8, W, TT, KE)
+  if (n <= 256) {
+    if (pq) { MOE_RT_S(true, 4, 1, 4); } else { MOE_RT_S(false, 4, 1, 4); }
   } else {
-    if (pq) MOE_DEC(true, 8); else MOE_DEC(false, 8);
+    if (pq) { MOE_RT_S(true, 4, 2, 4); } else { MOE_RT_S(false, 4, 2, 4); }
   }
-#undef MOE_DEC
+#undef MOE_RT_S
+#undef MOE_RT
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }
 
 extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* gate_w,
                                  const void* gate_b, int n, int H, int E, int k, float eps,
                                  void* t_out, void* idx_out, void* w_out, hipStream_t stream) {
+  return moe_launch_router_pieces(x, norm_w, gate_w, gate_b, n, H, E, k, eps, t_out, idx_out,
+                                  w_out, nullptr, nullptr, stream);
+}
+
+// Logits of the n tokens into logits[n][E] (fp32 holding bf16 values), t,
+// and (pq != null, H % 32 == 0) the two fp8 pieces of t.  Eight experts per
+// workgroup; TT tokens per workgroup share each gate row read.
+extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
+                                        const void* gate_b, int n, int H, int E, float eps,
+                                        void* t_out, float* logits, void* pq, void* pqs,
+                                        hipStream_t stream) {
   if (n == 0) return moe::kOk;
-  if (n <= 512)
-    return moe_launch_router_pieces(x, norm_w, gate_w, gate_b, n, H, E, k, eps, t_out, idx_out,
-                                    w_out, nullptr, nullptr, stream);
+  if (H > 4096 || H % 8 || E > 256 || (pq && H % 32)) return moe::kErrUnsupported;
   const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
                  *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
-  uint16_t *pt = (uint16_t*)t_out, *pw = (uint16_t*)w_out;
-  int32_t* pi = (int32_t*)idx_out;
-  // One token per workgroup while that fills the chip; four once the gate
-  // matrix re-reads (one per workgroup) start to cost more than latency.
-  constexpr int NT = moe::kRouterThreads;
-  if (n <= 512) {
-    const size_t lds = (size_t)1 * H * 2 + NT * 1 * 8 + (size_t)1 * E * 4;
-    hipLaunchKernelGGL(moe::moe_router_kernel<1>, dim3(n), dim3(NT), lds, stream, px, pn, pg, pb,
-                       n, H, E, k, eps, pt, pi, pw);
+  uint16_t* pt = (uint16_t*)t_out;
+  uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
+  constexpr int W = 8;
+  const int ey = (E + W - 1) / W;
+#define MOE_LG(PC, S, TT)                                                                        \
+  hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT>), dim3((n + TT - 1) / TT, ey), \
+                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs)
+#define MOE_LG_TT(PC, S, TTBIG)              \
+  if (n <= 128) MOE_LG(PC, S, 1);            \
+  else if (n <= 1024) MOE_LG(PC, S, 4);      \
+  else MOE_LG(PC, S, TTBIG)
+  if (H <= 64 * 6 * 8) {
+    if (pq) { MOE_LG_TT(true, 6, 8); } else { MOE_LG_TT(false, 6, 8); }
   } else {
-    const size_t lds = (size_t)4 * H * 2 + NT * 4 * 8 + (size_t)4 * E * 4;
-    hipLaunchKernelGGL(moe::moe_router_kernel<4>, dim3((n + 3) / 4), dim3(NT), lds, stream, px, pn,
-                       pg, pb, n, H, E, k, eps, pt, pi, pw);
+    if (pq) { MOE_LG_TT(true, 8, 4); } else { MOE_LG_TT(false, 8, 4); }
+  }
+#undef MOE_LG_TT
+#undef MOE_LG
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}
+
+// Chunks of tokens whose expert counts the large-n grouping keeps.
+extern "C" int moe_select_chunks(int n) { return (n + moe::kSelChunk - 1) / moe::kSelChunk; }
+
+// Top-k + softmax of the logits, then the grouping of the pairs: one
+// workgroup for n <= 128, otherwise a select/count pass over chunks of
+// kSelChunk tokens (counts[chunks][E]) and a placement pass.
+extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out,
+                                       void* w_out, void* counts, void* indptr,
+                                       void* sorted_pairs, void* token_indices,
+                                       void* expert_ids, void* pair_pos, hipStream_t stream) {
+  if (E > 256 || k > 8 || k < 1) return moe::kErrUnsupported;
+  int32_t* pi = (int32_t*)idx_out;
+  uint16_t* pw = (uint16_t*)w_out;
+  int32_t *ip = (int32_t*)indptr, *sp = (int32_t*)sorted_pairs, *ti = (int32_t*)token_indices,
+          *ei = (int32_t*)expert_ids, *pp = (int32_t*)pair_pos;
+  if (n <= 128) {
+    hipLaunchKernelGGL(moe::moe_select_permute_kernel, dim3(1), dim3(1024), 0, stream, logits, n,
+                       E, k, pi, pw, ip, sp, ti, ei, pp);
+  } else {
+    const int nch = moe_select_chunks(n);
+    int32_t* cnt = (int32_t*)counts;
+    hipLaunchKernelGGL(moe::moe_select_count_kernel, dim3(nch), dim3(1024), 0, stream, logits,
+                       n, E, k, pi, pw, cnt);
+    hipLaunchKernelGGL(moe::moe_place_kernel, dim3(nch), dim3(1024), 0, stream, pi, cnt, nch,
+                       n * k, k, E, ip, sp, ti, ei, pp);
   }
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }

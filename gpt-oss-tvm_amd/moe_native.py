@@ -280,7 +280,7 @@ def workspace_bytes(n, E, k, H, inter) -> int:
 
 
 def workspace_layout(n, E, k, H, inter) -> list[int]:
-    offs = (_SZ * 12)()
+    offs = (_SZ * 14)()
     _check(_lib.moe_workspace_layout(n, E, k, H, inter, offs), "moe_workspace_layout")
     return list(offs)
 

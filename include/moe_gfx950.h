@@ -196,9 +196,10 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
 
 /* Byte offsets of the intermediates inside the block workspace, in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
- * t_pieces, act, act_pieces, y. */
+ * t_pieces, act, act_pieces, y, logits (fp32 [n, E], bf16 values), counts
+ * (int32 [ceil(n / 64), E], expert histogram per 64-token chunk). */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                                 size_t offsets[12]);
+                                 size_t offsets[14]);
 
 MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                       const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,

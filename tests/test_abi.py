@@ -113,6 +113,7 @@ def test_workspace_layout(native):
     n, E, k, H, I = 64, 32, 4, 2880, 2880
     total = native.workspace_bytes(n, E, k, H, I)
     offs = native.workspace_layout(n, E, k, H, I)
-    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
-    assert offs[-1] + n * k * H * 4 <= total
+    assert len(offs) == 14 and offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert offs[11] + n * k * H * 4 <= offs[12]             # y before logits
+    assert offs[13] + (n + 63) // 64 * E * 4 <= total       # counts last
     assert native.workspace_bytes(n, E, k, H + 1, I) == 0

@@ -16,6 +16,7 @@ torch = pytest.importorskip("torch")
 from oracle import moe_oracle as O  # noqa: E402
 from gpu_util import (bf16_dev, f32_dev, host, host_bf16, i32_dev, make_block, norm_rel,  # noqa: E402
                       params_from_npz, u8_dev)
+import pieces_model as PM  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -72,7 +73,8 @@ def test_dequant_fused_path_exact_in_range(native):
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("E,H,n,seed", [(32, 2880, 64, 1), (32, 2880, 1, 2), (32, 2880, 1000, 3),
-                                        (128, 2880, 300, 4), (8, 128, 7, 5), (256, 64, 33, 6)])
+                                        (128, 2880, 300, 4), (8, 128, 7, 5), (256, 64, 33, 6),
+                                        (32, 2880, 257, 9), (128, 4096, 5, 10)])
 def test_router_bit_exact(native, E, H, n, seed):
     p = O.make_params(seed, num_experts=E, hidden=H, inter=64)
     x = O.make_input(seed + 100, n, hidden=H)
@@ -173,6 +175,39 @@ def test_many_tokens_per_expert(native):
     assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
 
 
+@pytest.mark.parametrize("E,H,I,n,seed", [(8, 128, 64, 2000, 31), (32, 256, 64, 1030, 32),
+                                          (128, 128, 64, 700, 33), (32, 2880, 64, 64, 34),
+                                          (32, 2880, 64, 1, 35), (12, 192, 64, 257, 36)])
+def test_block_internal_routing(native, E, H, I, n, seed):
+    """The block's own router and grouping (logits kernel, then one workgroup of
+    top-k + grouping for n k <= 4096, or the chunked two-pass grouping above):
+    t, indices, weights and every grouping array bit-exact, output in tolerance."""
+    p = O.make_params(seed, num_experts=E, hidden=H, inter=I)
+    x = O.make_input(seed + 100, n, hidden=H)
+    tr = O.block_forward(x, p)
+    blk = make_block(p)
+    out = host_bf16(blk(bf16_dev(x).view(1, n, H)).view(n, H))
+    torch.cuda.synchronize()
+    ws = blk._workspace(n, torch.device("cuda:0"))
+    offs = native.workspace_layout(n, E, 4, H, I)
+    nk = n * 4
+
+    def region(i, dtype, count):
+        return ws[offs[i]: offs[i] + count * torch.tensor([], dtype=dtype).element_size()].view(dtype)
+
+    assert np.array_equal(host_bf16(region(0, torch.bfloat16, n * H)).reshape(n, H), tr.t)
+    assert np.array_equal(host(region(1, torch.int32, nk)).reshape(n, 4), tr.idx), \
+        f"ties at tokens {np.flatnonzero(O.tie_tokens(tr.g, 4))}"
+    assert np.array_equal(host_bf16(region(2, torch.bfloat16, nk)).reshape(n, 4), tr.w)
+    perm = O.permute(tr.idx, E)
+    assert np.array_equal(host(region(3, torch.int32, E + 1)), perm.indptr)
+    for i, ref in ((4, perm.sorted_pairs), (5, perm.token_indices), (6, perm.expert_ids),
+                   (7, perm.pair_pos)):
+        assert np.array_equal(host(region(i, torch.int32, nk)), ref), i
+    m = O.compare_outputs(out, tr.out)
+    assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
+
+
 # ---------------------------------------------------------------------------
 # fp8 pieces of the activations (the scaled-MFMA operand), bit-exact
 # ---------------------------------------------------------------------------
@@ -181,7 +216,6 @@ def test_many_tokens_per_expert(native):
                                                (5, 96, 2, False), (7, 160, 4, True),
                                                (3, 3072, 4, False), (1, 32, 2, True)])
 def test_quantize_pieces_bit_exact(native, rows, K, pieces, f32):
-    import pieces_model as PM
     rng = np.random.default_rng(rows * K + pieces)
     x = (rng.standard_normal((rows, K)) * np.exp(2 * rng.standard_normal((rows, K)))).astype(np.float32)
     x[0, :32] = 0.0                         # all-zero block
@@ -256,10 +290,11 @@ def test_block_20b_shape(native, block20b, n, seed):
     print(f"20B n={n}: {m}")
 
 
-def test_block_router_pieces_fused(native, block20b):
+@pytest.mark.parametrize("n", [64, 301])
+def test_block_router_pieces_fused(native, block20b, n):
     """The block's fused router writes the same t pieces as moe_quantize_pieces(t)."""
     p, blk = block20b
-    n, H = 64, 2880
+    H = 2880
     x = bf16_dev(O.make_input(15, n)).view(1, n, H)
     blk(x)
     torch.cuda.synchronize()
@@ -268,9 +303,10 @@ def test_block_router_pieces_fused(native, block20b):
     t = ws[offs[0]: offs[0] + n * H * 2].view(torch.bfloat16).view(n, H)
     assert np.array_equal(host_bf16(t), O.rms_norm(O.make_input(15, n), p.norm_w))
     nb = native.pieces_bytes(n, H, 2)
-    fused = host(ws[offs[8]: offs[8] + nb])
-    ref = host(native.quantize_pieces(t.contiguous(), 2))
-    assert np.array_equal(fused, ref), np.argwhere(fused != ref)[:4]
+    fused = PM.unpack(host(ws[offs[8]: offs[8] + nb]), n, H, 2)
+    ref = PM.unpack(host(native.quantize_pieces(t.contiguous(), 2)), n, H, 2)
+    for a, b in zip(fused, ref):  # codes, then scale runs (the alignment pad is not written)
+        assert np.array_equal(a, b), np.argwhere(a != b)[:4]
 
 
 def test_block_120b_shape(native):
