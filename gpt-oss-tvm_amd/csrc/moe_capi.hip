@@ -34,6 +34,11 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
                        const void* blocks, const void* scales, const void* bias, int E, int N,
                        int K, int max_tokens, int rows_active, int swiglu, float alpha,
                        float limit, void* out, int out_ld, hipStream_t stream);
+int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* indptr,
+                       const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
+                       const void* blocks, const void* scales, const void* bias, int E, int N,
+                       int K, int rows_active, int swiglu, float alpha, float limit, void* out,
+                       int out_ld, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -58,6 +63,30 @@ int check_dims(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I) {
 }
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Expert matmul dispatch (model/mlp_optimized.py:94-107 picks prefill or
+// decode kernels by token count): the tiled GEMM once the experts average
+// kGemmMinTokens or more tokens (each weight tile then serves many tokens),
+// the grouped GEMV below that or when N is not a multiple of its tile.
+constexpr int64_t kGemmMinTokens = 48;
+
+int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indptr,
+                  const int32_t* sorted_pairs, int k_top, int arow_mode, int orow_mode,
+                  const void* blocks, const void* scales, const void* bias, int E, int N, int K,
+                  int max_tokens, int pairs, int swiglu, float alpha, float limit, void* out,
+                  int out_ld, hipStream_t s) {
+  // the GEMM stores 16-byte row pieces and loads the bias 16 bytes at a time
+  if ((int64_t)pairs >= kGemmMinTokens * E && ((uintptr_t)out & 15u) == 0 && out_ld % 4 == 0 &&
+      ((uintptr_t)bias & 15u) == 0) {
+    const int rc = moe_launch_mx_gemm(packed, rows, pieces, indptr, sorted_pairs, k_top,
+                                      arow_mode, orow_mode, blocks, scales, bias, E, N, K, pairs,
+                                      swiglu, alpha, limit, out, out_ld, s);
+    if (rc != MOE_ERR_UNSUPPORTED) return rc;
+  }
+  return moe_launch_mx_gemv(packed, rows, pieces, indptr, sorted_pairs, k_top, arow_mode,
+                            orow_mode, blocks, scales, bias, E, N, K, max_tokens, pairs, swiglu,
+                            alpha, limit, out, out_ld, s);
+}
 
 constexpr int kNumRegions = 14;
 constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
@@ -203,9 +232,9 @@ int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indic
   const int rows = x_is_3d_f32 ? (int)nk : (int)n;
   const int pieces = x_is_3d_f32 ? kPiecesAct : kPiecesT;
   if ((rc = moe_launch_pieces(x, x_is_3d_f32, rows, (int)K, pieces, packed, s))) return rc;
-  return moe_launch_mx_gemv(packed, rows, pieces, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0, 0,
-                            blocks, scales, bias, (int)E, (int)N, (int)K, (int)nk, (int)nk, 0,
-                            0.f, 0.f, out, (int)N, s);
+  return expert_matmul(packed, rows, pieces, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0, 0, blocks,
+                       scales, bias, (int)E, (int)N, (int)K, (int)nk, (int)nk, 0, 0.f, 0.f, out,
+                       (int)N, s);
 }
 
 size_t moe_pieces_bytes(int64_t rows, int64_t K, int pieces) {
@@ -234,9 +263,9 @@ int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr, const int32_t* 
   if (!t_pieces || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act)
     return MOE_ERR_NULL;
   if (!aligned16(t_pieces) || !aligned16(blocks) || ((uintptr_t)act & 3u)) return MOE_ERR_ALIGN;
-  return moe_launch_mx_gemv(t_pieces, (int)n, kPiecesT, indptr, sorted_pairs, (int)k, 0, 1, blocks,
-                            scales, bias, (int)E, (int)(2 * I), (int)H, (int)(n * k), (int)(n * k),
-                            1, alpha, limit, act, (int)I, as_stream(stream));
+  return expert_matmul(t_pieces, (int)n, kPiecesT, indptr, sorted_pairs, (int)k, 0, 1, blocks,
+                       scales, bias, (int)E, (int)(2 * I), (int)H, (int)(n * k), (int)(n * k), 1,
+                       alpha, limit, act, (int)I, as_stream(stream));
 }
 
 int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
@@ -248,9 +277,9 @@ int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorte
   if (!act_pieces || !indptr || !sorted_pairs || !blocks || !scales || !bias || !y)
     return MOE_ERR_NULL;
   if (!aligned16(act_pieces) || !aligned16(blocks) || ((uintptr_t)y & 3u)) return MOE_ERR_ALIGN;
-  return moe_launch_mx_gemv(act_pieces, (int)(n * k), kPiecesAct, indptr, sorted_pairs, (int)k, 2,
-                            0, blocks, scales, bias, (int)E, (int)H, (int)I, (int)(n * k),
-                            (int)(n * k), 0, 0.f, 0.f, y, (int)H, as_stream(stream));
+  return expert_matmul(act_pieces, (int)(n * k), kPiecesAct, indptr, sorted_pairs, (int)k, 2, 0,
+                       blocks, scales, bias, (int)E, (int)H, (int)I, (int)(n * k), (int)(n * k), 0,
+                       0.f, 0.f, y, (int)H, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -335,14 +364,14 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
                                     ei, pp, s)))
     return rc;
-  if ((rc = moe_launch_mx_gemv(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
-                               mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1,
-                               alpha, limit, act, (int)I, s)))
+  if ((rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+                          mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1, alpha,
+                          limit, act, (int)I, s)))
     return rc;
   if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
-  if ((rc = moe_launch_mx_gemv(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
-                               mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f,
-                               0.f, y, (int)H, s)))
+  if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                          mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f, y,
+                          (int)H, s)))
     return rc;
   return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
 }

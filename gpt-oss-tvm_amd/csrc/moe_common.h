@@ -29,6 +29,16 @@ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint
 // fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
+// fp64 -> fp32 (RNE) -> bf16 (RNE): two roundings, as an fp32 result stored
+// to bf16.  The opaque fp32 step keeps the compiler from folding the pair
+// into one fp64 -> bf16 conversion, which rounds differently when the fp32
+// value lands on a bf16 tie.
+__device__ __forceinline__ uint16_t f64_to_bf16_via_f32(double v) {
+  float f = (float)v;
+  asm volatile("" : "+v"(f));
+  return f2bf(f);
+}
+
 // E8M0 byte -> fp32 2^(s-127); s = 0 is the fp32 subnormal 2^-127 and s = 255
 // is +inf, as exp2(float(s - 127)) gives (model/mlp.py:297-298).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {

@@ -1,0 +1,504 @@
+// Grouped expert GEMM for many tokens per expert (prefill), on the same
+// block-scaled instruction as the GEMV (v_mfma_scale_f32_16x16x128_f8f6f4):
+// fp8 activation pieces (A) times MXFP4 weights as stored (B), fp32 out.
+//
+// Reference operators: mxfp4_moe_mlp1_prefill / mxfp4_moe_mlp2_prefill
+// (model/mlp_optimized.py:214-460) with the fp32 semantics of
+// model/mlp.py:387-395 (einsum + bias, interleaved clamped SwiGLU on mlp1).
+//
+// Tiles.  A work unit is one (expert, token tile, column tile): 192 A rows
+// (192 / P tokens, P pieces each) against 192 weight rows over the whole K.
+// Eight waves split it 4 x 2: each wave owns 48 A rows x 96 columns, i.e.
+// 3 x 6 MFMA tiles of 16 x 16, and keeps their 18 accumulators for all of K.
+//
+// Staging.  The unit's scale bytes (A: 112 per row, B: G per column) are
+// staged once.  Per 128-wide K chunk a stage holds the tile's A codes
+// (192 x 128 bytes) and B codes (192 x 64).  Both come by direct
+// global-to-LDS loads (no registers), 16 bytes per lane; three code stages
+// form a ring, so while chunk c is multiplied the loads of chunks c + 1 and
+// c + 2 are in flight.  A wave's loads complete in issue order, so "chunk c
+// has landed" is vmcnt <= (its loads per chunk) on each wave plus a barrier.
+// A and B code rows are stored with their 16-byte parts XOR-swizzled so that
+// the MFMA operand reads of 16 lanes hit distinct LDS banks.
+//
+// Operand layout per K chunk c (lane l = 16 g + r), as in the GEMV:
+//   A  row r: bytes 0..15 -> k = 16 g + 0..15, bytes 16..31 -> k = 64 + 16 g + 0..15
+//   B  column r: MX block 4 c + g of that weight row (low nibble first)
+//   scales: lane (r, g) gives the E8M0 of block 4 c + g of its row / column
+//   D  column r, elements i = 0..3 -> A rows 4 g + i
+// A token's P piece rows share one lane's four accumulator rows, so the
+// pieces are summed in registers in the epilogue, as the GEMV does.
+#include <type_traits>
+
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int kGmRows = 192;                       // A rows per tile
+constexpr int kGmCols = 192;                       // weight rows (output columns) per tile
+constexpr int kGmWaves = 8;                        // 4 (A rows) x 2 (columns)
+constexpr int kGmThreads = 64 * kGmWaves;
+constexpr int kGmStages = 3;
+constexpr int kGmAInst = kGmRows * 8 / 64;         // 24 A-code loads per chunk (3 per wave)
+constexpr int kGmBInst = kGmCols * 4 / 64;         // 12 B-code loads per chunk
+constexpr int kGmAo = 0;                           // in a stage: A codes, then B codes
+constexpr int kGmBo = kGmRows * 128;
+constexpr int kGmStage = kGmBo + kGmCols * 64;     // 36864 bytes
+constexpr int kGmSclRow = 112;                     // scale bytes per piece row (4 runs of 28)
+constexpr int kGmMaxG = 96;                        // K <= 3072
+constexpr int kGmASc = kGmStages * kGmStage;       // A scales of the unit [rows][112]
+constexpr int kGmBSc = kGmASc + kGmRows * kGmSclRow;  // B scales of the unit [cols][G]
+constexpr int kGmBScBytes = kGmCols * kGmMaxG;     // 192 G, G <= 96, in whole 1 KB loads
+constexpr int kGmBias = kGmBSc + kGmBScBytes;      // bias of the unit's columns (bf16)
+constexpr int kGmFixedLds = kGmBias + 1024;        // 152064 bytes
+constexpr int kGmCUs = 256;                        // MI355X
+constexpr int kGmXcds = 8;                         // 8 XCDs of 32 CUs, one L2 each
+
+// dynamic part: unit prefix and indptr, E + 1 ints each
+__host__ __device__ constexpr int gm_lds_bytes(int E) { return 2 * (E + 1) * 4; }
+static_assert(kGmFixedLds + gm_lds_bytes(256) <= 160 * 1024, "LDS");
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int S, int E, class F>
+__device__ __forceinline__ void gm_static_for(F&& f) {
+  if constexpr (S < E) {
+    f(std::integral_constant<int, S>{});
+    gm_static_for<S + 1, E>(f);
+  }
+}
+
+// s_waitcnt with only the vector-memory count: vmcnt(n), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// LDS reads of the staged operands, issued as inline asm: the compiler does
+// not count them against the direct loads in flight (it would otherwise wait
+// for all of those before any LDS read).  Their results pass through
+// lgkm_wait, whose operand ties keep every use after the wait.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_b128(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_u8(uint32_t a) {
+  uint32_t v;
+  asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int P, int kEpi>
+__global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
+    const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
+    int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
+    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
+    float alpha, float limit, float* __restrict__ out, int out_ld, int xcds) {
+  __shared__ __align__(16) uint8_t ring[kGmFixedLds];
+  extern __shared__ __align__(16) uint8_t lds[];  // unit prefix
+  constexpr int TPT = kGmRows / P;  // tokens per tile
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 3, wn = wave >> 2;
+  const int r = lane & 15, g = lane >> 4;
+  const int NT = N / kGmCols;
+  const int NC = Kp >> 7;
+  // B-code loads per chunk: instruction k < 12 belongs to wave k % 8
+  const bool two_b = wave < kGmBInst - kGmWaves;
+  // Per-lane LDS read bases of each stage; the operand index goes into the
+  // instructions' immediate offsets.  Lane (r, g): B column 96 wn + 16 b + r
+  // (part g, swizzled by (column >> 1) & 3 = (r >> 1) & 3); A row
+  // 48 wm + 16 f + r (parts g and g + 4, swizzled by row & 7 = r & 7).
+  const uint32_t rbase = lds_addr(ring);
+  uint32_t vb[kGmStages], va0[kGmStages], va1[kGmStages];
+#pragma unroll
+  for (int S = 0; S < kGmStages; ++S) {
+    const uint32_t st = rbase + S * kGmStage;
+    vb[S] = st + kGmBo + (96 * wn + r) * 64 + ((g ^ ((r >> 1) & 3)) << 4);
+    va0[S] = st + kGmAo + (48 * wm + r) * 128 + ((g ^ (r & 7)) << 4);
+    va1[S] = st + kGmAo + (48 * wm + r) * 128 + (((g + 4) ^ (r & 7)) << 4);
+  }
+  // scale bytes: A row 48 wm + 16 f + r, run g; B column 96 wn + 16 b + r
+  const uint32_t vas = rbase + kGmASc + (48 * wm + r) * kGmSclRow + g * 28;
+  const uint32_t vbs = rbase + kGmBSc + (96 * wn + r) * G;
+  int* const pre = (int*)lds;
+  int* const ipl = pre + (E + 1);  // indptr, read once
+
+  // Exclusive prefix of the unit counts: ceil(cnt_e / TPT) * NT.
+  if (wave == 0) {
+    int carry = 0;
+    if (lane == 0) pre[0] = 0;
+    for (int i = lane; i <= E; i += 64) ipl[i] = indptr[i];
+    for (int b = 0; b < E; b += 64) {
+      const int i = b + lane;
+      int v = 0;
+      if (i < E) v = (indptr[i + 1] - indptr[i] + TPT - 1) / TPT * NT;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, kWave);
+        if (lane >= o) v += t;
+      }
+      if (i < E) pre[i + 1] = carry + v;
+      carry += __shfl(v, 63, kWave);
+    }
+  }
+  __syncthreads();
+  const int total = pre[E];
+  // Units go round-robin over the workgroups in XCD-major numbering: at each
+  // step the workgroups of one XCD take consecutive units, the column tiles
+  // of one token tile, so that tile's A rows are fetched into that XCD's L2
+  // once and read from there by all of them.
+  const int vwg = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
+                                 (int)(blockIdx.x / xcds)
+                           : (int)blockIdx.x;
+  auto expert_of = [&](int u) {  // largest e with pre[e] <= u
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= u) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+
+  for (int u = vwg; u < total; u += gridDim.x) {
+    const int e = expert_of(u);
+    const int off = u - pre[e];
+    const int mt = off / NT, nt = off - mt * NT;
+    const int start = ipl[e];
+    const int m0 = mt * TPT;
+    const int ntok = min(TPT, ipl[e + 1] - start - m0);
+    const int n0 = nt * kGmCols;
+    auto src_row = [&](int tt) {  // activation row of token tt of this tile
+      const int j = start + m0 + tt;
+      return arow_mode == 0 ? sorted_pairs[j] / k_top : arow_mode == 1 ? sorted_pairs[j] : j;
+    };
+    // Rows past the tile's tokens load token 0's row: their MFMA rows are
+    // computed and never stored (a D row depends on its A row only).
+    auto piece_row = [&](int R) {  // packed-pieces row of tile A row R
+      const int tt = R / P, p = R - tt * P;
+      return (uint32_t)(src_row(tt < ntok ? tt : 0) * P + p);
+    };
+
+    // The unit's scales, 16 bytes per lane: A rows (7 loads of 16 per row;
+    // loads past the last row repeat it), then the B columns' G bytes each
+    // (192 G contiguous checkpoint bytes; the tail repeats the last 16).
+    {
+      constexpr int kAU = kGmRows * 7;                        // 1344 A-scale loads
+      const int nbu = kGmCols * G / 16;                       // B-scale loads
+      for (int i0 = 64 * wave; i0 < kAU; i0 += kGmThreads) {
+        const int uu = min(i0 + lane, kAU - 1), R = uu / 7;
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(qs + piece_row(R) * kGmSclRow + (uu - R * 7) * 16),
+            (lds_ptr_t)(ring + kGmASc + i0 * 16), 16, 0, 0);
+      }
+      const uint8_t* bsrc = scales + ((size_t)e * N + n0) * G;
+      for (int i0 = 64 * wave; i0 < nbu; i0 += kGmThreads)
+        __builtin_amdgcn_global_load_lds((const void*)(bsrc + min(i0 + lane, nbu - 1) * 16),
+                                         (lds_ptr_t)(ring + kGmBSc + i0 * 16), 16, 0, 0);
+      // the columns' bias: 384 bytes, 24 loads of 16 (the rest repeat the last)
+      if (wave == kGmWaves - 1)
+        __builtin_amdgcn_global_load_lds(
+            (const void*)((const uint8_t*)(bias + (size_t)e * N + n0) + min(lane, 23) * 16),
+            (lds_ptr_t)(ring + kGmBias), 16, 0, 0);
+    }
+
+    // This wave's code loads of a chunk (lane l), 32-bit offsets from q and
+    // blocks (the launcher checks the ranges):
+    //  A 3: instruction 3 w + m, rows 8 (3 w + m) + l / 8, global part
+    //       (l % 8) ^ (l / 8)
+    //  B 1 or 2: instruction k = w (+ 8), columns 16 k + l / 4, global part
+    //       (l % 4) ^ ((column >> 1) & 3)
+    uint32_t ap[3], bp[2];
+    int bpart[2];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const int R = 8 * (3 * wave + m) + (lane >> 3);
+      ap[m] = piece_row(R) * (uint32_t)Kp + (((lane & 7) ^ (lane >> 3)) << 4);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int C = 16 * (wave + kGmWaves * m) + (lane >> 2);
+      bp[m] = (uint32_t)(((size_t)e * N + n0 + min(C, kGmCols - 1)) * G * 16);
+      bpart[m] = (lane & 3) ^ ((C >> 1) & 3);
+    }
+    auto issue_chunk = [&](int c, int S) {
+      uint8_t* st = ring + S * kGmStage;
+#pragma unroll
+      for (int m = 0; m < 3; ++m)
+        __builtin_amdgcn_global_load_lds((const void*)(q + ap[m] + c * 128),
+                                         (lds_ptr_t)(st + kGmAo + (3 * wave + m) * 1024), 16, 0,
+                                         0);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        if (m == 0 || two_b) {
+          // past K a column re-reads block G - 1 (finite; its A codes are zero)
+          const uint32_t blk = (uint32_t)min(4 * c + bpart[m], G - 1);
+          __builtin_amdgcn_global_load_lds((const void*)(blocks + bp[m] + blk * 16),
+                                           (lds_ptr_t)(st + kGmBo + (wave + kGmWaves * m) * 1024),
+                                           16, 0, 0);
+        }
+      }
+    };
+
+    // Chunks 0..2 in flight; chunk 0's operands go to registers first.
+    issue_chunk(0, 0);
+    if (NC > 1) issue_chunk(1, 1);
+    if (NC > 2) issue_chunk(2, 2);
+
+    f32x4 acc[3][6];
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+#pragma unroll
+      for (int b = 0; b < 6; ++b) acc[f][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // A operand groups holding no token of the tile are skipped (uniform)
+    int nf = 0;
+#pragma unroll
+    for (int f = 0; f < 3; ++f) nf += (48 * wm + 16 * f) / P < ntok ? 1 : 0;
+
+    // Operands of one chunk in registers: six B groups (16 bytes + scale) and
+    // three A groups (32 bytes + scale).
+    struct Ops {
+      u32x4 b[6];
+      uint32_t bs[6];
+      u32x4 a0[3], a1[3];
+      uint32_t as[3];
+    };
+    auto read_b = [&](Ops& o, int c, auto sv) {
+      constexpr int S = decltype(sv)::value;
+      const uint32_t bsc = vbs + (uint32_t)min(4 * c + g, G - 1);
+      gm_static_for<0, 6>([&](auto bv) {
+        constexpr int b = decltype(bv)::value;
+        o.b[b] = lds_b128<b * 1024>(vb[S]);
+        o.bs[b] = lds_u8<0>(bsc + b * 16 * G);
+      });
+    };
+    auto read_a = [&](Ops& o, int c, auto sv, auto fv) {
+      constexpr int S = decltype(sv)::value, f = decltype(fv)::value;
+      o.a0[f] = lds_b128<f * 2048>(va0[S]);
+      o.a1[f] = lds_b128<f * 2048>(va1[S]);
+      o.as[f] = lds_u8<f * 16 * kGmSclRow>(vas + c);
+    };
+    auto wait_ops = [&](Ops& o) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(o.b[0]), "+v"(o.b[1]), "+v"(o.b[2]), "+v"(o.b[3]), "+v"(o.b[4]),
+                     "+v"(o.b[5]), "+v"(o.bs[0]), "+v"(o.bs[1]), "+v"(o.bs[2]), "+v"(o.bs[3]),
+                     "+v"(o.bs[4]), "+v"(o.bs[5]), "+v"(o.a0[0]), "+v"(o.a0[1]), "+v"(o.a0[2]),
+                     "+v"(o.a1[0]), "+v"(o.a1[1]), "+v"(o.a1[2]), "+v"(o.as[0]), "+v"(o.as[1]),
+                     "+v"(o.as[2]));
+    };
+    auto mfma_group = [&](const Ops& o, auto fv) {
+      constexpr int f = decltype(fv)::value;
+      const i32x8 A = {(int)o.a0[f][0], (int)o.a0[f][1], (int)o.a0[f][2], (int)o.a0[f][3],
+                       (int)o.a1[f][0], (int)o.a1[f][1], (int)o.a1[f][2], (int)o.a1[f][3]};
+#pragma unroll
+      for (int b = 0; b < 6; ++b) {
+        const i32x8 B = {(int)o.b[b][0], (int)o.b[b][1], (int)o.b[b][2], (int)o.b[b][3],
+                         0, 0, 0, 0};
+        acc[f][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[f][b], 0, 4, 0,
+                                                                     (int)o.as[f], 0,
+                                                                     (int)o.bs[b]);
+      }
+    };
+
+    // wait until at most `pending` later chunks' loads are outstanding (a
+    // wave issues 4 or 5 loads per chunk; its loads complete in order)
+    auto wait_chunks = [&](int pending) {
+      if (pending >= 2) {
+        if (two_b) wait_vmcnt<10>(); else wait_vmcnt<8>();
+      } else if (pending == 1) {
+        if (two_b) wait_vmcnt<5>(); else wait_vmcnt<4>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    };
+    Ops cur, nxt;
+    // chunk 0 landed (and the unit's scales: issued before it)
+    wait_chunks(min(NC - 1, 2));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(cur, 0, std::integral_constant<int, 0>{});
+    gm_static_for<0, 3>([&](auto fv) { read_a(cur, 0, std::integral_constant<int, 0>{}, fv); });
+    wait_ops(cur);
+
+    // Step c: chunk c + 1 landed everywhere (its waves' vmcnt + barrier; the
+    // barrier also certifies that every wave has read chunk c out of stage
+    // c % 3), issue chunk c + 3 into that stage, then multiply chunk c from
+    // registers while chunk c + 1's operands are read from LDS.  The barrier
+    // carries no memory fence: a fence would wait for the loads in flight.
+    auto step = [&](int c, Ops& cu, Ops& nx, auto sv) {
+      constexpr int S = decltype(sv)::value;           // stage of chunk c
+      constexpr int S1 = (S + 1) % kGmStages;          // stage of chunk c + 1
+      const bool more = c + 1 < NC;
+      if (more) {
+        wait_chunks(c + 2 < NC ? 1 : 0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 3 < NC) issue_chunk(c + 3, S);
+        read_b(nx, c + 1, std::integral_constant<int, S1>{});
+      }
+      gm_static_for<0, 3>([&](auto fv) {
+        constexpr int f = decltype(fv)::value;
+        if (more) read_a(nx, c + 1, std::integral_constant<int, S1>{}, fv);
+        if (f < nf) mfma_group(cu, fv);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if (more) wait_ops(nx);
+    };
+    // Register sets alternate with the chunk parity and stages with c % 3,
+    // so the loop is unrolled by six.
+    for (int c = 0; c < NC; c += 6) {
+      step(c, cur, nxt, std::integral_constant<int, 0>{});
+      if (c + 1 < NC) step(c + 1, nxt, cur, std::integral_constant<int, 1>{});
+      if (c + 2 < NC) step(c + 2, cur, nxt, std::integral_constant<int, 2>{});
+      if (c + 3 < NC) step(c + 3, nxt, cur, std::integral_constant<int, 0>{});
+      if (c + 4 < NC) step(c + 4, cur, nxt, std::integral_constant<int, 1>{});
+      if (c + 5 < NC) step(c + 5, nxt, cur, std::integral_constant<int, 2>{});
+    }
+    // The MFMAs combine all 64 lanes; the LDS writes below are per-lane.  The
+    // empty asm keeps the compiler from sinking the chains into them.
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+#pragma unroll
+      for (int b = 0; b < 6; ++b) asm volatile("" : "+v"(acc[f][b]));
+    // every wave is done with the stages: the output tile reuses them
+    __syncthreads();
+
+    // Epilogue: bias (+ SwiGLU) into an LDS tile of the unit's outputs, then
+    // row-contiguous 16-byte stores.  mlp1 with SwiGLU: [TPT][96] act columns
+    // n0 / 2 ..; otherwise [TPT][192] columns n0 ...
+    constexpr int TW = kEpi == 1 ? kGmCols / 2 : kGmCols;
+    constexpr int TWp = TW + 4;
+    float* const tile = (float*)ring;
+    static_assert(TPT * TWp * 4 <= kGmStages * kGmStage, "output tile");
+    const uint16_t* const bias_l = (const uint16_t*)(ring + kGmBias);
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+      const int cl = 96 * wn + 16 * b + r;  // column within the tile
+      const float bn = bf2f(bias_l[cl]);
+#pragma unroll
+      for (int f = 0; f < 3; ++f) {
+        const f32x4 a = acc[f][b];
+        if constexpr (P == 4) {
+          const int tt = 12 * wm + 4 * f + g;
+          tile[tt * TWp + cl] = (((a[3] + a[2]) + a[1]) + a[0]) + bn;
+        } else {
+          const float y0 = (a[1] + a[0]) + bn;
+          const float y1 = (a[3] + a[2]) + bn;
+          const int tt0 = 24 * wm + 8 * f + 2 * g;
+          if constexpr (kEpi == 1) {
+            // columns 2 j (glu) and 2 j + 1 (linear) sit in lanes r and r ^ 1;
+            // the even lane takes token tt0, the odd lane token tt0 + 1
+            const bool odd = (r & 1) != 0;
+            const float send = odd ? y0 : y1;  // what the partner needs
+            const float recv = __shfl_xor(send, 1, kWave);
+            const float glu = odd ? recv : y0;
+            const float lin = odd ? y1 : recv;
+            const float xg = fminf(glu, limit);
+            const float xl = fminf(fmaxf(lin, -limit), limit);
+            const float z = __fmul_rn(alpha, xg);
+            const float sig = 1.0f / (1.0f + expf(-z));
+            tile[(tt0 + (odd ? 1 : 0)) * TWp + (cl >> 1)] =
+                __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+          } else {
+            tile[tt0 * TWp + cl] = y0;
+            tile[(tt0 + 1) * TWp + cl] = y1;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    {
+      constexpr int U = TW / 4;  // 16-byte units per row
+      const int cbase = kEpi == 1 ? n0 / 2 : n0;
+      for (int uu = tid; uu < ntok * U; uu += kGmThreads) {
+        const int row = uu / U, cu4 = uu - row * U;
+        const int j = start + m0 + row;
+        const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+        *(f32x4*)(out + (size_t)orow * out_ld + cbase + 4 * cu4) =
+            *(const f32x4*)(tile + row * TWp + 4 * cu4);
+      }
+    }
+    // The next unit's loads may not overwrite the tile still being read:
+    // a plain barrier (the tile's LDS reads have been consumed by the stores;
+    // the stores themselves need not complete).
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <int P, int kEpi>
+int launch_gm(dim3 grid, size_t lds, hipStream_t stream, const uint8_t* q, const uint8_t* qs,
+              int Kp, const int* indptr, const int* sp, int k_top, int arow, int orow,
+              const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, int N, int G,
+              int E, float alpha, float limit, float* out, int out_ld, int xcds) {
+  static const bool lds_ok = [] {  // more than 64 KB of dynamic LDS, once per kernel
+    return hipFuncSetAttribute((const void*)moe_mx_gemm_kernel<P, kEpi>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               gm_lds_bytes(256)) == hipSuccess;
+  }();
+  if (!lds_ok) return kErrLaunch;
+  hipLaunchKernelGGL((moe_mx_gemm_kernel<P, kEpi>), grid, dim3(kGmThreads), lds, stream, q, qs,
+                     Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, alpha,
+                     limit, out, out_ld, xcds);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace moe
+
+extern "C" {
+
+size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
+
+// Same contract as moe_launch_mx_gemv (packed pieces, grouping arrays,
+// checkpoint weights); requires N % 192 == 0 and K <= 3072.
+int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* indptr,
+                       const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
+                       const void* blocks, const void* scales, const void* bias, int E, int N,
+                       int K, int rows_active, int swiglu, float alpha, float limit, void* out,
+                       int out_ld, hipStream_t stream) {
+  if (rows_active <= 0) return moe::kOk;
+  if (N % moe::kGmCols || K % 32 || K > 32 * moe::kGmMaxG || E > 256)
+    return moe::kErrUnsupported;
+  // 32-bit offsets into the pieces and the weights
+  if ((int64_t)rows * pieces * ((K + 127) / 128 * 128) >= ((int64_t)1 << 31) ||
+      (int64_t)E * N * (K / 32) * 16 >= ((int64_t)1 << 31))
+    return moe::kErrUnsupported;
+  const int NC = (K + 127) / 128, Kp = NC * 128, G = K / 32;
+  const uint8_t* q = (const uint8_t*)packed;
+  const uint8_t* qs = q + moe_pieces_q_bytes(rows, K, pieces);
+  const int tpt = moe::kGmRows / pieces;
+  const int64_t units_max = (int64_t)(N / moe::kGmCols) *
+                            ((int64_t)max(1, min(E, rows_active)) + rows_active / tpt);
+  if (units_max >= ((int64_t)1 << 31)) return moe::kErrUnsupported;
+  const int nwg = (int)(units_max < moe::kGmCUs ? units_max : moe::kGmCUs);
+  const int xcds = nwg % moe::kGmXcds == 0 ? moe::kGmXcds : 1;
+  const size_t lds = moe::gm_lds_bytes(E);
+  const int* ip = (const int*)indptr;
+  const int* sp = (const int*)sorted_pairs;
+  const uint8_t* b = (const uint8_t*)blocks;
+  const uint8_t* s = (const uint8_t*)scales;
+  const uint16_t* bi = (const uint16_t*)bias;
+  float* o = (float*)out;
+  const dim3 grid(nwg);
+  if (pieces == 2 && swiglu)
+    return moe::launch_gm<2, 1>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+  if (pieces == 2)
+    return moe::launch_gm<2, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+  if (pieces == 4 && !swiglu)
+    return moe::launch_gm<4, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+  return moe::kErrUnsupported;
+}
+
+}  // extern "C"

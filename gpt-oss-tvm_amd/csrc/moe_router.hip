@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
         for (int t2 = 0; t2 < TT; ++t2) a = lane == bb * TT + t2 ? acc[bb][t2] : a;
       if (eb + b < nown) {
         const int e = wave + W * (eb + b);
-        const float d = bf2f(f2bf((float)a));
+        const float d = bf2f(f64_to_bf16_via_f32(a));
         logit[tt][e] = bf2f(f2bf(__fadd_rn(d, bf2f(gate_b[e]))));
       }
     }
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
     };
     double sum = lane_f64(0);
     for (int j = 1; j < k; ++j) sum += lane_f64(j);
-    if (lane < k) w_out[(size_t)tok * k + lane] = f2bf((float)(ex / sum));
+    if (lane < k) w_out[(size_t)tok * k + lane] = f64_to_bf16_via_f32(ex / sum);
   }
 }
 
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   for (int tt = 0; tt < TT; ++tt) {
     const double a = wave_sum_f64(acc[tt]);
     if (lane == 0 && tt < ntok) {
-      const float d = bf2f(f2bf((float)a));
+      const float d = bf2f(f64_to_bf16_via_f32(a));
       logits[(size_t)(tok0 + tt) * E + e] = bf2f(f2bf(__fadd_rn(d, bias)));
     }
   }
@@ -460,7 +460,7 @@ __device__ __forceinline__ void softmax_token(const float* topv, int k,
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    if (j < k) w[j] = f2bf((float)(ex[j] / sum));
+    if (j < k) w[j] = f64_to_bf16_via_f32(ex[j] / sum);
 }
 
 // Placement of pairs [p0, p1) of a stable counting sort by expert, given

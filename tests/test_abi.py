@@ -45,7 +45,7 @@ def test_library_exports_every_header_symbol(native):
 
 def test_internal_launchers_are_hidden(native):
     with pytest.raises(AttributeError):
-        getattr(native.lib(), "moe_launch_expert_gemv")
+        getattr(native.lib(), "moe_launch_mx_gemv")
 
 
 def test_status_codes_match_header(native):

@@ -90,6 +90,29 @@ def test_router_bit_exact(native, E, H, n, seed):
     print(f"E={E} n={n}: {int(ties.sum())} tokens with a 4th/5th tie, all routed identically")
 
 
+def test_router_dot_on_bf16_tie(native):
+    """Token 101 of this input has a gate dot whose fp32 value is exactly a bf16
+    tie (low half 0x8000) while the exact dot lies above it: the two roundings
+    fp64 -> fp32 -> bf16 give the even neighbour, one fp64 -> bf16 rounding the
+    upper one.  Both router paths must keep the two roundings."""
+    p = O.make_params(0, num_experts=32, hidden=2880, inter=64)
+    x = O.make_input(16, 520)
+    t_ref = O.rms_norm(x, p.norm_w)
+    d = (O.bf16_to_f32(t_ref).astype(np.float64) @ O.bf16_to_f32(p.gate_w).astype(np.float64).T)
+    assert (d.astype(np.float32).view(np.uint32)[101, 6] & 0xFFFF) == 0x8000
+    w_ref, idx_ref = O.topk_softmax(O.router_logits(t_ref, p.gate_w, p.gate_b), 4)
+    _, idx, w = native.router_topk(bf16_dev(x), bf16_dev(p.norm_w), bf16_dev(p.gate_w),
+                                   bf16_dev(p.gate_b), 4, 1e-5)
+    assert np.array_equal(host(idx), idx_ref) and np.array_equal(host_bf16(w), w_ref)
+    blk = make_block(p)
+    blk(bf16_dev(x).view(1, 520, 2880))
+    torch.cuda.synchronize()
+    ws = blk._workspace(520, torch.device("cuda:0"))
+    offs = native.workspace_layout(520, 32, 4, 2880, 64)
+    wb = host(ws[offs[2]: offs[2] + 520 * 8].view(torch.int16)).view(np.uint16).reshape(520, 4)
+    assert np.array_equal(wb, w_ref), np.argwhere(wb != w_ref)
+
+
 def test_router_tie_rule(native):
     """Exactly tied logits: the lower expert index wins (as the oracle's stable sort)."""
     E, H, n = 32, 64, 8
@@ -208,6 +231,23 @@ def test_block_internal_routing(native, E, H, I, n, seed):
     assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
 
 
+@pytest.mark.parametrize("E,H,I,n,seed,skew", [(8, 192, 192, 200, 41, False),
+                                               (8, 192, 96, 300, 42, True),
+                                               (12, 384, 96, 157, 43, False)])
+def test_block_gemm_path(native, E, H, I, n, seed, skew):
+    """Experts averaging 48 or more tokens take the tiled GEMM (token tiles of
+    128 for mlp1, 64 for mlp2); skewed routing puts 300 tokens on 4 experts
+    (several token tiles each).  Act and output against the oracle."""
+    p = O.make_params(seed, num_experts=E, hidden=H, inter=I)
+    if skew:
+        p.gate_b[:] = O.f32_to_bf16(np.array([10, 9, 8, 7] + [-10] * (E - 4), np.float32))
+    x = O.make_input(seed + 100, n, hidden=H)
+    tr = O.block_forward(x, p)
+    assert n * 4 >= 48 * E
+    blk = make_block(p)
+    _check_block(blk, x, tr)
+
+
 # ---------------------------------------------------------------------------
 # fp8 pieces of the activations (the scaled-MFMA operand), bit-exact
 # ---------------------------------------------------------------------------
@@ -280,9 +320,10 @@ def block20b():
     return p, make_block(p)
 
 
-@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (5, 12)])
+@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (5, 12), (520, 16)])
 def test_block_20b_shape(native, block20b, n, seed):
-    """BASELINE configs 0 (n = 1) and 1 (n = 64) at full 20B shape, plus a ragged n."""
+    """BASELINE configs 0 (n = 1) and 1 (n = 64) at full 20B shape, a ragged n,
+    and 520 tokens (the tiled GEMM path)."""
     p, blk = block20b
     x = O.make_input(seed, n)
     tr = O.block_forward(x, p)
