@@ -368,11 +368,27 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
                           mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1, alpha,
                           limit, act, (int)I, s)))
     return rc;
-  if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
-  if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
-                          mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f, y,
-                          (int)H, s)))
-    return rc;
+  if ((int64_t)nk >= kGemmMinTokens * E) {
+    if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
+    if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                            mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f,
+                            y, (int)H, s)))
+      return rc;
+  } else if ((int64_t)nk <= 2 * E) {
+    // at most two pairs per expert on average: the GEMV encodes the fp32 act
+    // rows itself while staging them (one kernel less; with more tokens per
+    // expert the encoding would lengthen each staging more than it saves)
+    if ((rc = moe_launch_mx_gemv(act, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                                 mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 2, 0.f,
+                                 0.f, y, (int)H, s)))
+      return rc;
+  } else {
+    if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
+    if ((rc = moe_launch_mx_gemv(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
+                                 mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f,
+                                 0.f, y, (int)H, s)))
+      return rc;
+  }
   return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
 }
 

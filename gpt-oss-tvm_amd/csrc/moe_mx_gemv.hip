@@ -141,7 +141,8 @@ __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict_
 // arow_mode: piece row of sorted position j: 0 = sorted_pairs[j] / k_top
 // (token), 1 = sorted_pairs[j] (pair), 2 = j.  orow_mode: output row: 0 =
 // sorted_pairs[j], 1 = j.  kEpi: 0 = store y (N columns), 1 = interleaved
-// SwiGLU (N/2 columns).
+// SwiGLU (N/2 columns), 2 = store y with the activations given as fp32 rows
+// (arow_mode 2), encoded into P pieces while they are staged.
 template <int P, int kEpi, int NCT>
 __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
@@ -281,7 +282,57 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     const int start = indptr[e];
     const int nb = min(tpb, indptr[e + 1] - start - b0);
     if (u != ubeg) __syncthreads();  // the previous segment's operands are no longer read
-    {
+    if constexpr (kEpi == 2) {
+      // Stage the batch from fp32 rows (q holds float rows of length 32 G),
+      // encoding the P pieces on the way, exactly as moe_pieces_kernel does:
+      // four threads per 32-element block (8 elements each), the block
+      // maximum by lane exchange.  Blocks past K are zero.  Whole quads past
+      // the end compute on the batch's first block and store nothing.
+      const float* xf = (const float*)q;
+      const int K = G * 32;
+      const int nblk = NCT * 4;
+      const int tasks = nb * nblk * 4;
+      for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
+        const int id = t0q + threadIdx.x;
+        const bool valid = id < tasks;
+        const int idc = valid ? id : (id & 3);
+        const int quarter = idc & 3, rb = idc >> 2;
+        const int tt = rb / nblk, blk = rb - tt * nblk;
+        const int j = start + b0 + tt;
+        const int k0 = blk * 32 + quarter * 8;
+        float rr[8];
+        if (blk * 32 < K) {
+          const f32x4* src = (const f32x4*)(xf + (size_t)j * K + k0);
+          const f32x4 v0 = src[0], v1 = src[1];
+          rr[0] = v0[0]; rr[1] = v0[1]; rr[2] = v0[2]; rr[3] = v0[3];
+          rr[4] = v1[0]; rr[5] = v1[1]; rr[6] = v1[2]; rr[7] = v1[3];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) rr[i] = 0.0f;
+        }
+        const int gi = tt / TPG, c = blk >> 2, gg = blk & 3;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
+          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+          const uint32_t sc = e8m0_for_amax(amax);
+          const float inv = __uint_as_float((254u - sc) << 23);
+          const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+          uint32_t lo, hi;
+          e4m3_piece8(rr, inv, scf, lo, hi);
+          if (valid) {
+            const int m = (tt - gi * TPG) * P + p;
+            *(uint2*)(lds + gi * kMxGroupBytes + m * kMxRowStride + k0) = make_uint2(lo, hi);
+            if (quarter == 0)
+              lds[gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + gg * kMxSclRun + c] =
+                  (uint8_t)sc;
+          }
+        }
+      }
+    } else {
       // Stage the batch: 16-byte units, kFill loads in flight per thread.
       // Units past the end repeat the last one (same data to the same place).
       constexpr int kFill = NCT == 23 ? 8 : 4;
@@ -518,9 +569,11 @@ int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, 
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }
 
-// packed: pieces of the activation rows (moe_launch_pieces); max_tokens bounds
-// the tokens of one expert (sizes the LDS batch); rows_active bounds the pairs
-// (and so the experts that hold any).
+// packed: pieces of the activation rows (moe_launch_pieces), or with
+// swiglu == 2 fp32 activation rows of length K (arow_mode 2, pieces == 4),
+// encoded while staged; max_tokens bounds the tokens of one expert (sizes the
+// LDS batch); rows_active bounds the pairs (and so the experts that hold any).
+// swiglu: 0 plain, 1 interleaved SwiGLU epilogue, 2 plain with fp32 rows.
 int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* indptr,
                        const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
                        const void* blocks, const void* scales, const void* bias, int E, int N,
@@ -579,6 +632,10 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
                                 out_ld, xcds);
   if (pieces == 2)
     return moe::launch_mx<2, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
+                                out_ld, xcds);
+  if (pieces == 4 && swiglu == 2)  // fp32 activation rows, encoded while staged
+    return moe::launch_mx<4, 2>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld, xcds);
   if (pieces == 4 && !swiglu)
