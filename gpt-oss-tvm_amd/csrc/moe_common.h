@@ -168,4 +168,23 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+// LDS pointer type of the direct global-to-LDS loads (global_load_lds).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight:
+// waits for this wave's LDS operations only, then s_barrier.  __syncthreads'
+// release fence would also wait for every outstanding global load (vmcnt(0)),
+// which drains a load pipeline at each barrier.  The memory clobber keeps the
+// compiler from moving memory accesses across it.  LDS written by
+// global_load_lds must be covered by a vmcnt wait before it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// s_waitcnt with only the vector-memory count: vmcnt(n), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace moe

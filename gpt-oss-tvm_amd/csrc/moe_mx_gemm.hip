@@ -58,7 +58,6 @@ constexpr int kGmXcds = 8;                         // 8 XCDs of 32 CUs, one L2 e
 __host__ __device__ constexpr int gm_lds_bytes(int E) { return 2 * (E + 1) * 4; }
 static_assert(kGmFixedLds + gm_lds_bytes(256) <= 160 * 1024, "LDS");
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int S, int E, class F>
 __device__ __forceinline__ void gm_static_for(F&& f) {
@@ -68,11 +67,6 @@ __device__ __forceinline__ void gm_static_for(F&& f) {
   }
 }
 
-// s_waitcnt with only the vector-memory count: vmcnt(n), n < 64
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // LDS reads of the staged operands, issued as inline asm: the compiler does
 // not count them against the direct loads in flight (it would otherwise wait

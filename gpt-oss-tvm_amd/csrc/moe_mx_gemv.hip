@@ -36,6 +36,8 @@ constexpr int kMxMaxChunks = 24;                           // K <= 3072
 constexpr int kMxSclRun = 28;                              // scale bytes per (row, lane group)
 constexpr int kMxSclRow = 4 * kMxSclRun;                   // 112 scale bytes per piece row
 constexpr int kMxMaxGroups = 3;
+constexpr int kMxRowMap = 32;                              // >= kMxMaxGroups * 16 / 2 tokens
+static_assert(kMxMaxGroups * 8 <= kMxRowMap, "row map");
 constexpr int kLdsBytes = 160 * 1024;                      // per CU
 constexpr int kNumCUs = 256;                               // MI355X
 constexpr int kNumXcds = 8;                                // 8 XCDs of 32 CUs, one L2 each
@@ -161,9 +163,15 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   const int r = lane & 15, g = lane >> 4;
   const int ntiles = N >> 4;
   const int tpb = groups_cap * TPG;
-  // LDS: [groups_cap A operand groups][per-wave scale staging][E+1 unit prefix]
+  // LDS: [groups_cap A operand groups][per-wave scale staging][E+1 unit
+  // prefix][E+1 indptr][sorted_pairs of one batch, kMxRowMap ints]
   uint8_t* const sstage = lds + groups_cap * kMxGroupBytes + wave * (16 * G);
   int* const pre = (int*)(lds + groups_cap * kMxGroupBytes + nwaves * (16 * G));
+  int* const ipl = pre + (E + 1);
+  int* const rowmap = ipl + (E + 1);
+  // the segment's tile counter (see the tile loop)
+  __attribute__((address_space(3))) int* const tile_ctr =
+      (__attribute__((address_space(3))) int*)(rowmap + kMxRowMap);
 
   // Exclusive prefix of the unit counts: ceil(cnt_e / tpb) * ntiles.
   if (wave == 0) {
@@ -172,7 +180,12 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     for (int b = 0; b < E; b += 64) {
       const int i = b + lane;
       int v = 0;
-      if (i < E) v = (indptr[i + 1] - indptr[i] + tpb - 1) / tpb * ntiles;
+      if (i < E) {
+        const int a0 = indptr[i], a1 = indptr[i + 1];
+        v = (a1 - a0 + tpb - 1) / tpb * ntiles;
+        ipl[i] = a0;
+        if (i == E - 1) ipl[E] = a1;
+      }
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int t = __shfl_up(v, o, kWave);
@@ -190,8 +203,32 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
                                 (int)(blockIdx.x / xcds)
                           : (int)blockIdx.x;
-  const int ubeg = (int)(total * vb / gridDim.x);
-  const int uend = (int)(total * (vb + 1) / gridDim.x);
+  // Units lie batch after batch (ntiles each).  With no more batches than
+  // workgroups, every batch gets floor or ceil of grid / batches workgroups
+  // and each of those an equal share of its tiles: one segment (one staging)
+  // per workgroup.  A share that straddled two batches would stage twice and
+  // finish last.  With more batches than workgroups, the units are split
+  // evenly and a share may span several segments.
+  const int nbatches = (int)(total / ntiles);
+  int ubeg, uend;
+  if (nbatches > 0 && nbatches <= (int)gridDim.x) {
+    const int q = (int)gridDim.x / nbatches, rmd = (int)gridDim.x % nbatches;
+    int b, i, w;
+    if (vb < rmd * (q + 1)) {
+      b = vb / (q + 1);
+      i = vb - b * (q + 1);
+      w = q + 1;
+    } else {
+      b = rmd + (vb - rmd * (q + 1)) / q;
+      i = vb - rmd * (q + 1) - (b - rmd) * q;
+      w = q;
+    }
+    ubeg = b * ntiles + ntiles * i / w;
+    uend = b * ntiles + ntiles * (i + 1) / w;
+  } else {
+    ubeg = (int)(total * vb / gridDim.x);
+    uend = (int)(total * (vb + 1) / gridDim.x);
+  }
   if (ubeg >= uend) return;
   auto expert_of = [&](int u) {  // largest e with pre[e] <= u
     int lo = 0, hi = E - 1;
@@ -263,10 +300,65 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     return sgm;
   };
 
+  const bool need_sp = arow_mode != 2 || orow_mode == 0;
+  // Direct-to-LDS staging of packed pieces (NCT == 23): a group's bytes tile
+  // exactly into 1 KB windows, one 64-lane x 16-byte global_load_lds each.
+  // A 16-byte slot is 16 code bytes of a piece row, the row's pad (never
+  // read) or 16 of its scale bytes.  Rows past the batch repeat its last
+  // token (finite data; their outputs are not stored).  No registers hold
+  // the data, so a batch's whole staging is in flight at once.
+  constexpr bool kDirect = kEpi != 2 && NCT == 23;
+  static_assert(mx_group_bytes(23) % 1024 == 0, "group windows");
+  auto fill_direct = [&](int start, int b0, int nb) {
+    constexpr int kWin = kMxGroupBytes / 1024;
+    const int nwin = ((nb + TPG - 1) / TPG) * kWin;
+    for (int wi = wave; wi < nwin; wi += nwaves) {
+      const int gi = wi / kWin;
+      const int o = (wi - gi * kWin) * 1024 + lane * 16;
+      const bool in_rows = o < 16 * kMxRowStride;
+      const int m = in_rows ? o / kMxRowStride : (o - 16 * kMxRowStride) / kMxSclRow;
+      const int within =
+          in_rows ? o - m * kMxRowStride : o - 16 * kMxRowStride - m * kMxSclRow;
+      const int tt = min(gi * TPG + m / P, nb - 1);
+      const int row = arow_mode == 0   ? rowmap[tt] / k_top
+                      : arow_mode == 1 ? rowmap[tt]
+                                       : start + b0 + tt;
+      const size_t prow = (size_t)row * P + (m % P);
+      const uint8_t* src = in_rows ? q + prow * Kp + (within < Kp ? within : 0)
+                                   : qs + prow * kMxSclRow + within;
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(lds + wi * 1024), 16, 0,
+                                       0);
+    }
+  };
+
   Seg sg = seg_at(ubeg);
-  // in flight during the first staging (a wave without a tile in the first
-  // segment loads the segment's first tile; it is replaced before use)
-  issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
+  if constexpr (kDirect) {
+    // The first batch is staged before any tile is requested: loads complete
+    // in issue order, so the first MFMAs then wait for their own tile only
+    // rather than for a whole chip-wide round of tile loads.
+    const int start = ipl[sg.e], nb = min(tpb, ipl[sg.e + 1] - start - sg.b0);
+    if (arow_mode != 2) {
+      if ((int)threadIdx.x < nb) rowmap[threadIdx.x] = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
+      __syncthreads();  // (nothing else in flight)
+    }
+    fill_direct(start, sg.b0, nb);
+    const bool rm_lane = arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
+    int rm = 0;
+    if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
+    if (threadIdx.x == 0) *tile_ctr = nwaves;
+    __builtin_amdgcn_sched_barrier(0);
+    issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
+    __builtin_amdgcn_sched_barrier(0);
+    // everything before the first half's 15 loads (2 scale, 1 bias, 12
+    // chunks) has landed: the staging and the row map entry
+    wait_vmcnt<15>();
+    if (rm_lane) rowmap[threadIdx.x] = rm;
+    lds_barrier();
+  } else {
+    // in flight during the first staging (a wave without a tile in the first
+    // segment loads the segment's first tile; it is replaced before use)
+    issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
+  }
 
   if (NCT * 128 > Kp) {  // zero the K tail of every staged row once
     const int tail16 = (NCT * 128 - Kp) >> 4;
@@ -279,92 +371,107 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
 
   for (int u = ubeg; u < uend;) {
     const int e = sg.e, b0 = sg.b0, t0 = sg.t0, len = sg.len;
-    const int start = indptr[e];
-    const int nb = min(tpb, indptr[e + 1] - start - b0);
-    if (u != ubeg) __syncthreads();  // the previous segment's operands are no longer read
-    if constexpr (kEpi == 2) {
-      // Stage the batch from fp32 rows (q holds float rows of length 32 G),
-      // encoding the P pieces on the way, exactly as moe_pieces_kernel does:
-      // four threads per 32-element block (8 elements each), the block
-      // maximum by lane exchange.  Blocks past K are zero.  Whole quads past
-      // the end compute on the batch's first block and store nothing.
-      const float* xf = (const float*)q;
-      const int K = G * 32;
-      const int nblk = NCT * 4;
-      const int tasks = nb * nblk * 4;
-      for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
-        const int id = t0q + threadIdx.x;
-        const bool valid = id < tasks;
-        const int idc = valid ? id : (id & 3);
-        const int quarter = idc & 3, rb = idc >> 2;
-        const int tt = rb / nblk, blk = rb - tt * nblk;
-        const int j = start + b0 + tt;
-        const int k0 = blk * 32 + quarter * 8;
-        float rr[8];
-        if (blk * 32 < K) {
-          const f32x4* src = (const f32x4*)(xf + (size_t)j * K + k0);
-          const f32x4 v0 = src[0], v1 = src[1];
-          rr[0] = v0[0]; rr[1] = v0[1]; rr[2] = v0[2]; rr[3] = v0[3];
-          rr[4] = v1[0]; rr[5] = v1[1]; rr[6] = v1[2]; rr[7] = v1[3];
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) rr[i] = 0.0f;
-        }
-        const int gi = tt / TPG, c = blk >> 2, gg = blk & 3;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          float amax = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
-          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
-          const uint32_t sc = e8m0_for_amax(amax);
-          const float inv = __uint_as_float((254u - sc) << 23);
-          const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
-          uint32_t lo, hi;
-          e4m3_piece8(rr, inv, scf, lo, hi);
-          if (valid) {
-            const int m = (tt - gi * TPG) * P + p;
-            *(uint2*)(lds + gi * kMxGroupBytes + m * kMxRowStride + k0) = make_uint2(lo, hi);
-            if (quarter == 0)
-              lds[gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + gg * kMxSclRun + c] =
-                  (uint8_t)sc;
-          }
-        }
+    const int start = ipl[e];
+    const int nb = min(tpb, ipl[e + 1] - start - b0);
+    // The batch's sorted_pairs entries go to LDS (rowmap[tt] for token tt of
+    // the batch), so no global load sits in the staging's address chain or in
+    // the epilogue: loads complete in issue order, and waiting on one issued
+    // behind the tiles in flight would wait for all of them.  The barriers
+    // here wait for LDS traffic only (lds_barrier), for the same reason.
+    // (direct staging stages the first segment above)
+    if (!kDirect || u != ubeg) {
+      if (u != ubeg) lds_barrier();  // the previous segment's operands are no longer read
+      if (threadIdx.x == 0) *tile_ctr = nwaves;  // read after the staging's barrier
+      if (need_sp) {
+        if ((int)threadIdx.x < nb) rowmap[threadIdx.x] = sorted_pairs[start + b0 + (int)threadIdx.x];
+        lds_barrier();
       }
-    } else {
-      // Stage the batch: 16-byte units, kFill loads in flight per thread.
-      // Units past the end repeat the last one (same data to the same place).
-      constexpr int kFill = NCT == 23 ? 8 : 4;
-      const int row16 = Kp >> 4;
-      const int units = row16 + kMxSclRow / 16;
-      const int total_units = nb * P * units;
-      for (int u0 = threadIdx.x; u0 < total_units; u0 += kFill * blockDim.x) {
-        u32x4 v[kFill];
-        uint32_t dst[kFill];
-#pragma unroll
-        for (int i = 0; i < kFill; ++i) {
-          const int uu = min(u0 + i * (int)blockDim.x, total_units - 1);
-          const int rp = uu / units, c = uu - rp * units;
-          const int tt = rp / P, p = rp - tt * P;
+      if constexpr (kDirect) {
+        fill_direct(start, b0, nb);
+        wait_vmcnt<0>();
+      } else if constexpr (kEpi == 2) {
+        // Stage the batch from fp32 rows (q holds float rows of length 32 G),
+        // encoding the P pieces on the way, exactly as moe_pieces_kernel does:
+        // four threads per 32-element block (8 elements each), the block
+        // maximum by lane exchange.  Blocks past K are zero.  Whole quads past
+        // the end compute on the batch's first block and store nothing.
+        const float* xf = (const float*)q;
+        const int K = G * 32;
+        const int nblk = NCT * 4;
+        const int tasks = nb * nblk * 4;
+        for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
+          const int id = t0q + threadIdx.x;
+          const bool valid = id < tasks;
+          const int idc = valid ? id : (id & 3);
+          const int quarter = idc & 3, rb = idc >> 2;
+          const int tt = rb / nblk, blk = rb - tt * nblk;
           const int j = start + b0 + tt;
-          const int row = arow_mode == 0 ? sorted_pairs[j] / k_top
-                          : arow_mode == 1 ? sorted_pairs[j] : j;
-          const int gi = tt / TPG, m = (tt - gi * TPG) * P + p;
-          const size_t prow = (size_t)row * P + p;
-          if (c < row16) {
-            v[i] = *(const u32x4*)(q + prow * Kp + c * 16);
-            dst[i] = gi * kMxGroupBytes + m * kMxRowStride + c * 16;
+          const int k0 = blk * 32 + quarter * 8;
+          float rr[8];
+          if (blk * 32 < K) {
+            const f32x4* src = (const f32x4*)(xf + (size_t)j * K + k0);
+            const f32x4 v0 = src[0], v1 = src[1];
+            rr[0] = v0[0]; rr[1] = v0[1]; rr[2] = v0[2]; rr[3] = v0[3];
+            rr[4] = v1[0]; rr[5] = v1[1]; rr[6] = v1[2]; rr[7] = v1[3];
           } else {
-            v[i] = *(const u32x4*)(qs + prow * kMxSclRow + (c - row16) * 16);
-            dst[i] = gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + (c - row16) * 16;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rr[i] = 0.0f;
+          }
+          const int gi = tt / TPG, c = blk >> 2, gg = blk & 3;
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            const uint32_t sc = e8m0_for_amax(amax);
+            const float inv = __uint_as_float((254u - sc) << 23);
+            const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+            uint32_t lo, hi;
+            e4m3_piece8(rr, inv, scf, lo, hi);
+            if (valid) {
+              const int m = (tt - gi * TPG) * P + p;
+              *(uint2*)(lds + gi * kMxGroupBytes + m * kMxRowStride + k0) = make_uint2(lo, hi);
+              if (quarter == 0)
+                lds[gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + gg * kMxSclRun + c] =
+                    (uint8_t)sc;
+            }
           }
         }
+      } else {
+        // Stage the batch: 16-byte units, kFill loads in flight per thread.
+        // Units past the end repeat the last one (same data to the same place).
+        constexpr int kFill = NCT == 23 ? 8 : 4;
+        const int row16 = Kp >> 4;
+        const int units = row16 + kMxSclRow / 16;
+        const int total_units = nb * P * units;
+        for (int u0 = threadIdx.x; u0 < total_units; u0 += kFill * blockDim.x) {
+          u32x4 v[kFill];
+          uint32_t dst[kFill];
 #pragma unroll
-        for (int i = 0; i < kFill; ++i) *(u32x4*)(lds + dst[i]) = v[i];
+          for (int i = 0; i < kFill; ++i) {
+            const int uu = min(u0 + i * (int)blockDim.x, total_units - 1);
+            const int rp = uu / units, c = uu - rp * units;
+            const int tt = rp / P, p = rp - tt * P;
+            const int j = start + b0 + tt;
+            const int row = arow_mode == 0 ? rowmap[tt] / k_top : arow_mode == 1 ? rowmap[tt] : j;
+            const int gi = tt / TPG, m = (tt - gi * TPG) * P + p;
+            const size_t prow = (size_t)row * P + p;
+            if (c < row16) {
+              v[i] = *(const u32x4*)(q + prow * Kp + c * 16);
+              dst[i] = gi * kMxGroupBytes + m * kMxRowStride + c * 16;
+            } else {
+              v[i] = *(const u32x4*)(qs + prow * kMxSclRow + (c - row16) * 16);
+              dst[i] = gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + (c - row16) * 16;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < kFill; ++i) *(u32x4*)(lds + dst[i]) = v[i];
+        }
       }
+      lds_barrier();  // (the staging's loads have been waited for)
     }
-    __syncthreads();
     const int ngroups = (nb + TPG - 1) / TPG;
     const int u_next = u + len;
     Seg nx = {-1, 0, 0, 0};
@@ -417,9 +524,12 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
       });
     };
 
-    for (int it = 0;; ++it) {
-      const int tl = wave + nwaves * it;
-      if (tl >= len) break;
+    // Wave w computes tile w of the segment first (its first half was
+    // prefetched); further tiles are handed out from an LDS counter when a
+    // wave issues its next first half, so waves whose loads are served
+    // faster take more tiles and the workgroup's waves finish together.
+    for (int tl = wave; tl < len;) {
+      int tl_next = len;
       const int tile = t0 + tl;
       const int r0 = tile << 4;
       issue_h1(e, tile);
@@ -439,9 +549,14 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
             // tile of the next segment, else (nothing left) this tile again.
             // Issued unconditionally: a branch here would make the waits of
             // the second half below count the new loads too.
+            int grab = 0;
+            if (lane == 0)
+              grab = __hip_atomic_fetch_add(tile_ctr, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP);
+            tl_next = __builtin_amdgcn_readfirstlane(grab);
             int ne = e, nt = tile;
-            if (tl + nwaves < len) {
-              nt = tile + nwaves;
+            if (tl_next < len) {
+              nt = t0 + tl_next;
             } else if (nx.e >= 0 && wave < nx.len) {
               ne = nx.e;
               nt = nx.t0 + wave;
@@ -461,7 +576,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
             const float y = (((acc[3] + acc[2]) + acc[1]) + acc[0]) + bn;
             if (tt < nb) {
               const int j = start + b0 + tt;
-              const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+              const int orow = orow_mode == 0 ? rowmap[tt] : j;
               out[(size_t)orow * out_ld + r0 + r] = y;
             }
           } else {
@@ -477,7 +592,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
                 for (int h = 0; h < 2; ++h) {
                   if (tt0 + h < nb) {
                     const int j = start + b0 + tt0 + h;
-                    const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+                    const int orow = orow_mode == 0 ? rowmap[tt0 + h] : j;
                     const float xg = fminf(yy[h], limit);
                     const float xl = fminf(fmaxf(ll[h], -limit), limit);
                     const float z = __fmul_rn(alpha, xg);
@@ -493,15 +608,21 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
               for (int h = 0; h < 2; ++h) {
                 if (tt0 + h < nb) {
                   const int j = start + b0 + tt0 + h;
-                  const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+                  const int orow = orow_mode == 0 ? rowmap[tt0 + h] : j;
                   out[(size_t)orow * out_ld + r0 + r] = yy[h];
                 }
               }
             }
           }
       };
-      for (int gi = 0; gi < ngroups - 1; ++gi) do_group(gi, std::false_type{});
+      // Unrolled (ngroups <= kMxMaxGroups): a runtime loop holding stores and
+      // no loads gets a full vmcnt(0) in its preheader from the compiler,
+      // which would wait for the second half's loads before the first half.
+      static_for<0, kMxMaxGroups - 1>([&](auto gv) {
+        if (decltype(gv)::value < ngroups - 1) do_group(decltype(gv)::value, std::false_type{});
+      });
       do_group(ngroups - 1, std::true_type{});
+      tl = tl_next;
     }
     // a wave without tiles in this segment starts its next-segment tile now
     if (wave >= len && nx.e >= 0) issue_h0(nx.e, nx.t0 + (wave < nx.len ? wave : 0));
@@ -599,7 +720,8 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   }();
   const int tpg = 16 / pieces;
   const int gbytes = moe::mx_group_bytes(NC == 23 ? 23 : moe::kMxMaxChunks);
-  const int fixed = waves * 16 * G + (E + 1) * 4;  // scale staging + unit prefix
+  // scale staging, unit prefix, indptr, one batch's sorted_pairs, tile counter
+  const int fixed = waves * 16 * G + 2 * (E + 1) * 4 + (moe::kMxRowMap + 4) * 4;
   const int gfit = (moe::kLdsBytes - fixed) / gbytes;
   const int gcap = min(min(moe::kMxMaxGroups, gfit), (max_tokens + tpg - 1) / tpg);
   if (gcap < 1) return moe::kErrUnsupported;
