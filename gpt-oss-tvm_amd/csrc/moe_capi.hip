@@ -90,7 +90,13 @@ int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indpt
 
 constexpr int kNumRegions = 14;
 constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
-constexpr int kPiecesAct = 4;  // fp8 pieces of the fp32 SwiGLU output (~16 bits)
+// fp8 pieces of the fp32 SwiGLU output act, mlp2's operand: three carry
+// about 12 significant bits (relative to each 32-block's largest magnitude),
+// adding ~2e-5 of max |y| to y and far less than the bf16 rounding of the
+// block output, while mlp2 stages and multiplies a quarter less than with
+// four.  moe_einsum_fused keeps four pieces for fp32 x (about 16 bits).
+constexpr int kPiecesAct = 3;
+constexpr int kPiecesF32 = 4;
 
 void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kNumRegions],
             size_t* total) {
@@ -191,7 +197,7 @@ size_t moe_einsum_workspace_bytes(int64_t n, int64_t k, int64_t E, int64_t K, in
   if (n < 0 || k < 1 || E < 1 || K < 0) return 0;
   const int64_t rows = x_is_3d_f32 ? n * k : n;
   return einsum_grouping_bytes(n, k, E) +
-         moe_pieces_total_bytes(rows, K, x_is_3d_f32 ? kPiecesAct : kPiecesT);
+         moe_pieces_total_bytes(rows, K, x_is_3d_f32 ? kPiecesF32 : kPiecesT);
 }
 
 // Output rows per expert matmul come in 16-row tiles.
@@ -230,7 +236,7 @@ int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indic
   if (rc) return rc;
   // mlp1-style: bf16 rows per token; mlp2-style: fp32 rows per pair
   const int rows = x_is_3d_f32 ? (int)nk : (int)n;
-  const int pieces = x_is_3d_f32 ? kPiecesAct : kPiecesT;
+  const int pieces = x_is_3d_f32 ? kPiecesF32 : kPiecesT;
   if ((rc = moe_launch_pieces(x, x_is_3d_f32, rows, (int)K, pieces, packed, s))) return rc;
   return expert_matmul(packed, rows, pieces, indptr, sp, (int)k, x_is_3d_f32 ? 1 : 0, 0, blocks,
                        scales, bias, (int)E, (int)N, (int)K, (int)nk, (int)nk, 0, 0.f, 0.f, out,
@@ -238,7 +244,7 @@ int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expert_indic
 }
 
 size_t moe_pieces_bytes(int64_t rows, int64_t K, int pieces) {
-  if (rows < 0 || K <= 0 || K % 32 || K > kMaxK || (pieces != 2 && pieces != 4)) return 0;
+  if (rows < 0 || K <= 0 || K % 32 || K > kMaxK || pieces < 2 || pieces > 4) return 0;
   return moe_pieces_total_bytes(rows, K, pieces);
 }
 
@@ -246,7 +252,7 @@ int moe_quantize_pieces(const void* x, int x_is_f32, int64_t rows, int64_t K, in
                         void* packed, moe_stream_t stream) {
   if (rows < 0 || K <= 0 || K % 32 || K > kMaxK || rows >= ((int64_t)1 << 31) / 96)
     return MOE_ERR_SHAPE;
-  if (pieces != 2 && pieces != 4) return MOE_ERR_UNSUPPORTED;
+  if (pieces < 2 || pieces > 4 || (pieces == 3 && !x_is_f32)) return MOE_ERR_UNSUPPORTED;
   if (rows == 0) return MOE_OK;
   if (!x || !packed) return MOE_ERR_NULL;
   if (!aligned16(x) || !aligned16(packed)) return MOE_ERR_ALIGN;

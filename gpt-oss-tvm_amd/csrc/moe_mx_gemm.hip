@@ -55,7 +55,10 @@ constexpr int kGmCUs = 256;                        // MI355X
 constexpr int kGmXcds = 8;                         // 8 XCDs of 32 CUs, one L2 each
 
 // dynamic part: unit prefix and indptr, E + 1 ints each
-__host__ __device__ constexpr int gm_lds_bytes(int E) { return 2 * (E + 1) * 4; }
+// dynamic part: unit prefix and indptr, E + 1 ints each, then two buffers of
+// a unit's sorted_pairs entries (kGmSpMax ints each)
+constexpr int kGmSpMax = kGmRows / 2;
+__host__ __device__ constexpr int gm_lds_bytes(int E) { return 2 * (E + 1) * 4 + 2 * kGmSpMax * 4; }
 static_assert(kGmFixedLds + gm_lds_bytes(256) <= 160 * 1024, "LDS");
 
 
@@ -125,6 +128,14 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
   const uint32_t vbs = rbase + kGmBSc + (96 * wn + r) * G;
   int* const pre = (int*)lds;
   int* const ipl = pre + (E + 1);  // indptr, read once
+  // A unit's sorted_pairs entries (token tt at [tt]) in LDS, double-buffered:
+  // each unit's epilogue loads the next unit's before any of its stores, so
+  // no global load in the address chains or the stores waits behind stores
+  // (vmcnt counts loads and stores together, in issue order).
+  int* const spb = ipl + (E + 1);
+  const bool need_sp = arow_mode != 2 || orow_mode == 0;
+  int par = 0;
+  bool first_unit = true;
 
   // Exclusive prefix of the unit counts: ceil(cnt_e / TPT) * NT.
   if (wave == 0) {
@@ -163,6 +174,12 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
   };
 
   for (int u = vwg; u < total; u += gridDim.x) {
+    // An opaque copy of the lane index for this unit's address arithmetic:
+    // the compiler would otherwise hoist lane-dependent addresses out of the
+    // unit loop and spill them, and reloading a spill waits for every load in
+    // flight (vmcnt counts them in issue order), serialising the prologue.
+    int lane_u = lane;
+    asm volatile("" : "+v"(lane_u));
     const int e = expert_of(u);
     const int off = u - pre[e];
     const int mt = off / NT, nt = off - mt * NT;
@@ -170,41 +187,47 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     const int m0 = mt * TPT;
     const int ntok = min(TPT, ipl[e + 1] - start - m0);
     const int n0 = nt * kGmCols;
+    int* const spu = spb + par * kGmSpMax;
+    if (need_sp && first_unit) {
+      if (tid < ntok) spu[tid] = sorted_pairs[start + m0 + tid];
+      __syncthreads();  // (the first unit: nothing else in flight)
+    }
+    first_unit = false;
     auto src_row = [&](int tt) {  // activation row of token tt of this tile
-      const int j = start + m0 + tt;
-      return arow_mode == 0 ? sorted_pairs[j] / k_top : arow_mode == 1 ? sorted_pairs[j] : j;
+      return arow_mode == 0 ? spu[tt] / k_top : arow_mode == 1 ? spu[tt] : start + m0 + tt;
     };
     // Rows past the tile's tokens load token 0's row: their MFMA rows are
     // computed and never stored (a D row depends on its A row only).
     auto piece_row = [&](int R) {  // packed-pieces row of tile A row R
+      if constexpr (P == 3) asm volatile("" : "+v"(R));  // (not hoisted: see the epilogue)
       const int tt = R / P, p = R - tt * P;
       return (uint32_t)(src_row(tt < ntok ? tt : 0) * P + p);
     };
 
-    // The unit's scales, 16 bytes per lane: A rows (7 loads of 16 per row;
+    // The unit's scales, 16 bytes per lane_u: A rows (7 loads of 16 per row;
     // loads past the last row repeat it), then the B columns' G bytes each
     // (192 G contiguous checkpoint bytes; the tail repeats the last 16).
     {
       constexpr int kAU = kGmRows * 7;                        // 1344 A-scale loads
       const int nbu = kGmCols * G / 16;                       // B-scale loads
       for (int i0 = 64 * wave; i0 < kAU; i0 += kGmThreads) {
-        const int uu = min(i0 + lane, kAU - 1), R = uu / 7;
+        const int uu = min(i0 + lane_u, kAU - 1), R = uu / 7;
         __builtin_amdgcn_global_load_lds(
             (const void*)(qs + piece_row(R) * kGmSclRow + (uu - R * 7) * 16),
             (lds_ptr_t)(ring + kGmASc + i0 * 16), 16, 0, 0);
       }
       const uint8_t* bsrc = scales + ((size_t)e * N + n0) * G;
       for (int i0 = 64 * wave; i0 < nbu; i0 += kGmThreads)
-        __builtin_amdgcn_global_load_lds((const void*)(bsrc + min(i0 + lane, nbu - 1) * 16),
+        __builtin_amdgcn_global_load_lds((const void*)(bsrc + min(i0 + lane_u, nbu - 1) * 16),
                                          (lds_ptr_t)(ring + kGmBSc + i0 * 16), 16, 0, 0);
       // the columns' bias: 384 bytes, 24 loads of 16 (the rest repeat the last)
       if (wave == kGmWaves - 1)
         __builtin_amdgcn_global_load_lds(
-            (const void*)((const uint8_t*)(bias + (size_t)e * N + n0) + min(lane, 23) * 16),
+            (const void*)((const uint8_t*)(bias + (size_t)e * N + n0) + min(lane_u, 23) * 16),
             (lds_ptr_t)(ring + kGmBias), 16, 0, 0);
     }
 
-    // This wave's code loads of a chunk (lane l), 32-bit offsets from q and
+    // This wave's code loads of a chunk (lane_u l), 32-bit offsets from q and
     // blocks (the launcher checks the ranges):
     //  A 3: instruction 3 w + m, rows 8 (3 w + m) + l / 8, global part
     //       (l % 8) ^ (l / 8)
@@ -214,14 +237,14 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     int bpart[2];
 #pragma unroll
     for (int m = 0; m < 3; ++m) {
-      const int R = 8 * (3 * wave + m) + (lane >> 3);
-      ap[m] = piece_row(R) * (uint32_t)Kp + (((lane & 7) ^ (lane >> 3)) << 4);
+      const int R = 8 * (3 * wave + m) + (lane_u >> 3);
+      ap[m] = piece_row(R) * (uint32_t)Kp + (((lane_u & 7) ^ (lane_u >> 3)) << 4);
     }
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const int C = 16 * (wave + kGmWaves * m) + (lane >> 2);
+      const int C = 16 * (wave + kGmWaves * m) + (lane_u >> 2);
       bp[m] = (uint32_t)(((size_t)e * N + n0 + min(C, kGmCols - 1)) * G * 16);
-      bpart[m] = (lane & 3) ^ ((C >> 1) & 3);
+      bpart[m] = (lane_u & 3) ^ ((C >> 1) & 3);
     }
     auto issue_chunk = [&](int c, int S) {
       uint8_t* st = ring + S * kGmStage;
@@ -364,6 +387,18 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
       for (int b = 0; b < 6; ++b) asm volatile("" : "+v"(acc[f][b]));
     // every wave is done with the stages: the output tile reuses them
     __syncthreads();
+    // the next unit's sorted_pairs entries, loaded before this unit's stores
+    int spn = 0;
+    bool spn_lane = false;
+    if (need_sp && u + (int)gridDim.x < total) {
+      const int un = u + (int)gridDim.x;
+      const int e2 = expert_of(un);
+      const int st2 = ipl[e2], m02 = (un - pre[e2]) / NT * TPT;
+      if (tid < min(TPT, ipl[e2 + 1] - st2 - m02)) {
+        spn = sorted_pairs[st2 + m02 + tid];
+        spn_lane = true;
+      }
+    }
 
     // Epilogue: bias (+ SwiGLU) into an LDS tile of the unit's outputs, then
     // row-contiguous 16-byte stores.  mlp1 with SwiGLU: [TPT][96] act columns
@@ -373,6 +408,40 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     float* const tile = (float*)ring;
     static_assert(TPT * TWp * 4 <= kGmStages * kGmStage, "output tile");
     const uint16_t* const bias_l = (const uint16_t*)(ring + kGmBias);
+    if constexpr (P == 3) {
+      // The wave's 48 rows 48 wm + 4 q + i (q = 4 f + g, i < 4) hold 16
+      // tokens, row 3 t + p piece p of token t.  Every third quad repeats:
+      // q = 3k holds token 4k and piece 0 of token 4k + 1, q = 3k + 1 pieces
+      // 1, 2 of token 4k + 1 and 0, 1 of 4k + 2, q = 3k + 2 piece 2 of token
+      // 4k + 2 and token 4k + 3.  The quad holding a token's piece 0 sums it;
+      // the share of the next quad (q + 1: lane + 16, or for g = 3 the next
+      // f's lane group 0) comes by shuffle.  Sums run smallest piece first,
+      // ((p2 + p1) + p0) + bias, as for the other piece counts.
+#pragma unroll
+      for (int b = 0; b < 6; ++b) {
+        const int cl = 96 * wn + 16 * b + r;
+        const float bn = bf2f(bias_l[cl]);
+        float send[3];
+#pragma unroll
+        for (int f = 0; f < 3; ++f)
+          send[f] = (4 * f + g) % 3 == 1 ? acc[f][b][1] + acc[f][b][0] : acc[f][b][0];
+#pragma unroll
+        for (int f = 0; f < 3; ++f) {
+          const f32x4 a = acc[f][b];
+          const float down = __shfl_down(send[f], 16, kWave);
+          const float wrap = f < 2 ? __shfl_xor(send[f < 2 ? f + 1 : f], 48, kWave) : 0.0f;
+          const float recv = g < 3 ? down : wrap;
+          const int q = 4 * f + g, qm = q % 3;
+          const int tb = 16 * wm + (4 * q) / 3;
+          float y0;
+          if (qm == 0) y0 = ((a[2] + a[1]) + a[0]) + bn;
+          else if (qm == 1) y0 = ((recv + a[3]) + a[2]) + bn;
+          else y0 = ((a[3] + a[2]) + a[1]) + bn;
+          tile[(qm == 0 ? tb : tb + 1) * TWp + cl] = y0;
+          if (qm == 0) tile[(tb + 1) * TWp + cl] = (recv + a[3]) + bn;
+        }
+      }
+    } else {
 #pragma unroll
     for (int b = 0; b < 6; ++b) {
       const int cl = 96 * wn + 16 * b + r;  // column within the tile
@@ -408,6 +477,8 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
         }
       }
     }
+    }
+    if (spn_lane) spb[(par ^ 1) * kGmSpMax + tid] = spn;
     __syncthreads();
     {
       constexpr int U = TW / 4;  // 16-byte units per row
@@ -415,7 +486,7 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
       for (int uu = tid; uu < ntok * U; uu += kGmThreads) {
         const int row = uu / U, cu4 = uu - row * U;
         const int j = start + m0 + row;
-        const int orow = orow_mode == 0 ? sorted_pairs[j] : j;
+        const int orow = orow_mode == 0 ? spu[row] : j;
         *(f32x4*)(out + (size_t)orow * out_ld + cbase + 4 * cu4) =
             *(const f32x4*)(tile + row * TWp + 4 * cu4);
       }
@@ -426,6 +497,7 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    par ^= 1;
   }
 }
 
@@ -488,6 +560,9 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                                 b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
   if (pieces == 2)
     return moe::launch_gm<2, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+  if (pieces == 3 && !swiglu)
+    return moe::launch_gm<3, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
                                 b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
   if (pieces == 4 && !swiglu)
     return moe::launch_gm<4, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,

@@ -579,6 +579,37 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
               const int orow = orow_mode == 0 ? rowmap[tt] : j;
               out[(size_t)orow * out_ld + r0 + r] = y;
             }
+          } else if constexpr (P == 3) {
+            // Rows 3t + p hold piece p of token t (t < 5; row 15 unused), lane
+            // group g rows 4g .. 4g + 3: group 0 holds token 0 and piece 0 of
+            // token 1, group 1 the rest of token 1 and pieces 0, 1 of token 2,
+            // group 2 piece 2 of token 2 and token 3, group 3 token 4.  The
+            // straddling shares come from the next lane group (lane + 16).
+            // Sums run from the smallest piece up, as for P = 4.
+            const float send = g == 1 ? acc[1] + acc[0] : acc[0];
+            const float recv = __shfl_down(send, 16, kWave);
+            float y0, y1 = 0.0f;
+            int l0 = g + 1;  // local token of y0 (y1: token 1 of group 0)
+            if (g == 0) {
+              y0 = ((acc[2] + acc[1]) + acc[0]) + bn;
+              y1 = (recv + acc[3]) + bn;
+              l0 = 0;
+            } else if (g == 1) {
+              y0 = ((recv + acc[3]) + acc[2]) + bn;
+            } else if (g == 2) {
+              y0 = ((acc[3] + acc[2]) + acc[1]) + bn;
+            } else {
+              y0 = ((acc[2] + acc[1]) + acc[0]) + bn;
+            }
+  #pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int tt = gi * TPG + (h == 0 ? l0 : 1);
+              if ((h == 0 || g == 0) && tt < nb) {
+                const int j = start + b0 + tt;
+                const int orow = orow_mode == 0 ? rowmap[tt] : j;
+                out[(size_t)orow * out_ld + r0 + r] = h == 0 ? y0 : y1;
+              }
+            }
           } else {
             const float y0 = (acc[1] + acc[0]) + bn;
             const float y1 = (acc[3] + acc[2]) + bn;
@@ -683,6 +714,7 @@ int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, 
                      q, qs)
   if (pieces == 2 && !x_is_f32) MOE_PIECES(2, false);
   else if (pieces == 2) MOE_PIECES(2, true);
+  else if (pieces == 3 && x_is_f32) MOE_PIECES(3, true);
   else if (pieces == 4 && !x_is_f32) MOE_PIECES(4, false);
   else if (pieces == 4) MOE_PIECES(4, true);
   else return moe::kErrUnsupported;
@@ -754,6 +786,14 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
                                 out_ld, xcds);
   if (pieces == 2)
     return moe::launch_mx<2, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
+                                out_ld, xcds);
+  if (pieces == 3 && !swiglu)
+    return moe::launch_mx<3, 0>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
+                                orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
+                                out_ld, xcds);
+  if (pieces == 3 && swiglu == 2)  // fp32 activation rows, encoded while staged
+    return moe::launch_mx<3, 2>(NC, grid, block, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode,
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld, xcds);
   if (pieces == 4 && swiglu == 2)  // fp32 activation rows, encoded while staged

@@ -201,7 +201,7 @@ class MLPBlock(torch.nn.Module):
                                   SWIGLU_ALPHA, self.swiglu_limit)
         rec("mlp1", 1)
         rec("pieces_act", 0)
-        act_pk = _native.quantize_pieces(act, 4)
+        act_pk = _native.quantize_pieces(act, 3)
         rec("pieces_act", 1)
         rec("mlp2", 0)
         y = _native.mlp2(act_pk, perm["indptr"], perm["sorted_pairs"], n, k,

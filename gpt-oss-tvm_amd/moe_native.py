@@ -232,13 +232,13 @@ def mlp1_swiglu(t_pieces, n, H, indptr, sorted_pairs, k, blocks, scales, bias, a
 def mlp2(act_pieces, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
     """mlp2 over grouped pairs -> y fp32 [n*k, H] by pair.
 
-    act_pieces: quantize_pieces(act, 4) of mlp1_swiglu's output (sorted rows).
+    act_pieces: quantize_pieces(act, 3) of mlp1_swiglu's output (sorted rows).
     """
     E, H, G, _ = blocks.shape
     inter = G * 32
     _expect(act_pieces, "act_pieces", torch.uint8)
-    if act_pieces.numel() < pieces_bytes(n * k, inter, 4):
-        raise ValueError("act_pieces: buffer smaller than pieces_bytes(n*k, I, 4)")
+    if act_pieces.numel() < pieces_bytes(n * k, inter, 3):
+        raise ValueError("act_pieces: buffer smaller than pieces_bytes(n*k, I, 3)")
     _expect(blocks, "mlp2_weight_blocks", torch.uint8, (E, H, G, 16))
     _expect(scales, "mlp2_weight_scales", torch.uint8, (E, H, G))
     _expect(bias, "mlp2_bias", torch.bfloat16, (E, H))

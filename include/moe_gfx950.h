@@ -133,9 +133,10 @@ MOE_API int moe_einsum_fused(const void* x, int x_is_3d_f32, const int32_t* expe
  * even) what the earlier ones left, with the smallest scale that keeps the
  * block's codes below 256.  pieces = 2 reproduces bf16 input to within
  * 2^-14 of each 32-block's largest magnitude (exactly when a block spans at
- * most 6 binades); pieces = 4 carries fp32 input to about 16 significant bits.
- * x [rows, K] bf16 (x_is_f32 == 0) or fp32; packed: moe_pieces_bytes(rows, K,
- * pieces) bytes, 16-byte aligned.  K % 32 == 0, K <= 3072, pieces 2 or 4.
+ * most 6 binades); pieces = 3 (fp32 input only) carries about 12 significant
+ * bits and pieces = 4 about 16.  x [rows, K] bf16 (x_is_f32 == 0) or fp32;
+ * packed: moe_pieces_bytes(rows, K, pieces) bytes, 16-byte aligned.
+ * K % 32 == 0, K <= 3072, pieces 2 or 4 (bf16 or fp32) or 3 (fp32).
  */
 MOE_API size_t moe_pieces_bytes(int64_t rows, int64_t K, int pieces);
 MOE_API int moe_quantize_pieces(const void* x, int x_is_f32, int64_t rows, int64_t K, int pieces,
@@ -159,7 +160,7 @@ MOE_API int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr,
  * mlp2 over grouped pairs.
  * Replaces: mxfp4_moe_mlp2_{prefill,decode}, model/mlp_optimized.py:353-460, 573-660,
  * with the fp32 semantics of model/mlp.py:395.
- * act_pieces: moe_quantize_pieces(act, 1, n*k, I, 4) of moe_mlp1_swiglu's output;
+ * act_pieces: moe_quantize_pieces(act, 1, n*k, I, 3) of moe_mlp1_swiglu's output;
  * weights [E, H, I/32, 16], [E, H, I/32], bias [E, H] -> y [n*k, H] fp32,
  * row = pair p = token*k + slot.
  */

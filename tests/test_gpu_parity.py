@@ -254,7 +254,8 @@ def test_block_gemm_path(native, E, H, I, n, seed, skew):
 
 @pytest.mark.parametrize("rows,K,pieces,f32", [(64, 2880, 2, False), (256, 2880, 4, True),
                                                (5, 96, 2, False), (7, 160, 4, True),
-                                               (3, 3072, 4, False), (1, 32, 2, True)])
+                                               (3, 3072, 4, False), (1, 32, 2, True),
+                                               (256, 2880, 3, True), (9, 160, 3, True)])
 def test_quantize_pieces_bit_exact(native, rows, K, pieces, f32):
     rng = np.random.default_rng(rows * K + pieces)
     x = (rng.standard_normal((rows, K)) * np.exp(2 * rng.standard_normal((rows, K)))).astype(np.float32)
