@@ -38,7 +38,7 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                        const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
                        const void* blocks, const void* scales, const void* bias, int E, int N,
                        int K, int rows_active, int swiglu, float alpha, float limit, void* out,
-                       int out_ld, hipStream_t stream);
+                       int out_ld, void* out_qs, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -80,7 +80,7 @@ int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indpt
       ((uintptr_t)bias & 15u) == 0) {
     const int rc = moe_launch_mx_gemm(packed, rows, pieces, indptr, sorted_pairs, k_top,
                                       arow_mode, orow_mode, blocks, scales, bias, E, N, K, pairs,
-                                      swiglu, alpha, limit, out, out_ld, s);
+                                      swiglu, alpha, limit, out, out_ld, nullptr, s);
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }
   return moe_launch_mx_gemv(packed, rows, pieces, indptr, sorted_pairs, k_top, arow_mode,
@@ -370,12 +370,27 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
                                     ei, pp, s)))
     return rc;
-  if ((rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+  // With the tiled GEMM, mlp1's epilogue writes act's three pieces directly
+  // (a 192-column tile holds whole 32-element blocks of act): no fp32 act
+  // round trip and no separate encoding pass.
+  const bool gemm = (int64_t)nk >= kGemmMinTokens * E;
+  bool act_encoded = false;
+  if (gemm && ((uintptr_t)mlp1_bias & 15u) == 0) {
+    rc = moe_launch_mx_gemm(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+                            mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, nk, 2, alpha,
+                            limit, act_pk, (int)I,
+                            (char*)act_pk + moe_pieces_q_bytes(nk, I, kPiecesAct), s);
+    if (rc == MOE_OK) act_encoded = true;
+    else if (rc != MOE_ERR_UNSUPPORTED) return rc;
+  }
+  if (!act_encoded &&
+      (rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
                           mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1, alpha,
                           limit, act, (int)I, s)))
     return rc;
-  if ((int64_t)nk >= kGemmMinTokens * E) {
-    if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
+  if (gemm) {
+    if (!act_encoded && (rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s)))
+      return rc;
     if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
                             mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f,
                             y, (int)H, s)))

@@ -97,7 +97,8 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
     int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
     const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
-    float alpha, float limit, float* __restrict__ out, int out_ld, int xcds) {
+    float alpha, float limit, float* __restrict__ out, int out_ld, int xcds,
+    uint8_t* __restrict__ oqs) {
   __shared__ __align__(16) uint8_t ring[kGmFixedLds];
   extern __shared__ __align__(16) uint8_t lds[];  // unit prefix
   constexpr int TPT = kGmRows / P;  // tokens per tile
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     // Epilogue: bias (+ SwiGLU) into an LDS tile of the unit's outputs, then
     // row-contiguous 16-byte stores.  mlp1 with SwiGLU: [TPT][96] act columns
     // n0 / 2 ..; otherwise [TPT][192] columns n0 ...
-    constexpr int TW = kEpi == 1 ? kGmCols / 2 : kGmCols;
+    constexpr int TW = kEpi >= 1 ? kGmCols / 2 : kGmCols;
     constexpr int TWp = TW + 4;
     float* const tile = (float*)ring;
     static_assert(TPT * TWp * 4 <= kGmStages * kGmStage, "output tile");
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
           const float y0 = (a[1] + a[0]) + bn;
           const float y1 = (a[3] + a[2]) + bn;
           const int tt0 = 24 * wm + 8 * f + 2 * g;
-          if constexpr (kEpi == 1) {
+          if constexpr (kEpi >= 1) {
             // columns 2 j (glu) and 2 j + 1 (linear) sit in lanes r and r ^ 1;
             // the even lane takes token tt0, the odd lane token tt0 + 1
             const bool odd = (r & 1) != 0;
@@ -480,7 +481,65 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     }
     if (spn_lane) spb[(par ^ 1) * kGmSpMax + tid] = spn;
     __syncthreads();
-    {
+    if constexpr (kEpi == 2) {
+      // SwiGLU output straight into three fp8 pieces (the mlp2 operand), the
+      // encoding of moe_pieces_kernel: the tile holds act columns n0 / 2 ..
+      // n0 / 2 + 95 of its tokens, three whole 32-element blocks per row;
+      // four threads per block (8 values each) share its maximum by lane
+      // exchange.  out is the packed q of the act rows (length N / 2, padded
+      // to 128), oqs their scale runs.  The trip count is uniform so every
+      // quad exchanges with all four lanes; extra tasks store nothing.
+      constexpr int PO = 3;
+      const int Ka = N / 2, NCa = (Ka + 127) / 128, Kpa = NCa * 128;
+      uint8_t* const oq = (uint8_t*)out;
+      const int cbase = n0 / 2;
+      const int tasks = ntok * 12;
+      for (int i0 = 0; i0 < tasks; i0 += kGmThreads) {
+        const int id = i0 + tid;
+        const bool valid = id < tasks;
+        const int idc = valid ? id : (id & 3);
+        const int quarter = idc & 3, rb = idc >> 2;
+        const int tt = rb / 3, bk = rb - tt * 3;
+        const f32x4 v0 = *(const f32x4*)(tile + tt * TWp + bk * 32 + quarter * 8);
+        const f32x4 v1 = *(const f32x4*)(tile + tt * TWp + bk * 32 + quarter * 8 + 4);
+        float rr[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        const int orow = orow_mode == 0 ? spu[tt] : start + m0 + tt;
+        const int blk = cbase / 32 + bk, ch = blk >> 2, gg = blk & 3;
+#pragma unroll
+        for (int p = 0; p < PO; ++p) {
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
+          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+          const uint32_t sc = e8m0_for_amax(amax);
+          const float inv = __uint_as_float((254u - sc) << 23);
+          const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+          uint32_t lo, hi;
+          e4m3_piece8(rr, inv, scf, lo, hi);
+          const size_t prow = (size_t)orow * PO + p;
+          if (valid) {
+            *(uint2*)(oq + prow * Kpa + cbase + bk * 32 + quarter * 8) = make_uint2(lo, hi);
+            if (quarter == 0) oqs[prow * kGmSclRow + gg * 28 + ch] = (uint8_t)sc;
+          }
+        }
+      }
+      // The last column tile also writes the rows' tails: zero codes past
+      // Ka, zero scales for the blocks past Ka and for the runs' unused
+      // chunks [NCa, 28).
+      if (nt == NT - 1) {
+        for (int rp = tid; rp < ntok * PO; rp += kGmThreads) {
+          const int tt = rp / PO, p = rp - tt * PO;
+          const int orow = orow_mode == 0 ? spu[tt] : start + m0 + tt;
+          const size_t prow = (size_t)orow * PO + p;
+          for (int c = Ka; c < Kpa; c += 16) *(u32x4*)(oq + prow * Kpa + c) = u32x4{0u, 0u, 0u, 0u};
+          uint8_t* const run = oqs + prow * kGmSclRow;
+          for (int b = Ka / 32; b < 4 * NCa; ++b) run[(b & 3) * 28 + (b >> 2)] = 0;
+          for (int g4 = 0; g4 < 4; ++g4)
+            for (int z = NCa; z < 28; ++z) run[g4 * 28 + z] = 0;
+        }
+      }
+    } else {
       constexpr int U = TW / 4;  // 16-byte units per row
       const int cbase = kEpi == 1 ? n0 / 2 : n0;
       for (int uu = tid; uu < ntok * U; uu += kGmThreads) {
@@ -505,7 +564,7 @@ template <int P, int kEpi>
 int launch_gm(dim3 grid, size_t lds, hipStream_t stream, const uint8_t* q, const uint8_t* qs,
               int Kp, const int* indptr, const int* sp, int k_top, int arow, int orow,
               const uint8_t* blocks, const uint8_t* scales, const uint16_t* bias, int N, int G,
-              int E, float alpha, float limit, float* out, int out_ld, int xcds) {
+              int E, float alpha, float limit, float* out, int out_ld, int xcds, uint8_t* oqs) {
   static const bool lds_ok = [] {  // more than 64 KB of dynamic LDS, once per kernel
     return hipFuncSetAttribute((const void*)moe_mx_gemm_kernel<P, kEpi>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -514,7 +573,7 @@ int launch_gm(dim3 grid, size_t lds, hipStream_t stream, const uint8_t* q, const
   if (!lds_ok) return kErrLaunch;
   hipLaunchKernelGGL((moe_mx_gemm_kernel<P, kEpi>), grid, dim3(kGmThreads), lds, stream, q, qs,
                      Kp, indptr, sp, k_top, arow, orow, blocks, scales, bias, N, G, E, alpha,
-                     limit, out, out_ld, xcds);
+                     limit, out, out_ld, xcds, oqs);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -530,7 +589,7 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                        const void* sorted_pairs, int k_top, int arow_mode, int orow_mode,
                        const void* blocks, const void* scales, const void* bias, int E, int N,
                        int K, int rows_active, int swiglu, float alpha, float limit, void* out,
-                       int out_ld, hipStream_t stream) {
+                       int out_ld, void* out_qs, hipStream_t stream) {
   if (rows_active <= 0) return moe::kOk;
   if (N % moe::kGmCols || K % 32 || K > 32 * moe::kGmMaxG || E > 256)
     return moe::kErrUnsupported;
@@ -555,18 +614,24 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
   const uint16_t* bi = (const uint16_t*)bias;
   float* o = (float*)out;
   const dim3 grid(nwg);
+  if (pieces == 2 && swiglu == 2) {  // SwiGLU straight into 3 act pieces (out = their q)
+    if (!out_qs || ((uintptr_t)out & 15u)) return moe::kErrUnsupported;
+    return moe::launch_gm<2, 2>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds,
+                                (uint8_t*)out_qs);
+  }
   if (pieces == 2 && swiglu)
     return moe::launch_gm<2, 1>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
-                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds, nullptr);
   if (pieces == 2)
     return moe::launch_gm<2, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
-                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds, nullptr);
   if (pieces == 3 && !swiglu)
     return moe::launch_gm<3, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
-                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds, nullptr);
   if (pieces == 4 && !swiglu)
     return moe::launch_gm<4, 0>(grid, lds, stream, q, qs, Kp, ip, sp, k_top, arow_mode, orow_mode,
-                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds);
+                                b, s, bi, N, G, E, alpha, limit, o, out_ld, xcds, nullptr);
   return moe::kErrUnsupported;
 }
 
