@@ -422,47 +422,6 @@ __device__ __forceinline__ float key_value(uint32_t key) {
   return __uint_as_float((hi & 0x80000000u) ? (hi ^ 0x80000000u) : (~hi & 0xFFFF0000u));
 }
 
-// Rank of one token's logits (LDS key row kr, padded to a multiple of 32),
-// one wave: lane e (and e + 64, ...) counts the keys above its own; the k
-// winners go to topi / topv (LDS) at their rank.
-__device__ __forceinline__ void rank_wave(const uint32_t* kr, int E, int k, int* topi,
-                                          float* topv) {
-  const int lane = threadIdx.x & 63;
-  for (int e0 = 0; e0 < E; e0 += 64) {
-    const int e = e0 + lane;
-    const uint32_t key = kr[min(e, E - 1)];
-    int rank = 0;
-    for (int o0 = 0; o0 < E; o0 += 32) {
-      uint32_t ok[32];
-#pragma unroll
-      for (int o = 0; o < 32; ++o) ok[o] = kr[o0 + o];
-#pragma unroll
-      for (int o = 0; o < 32; ++o) rank += ok[o] > key ? 1 : 0;
-    }
-    if (e < E && rank < k) {
-      topi[rank] = e;
-      topv[rank] = key_value(key);
-    }
-  }
-}
-
-// Softmax of one token's k winners (model/mlp.py:382): fp64 exponentials
-// relative to the largest, summed in rank order, bf16 weights.  One thread.
-__device__ __forceinline__ void softmax_token(const float* topv, int k,
-                                              uint16_t* __restrict__ w) {
-  double ex[8], sum = 0.0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j < k) {
-      ex[j] = exp((double)topv[j] - (double)topv[0]);
-      sum = j == 0 ? ex[0] : sum + ex[j];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j < k) w[j] = f64_to_bf16_via_f32(ex[j] / sum);
-}
-
 // Placement of pairs [p0, p1) of a stable counting sort by expert, given
 // base[e] (LDS) = the sorted position of the chunk's first pair of expert e.
 // Within a round of 1024 pairs a pair's rank among same-expert pairs comes
@@ -546,15 +505,17 @@ constexpr int kSelTok = 256;
 
 // Top-k + softmax of the tokens [t0, t0 + nt), in passes of up to
 // kSelLds / Ep tokens: the rows' ranking keys are staged in LDS (stride Ep,
-// padded with -inf); one wave ranks each token; then one thread per token
-// takes the softmax and writes slot j of idx and w.  ti (when given) receives
-// the indices at [t - t0][k]; expert counts go to hist (LDS).
+// padded with -inf); one thread per (token, expert) counts the keys above
+// its own and the k winners go to topi / topv at their rank; then one thread
+// per (token, slot) takes its fp64 exponential, the token's k exponentials
+// are summed in rank order (gathered by shuffle within the token's 8 lanes)
+// and slot j of idx and w is written.  ti (when given) receives the indices
+// at [t - t0][k]; expert counts go to hist (LDS).
 __device__ __forceinline__ void select_range(const float* __restrict__ logits, int t0, int nt,
                                              int E, int k, uint32_t* keys, int* topi,
                                              float* topv, int32_t* __restrict__ idx_out,
                                              uint16_t* __restrict__ w_out, int* ti, int* hist) {
-  const int nw = blockDim.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int Ep = (E + 31) & ~31;
   const int per = min(kSelLds / Ep, kSelTok);
   for (int b0 = 0; b0 < nt; b0 += per) {
@@ -566,19 +527,35 @@ __device__ __forceinline__ void select_range(const float* __restrict__ logits, i
       keys[i] = rank_key(c < E ? src[r * E + c] : -INFINITY, c);
     }
     __syncthreads();
-    for (int r = wave; r < nbt; r += nw) rank_wave(keys + r * Ep, E, k, topi + r * 8, topv + r * 8);
+    for (int i = threadIdx.x; i < nbt * Ep; i += blockDim.x) {
+      const int r = i / Ep, c = i - r * Ep;
+      const uint32_t key = keys[i];
+      const u32x4* kr = (const u32x4*)(keys + r * Ep);
+      int rank = 0;
+      for (int o = 0; o < (Ep >> 2); ++o) {
+        const u32x4 q = kr[o];
+        rank += (q[0] > key) + (q[1] > key) + (q[2] > key) + (q[3] > key);
+      }
+      if (c < E && rank < k) {
+        topi[r * 8 + rank] = c;
+        topv[r * 8 + rank] = key_value(key);
+      }
+    }
     __syncthreads();
-    for (int r = threadIdx.x; r < nbt; r += blockDim.x) {
-      const int t = t0 + b0 + r;
-      softmax_token(topv + r * 8, k, w_out + (size_t)t * k);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j < k) {
-          const int e = topi[r * 8 + j];
-          idx_out[(size_t)t * k + j] = e;
-          if (ti) ti[(b0 + r) * k + j] = e;
-          atomicAdd(&hist[e], 1);
-        }
+    // 8 lanes per token: the loop bound keeps a token's lanes together
+    for (int i = threadIdx.x; i < nbt * 8; i += blockDim.x) {
+      const int r = i >> 3, j = i & 7;
+      const double ex = j < k ? exp((double)topv[r * 8 + j] - (double)topv[r * 8]) : 0.0;
+      const int base = lane & ~7;
+      double sum = __shfl(ex, base, kWave);
+      for (int jj = 1; jj < k; ++jj) sum += __shfl(ex, base + jj, kWave);
+      if (j < k) {
+        const int t = t0 + b0 + r;
+        const int e = topi[r * 8 + j];
+        w_out[(size_t)t * k + j] = f64_to_bf16_via_f32(ex / sum);
+        idx_out[(size_t)t * k + j] = e;
+        if (ti) ti[(b0 + r) * k + j] = e;
+        atomicAdd(&hist[e], 1);
       }
     }
   }
@@ -592,7 +569,7 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
     uint16_t* __restrict__ w_out, int32_t* __restrict__ indptr,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
-  __shared__ uint32_t keys[kSelLds];
+  __shared__ __align__(16) uint32_t keys[kSelLds];
   __shared__ int topi[kSelTok * 8];
   __shared__ float topv[kSelTok * 8];
   __shared__ int idx_lds[4096];
@@ -620,7 +597,7 @@ constexpr int kSelChunk = 64;
 __global__ __launch_bounds__(1024) void moe_select_count_kernel(
     const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out, int32_t* __restrict__ counts) {
-  __shared__ uint32_t keys[kSelLds];
+  __shared__ __align__(16) uint32_t keys[kSelLds];
   __shared__ int topi[kSelChunk * 8];
   __shared__ float topv[kSelChunk * 8];
   __shared__ int h[256];
