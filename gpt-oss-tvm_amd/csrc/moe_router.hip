@@ -244,7 +244,11 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
 }
 
 // Router logits: workgroup (bx, by) of W waves computes the logits of tokens
-// [TT bx, TT bx + TT) for experts [W by, W by + W), one expert per wave.
+// [TT bx, TT bx + TT) for experts [W epw by, W epw (by + 1)): wave w takes
+// experts W (epw by + i) + w, i < epw, one after another (the next gate row
+// loads while the current one's dots run).  Small n spreads the experts over
+// several workgroups per token (epw = 1); larger n gives each workgroup all
+// of them, so the norm and t of a token are computed once.
 //  1  the threads load the token rows and the norm weight cooperatively (one
 //     16-byte chunk per thread and token); each wave loads its gate row;
 //  2  per token, fp64 sum of squares: per thread, fixed-order wave tree, then
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
     float eps, uint16_t* __restrict__ t_out, float* __restrict__ logits,
-    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs) {
+    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs, int epw) {
   constexpr int kChunks = 64 * S;                // 16-byte chunks of a row, at most
   constexpr int J = (kChunks + 64 * W - 1) / (64 * W);  // chunks per thread and token
   __shared__ u32x4 t_lds[TT][kChunks];
@@ -274,17 +278,17 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tok0 = blockIdx.x * TT;
   const int ntok = min(TT, n - tok0);
-  const int e = blockIdx.y * W + wave;
-  const bool own = e < E;  // wave-uniform
+  const int e0 = (int)blockIdx.y * epw * W + wave;  // the wave's first expert
   const int H8 = H >> 3;
   const int NC = (H + 127) >> 7;
 
   u32x4 gv[S];
-  {
-    const u32x4* gr = (const u32x4*)(gate_w + (size_t)min(e, E - 1) * H);
+  auto load_gate = [&](int ee, u32x4* dst) {
+    const u32x4* gr = (const u32x4*)(gate_w + (size_t)min(ee, E - 1) * H);
 #pragma unroll
-    for (int i = 0; i < S; ++i) gv[i] = gr[min(lane + 64 * i, H8 - 1)];
-  }
+    for (int i = 0; i < S; ++i) dst[i] = gr[min(lane + 64 * i, H8 - 1)];
+  };
+  load_gate(e0, gv);
   // rows past n repeat the last token (computed, never stored)
   u32x4 xv[TT][J], wv[J];
 #pragma unroll
@@ -377,33 +381,42 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     }
   }
   __syncthreads();
-  if (!own) return;
 
-  double acc[TT];
+  for (int ei = 0; ei < epw; ++ei) {
+    const int e = e0 + ei * W;
+    if (e >= E) break;  // wave-uniform
+    u32x4 gn[S];
+    if (ei + 1 < epw) load_gate(e + W, gn);
+    double acc[TT];
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) acc[tt] = 0.0;
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = 0.0;
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const int c = lane + 64 * i;
-    if (c < H8) {
-      float gf[8];
-      unpack8(gv[i], gf);
+    for (int i = 0; i < S; ++i) {
+      const int c = lane + 64 * i;
+      if (c < H8) {
+        float gf[8];
+        unpack8(gv[i], gf);
 #pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        float tf[8];
-        unpack8(t_lds[tt][c], tf);
+        for (int tt = 0; tt < TT; ++tt) {
+          float tf[8];
+          unpack8(t_lds[tt][c], tf);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[tt] += (double)__fmul_rn(tf[q], gf[q]);
+          for (int q = 0; q < 8; ++q) acc[tt] += (double)__fmul_rn(tf[q], gf[q]);
+        }
       }
     }
-  }
-  const float bias = bf2f(gate_b[e]);
+    const float bias = bf2f(gate_b[e]);
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-    const double a = wave_sum_f64(acc[tt]);
-    if (lane == 0 && tt < ntok) {
-      const float d = bf2f(f64_to_bf16_via_f32(a));
-      logits[(size_t)(tok0 + tt) * E + e] = bf2f(f2bf(__fadd_rn(d, bias)));
+    for (int tt = 0; tt < TT; ++tt) {
+      const double a = wave_sum_f64(acc[tt]);
+      if (lane == 0 && tt < ntok) {
+        const float d = bf2f(f64_to_bf16_via_f32(a));
+        logits[(size_t)(tok0 + tt) * E + e] = bf2f(f2bf(__fadd_rn(d, bias)));
+      }
+    }
+    if (ei + 1 < epw) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) gv[i] = gn[i];
     }
   }
 }
@@ -725,7 +738,7 @@ extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* 
 
 // Logits of the n tokens into logits[n][E] (fp32 holding bf16 values), t,
 // and (pq != null, H % 32 == 0) the two fp8 pieces of t.  Eight experts per
-// workgroup; TT tokens per workgroup share each gate row read.
+// wave (n <= 128) or all E per workgroup; TT tokens per workgroup share each gate row read.
 extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
                                         const void* gate_b, int n, int H, int E, float eps,
                                         void* t_out, float* logits, void* pq, void* pqs,
@@ -737,10 +750,14 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
   uint16_t* pt = (uint16_t*)t_out;
   uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
   constexpr int W = 8;
-  const int ey = (E + W - 1) / W;
+  // experts per wave: one for n <= 128 (more workgroups per token), all of
+  // them above (the token's norm and t computed once)
+  const int epw = n <= 128 ? 1 : (E + W - 1) / W;
+  const int ey = (E + W * epw - 1) / (W * epw);
 #define MOE_LG(PC, S, TT)                                                                        \
   hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT>), dim3((n + TT - 1) / TT, ey), \
-                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs)
+                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs,   \
+                     epw)
 #define MOE_LG_TT(PC, S, TTBIG)              \
   if (n <= 128) MOE_LG(PC, S, 1);            \
   else if (n <= 1024) MOE_LG(PC, S, 4);      \
