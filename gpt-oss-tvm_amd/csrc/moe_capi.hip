@@ -41,6 +41,12 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                        int out_ld, void* out_qs, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
+int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
+                         const void* sorted_pairs, int k_top, const void* blocks1,
+                         const void* scales1, const void* bias1, const void* blocks2,
+                         const void* scales2, const void* bias2, int E, int H, int I, int nk,
+                         float alpha, float limit, void* act_packed, void* y, void* done,
+                         hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
                       hipStream_t stream);
 }
@@ -115,7 +121,9 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
       nk * (size_t)H * 4,     // y        fp32 [n*k, H]
       (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
-      (size_t)moe_select_chunks((int)n) * E * 4,  // counts int32 [chunks of 64 tokens, E]
+      // counts int32 [chunks of 64 tokens, E]; for n <= 128 its first E hold
+      // the decode launch's per-expert mlp1 completion counts
+      (size_t)moe_select_chunks((int)n) * E * 4,
   };
   size_t o = 0;
   for (int i = 0; i < kNumRegions; ++i) {
@@ -374,6 +382,15 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   // (a 192-column tile holds whole 32-element blocks of act): no fp32 act
   // round trip and no separate encoding pass.
   const bool gemm = (int64_t)nk >= kGemmMinTokens * E;
+  // Decode: mlp1, the encoding of act and mlp2 in one launch (counts[0..E)
+  // were zeroed by the selection above).
+  if (!gemm && n <= 128) {
+    rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
+                              mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
+                              (int)I, nk, alpha, limit, act_pk, y, counts, s);
+    if (rc == MOE_OK) return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
+    if (rc != MOE_ERR_UNSUPPORTED) return rc;
+  }
   bool act_encoded = false;
   if (gemm && ((uintptr_t)mlp1_bias & 15u) == 0) {
     rc = moe_launch_mx_gemm(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,

@@ -177,6 +177,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // which drains a load pipeline at each barrier.  The memory clobber keeps the
 // compiler from moving memory accesses across it.  LDS written by
 // global_load_lds must be covered by a vmcnt wait before it.
+// Cache-policy operand of the global_load_lds builtin: sc1 = device scope.
+constexpr int kCpolSc1 = 16;
+
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }

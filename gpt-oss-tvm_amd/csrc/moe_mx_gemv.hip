@@ -139,20 +139,66 @@ __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict_
 // first, so MFMA c waits only for the loads up to chunk c; every token group
 // of the batch then runs NCT MFMAs over them.  Each wave's first tile is
 // issued before the first staging, so its loads overlap it.
-//
-// arow_mode: piece row of sorted position j: 0 = sorted_pairs[j] / k_top
-// (token), 1 = sorted_pairs[j] (pair), 2 = j.  orow_mode: output row: 0 =
-// sorted_pairs[j], 1 = j.  kEpi: 0 = store y (N columns), 1 = interleaved
-// SwiGLU (N/2 columns), 2 = store y with the activations given as fp32 rows
-// (arow_mode 2), encoded into P pieces while they are staged.
-template <int P, int kEpi, int NCT>
-__global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
-    const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
-    const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
-    int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
-    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
-    int groups_cap, float alpha, float limit, float* __restrict__ out, int out_ld, int xcds) {
-  extern __shared__ __align__(16) uint8_t lds[];
+
+// LDS areas of one pass, as byte offsets from the dynamic LDS base (the A
+// operand groups start at 0).
+struct MxLds {
+  int sstage;    // per-wave scale staging, 16 G bytes per wave
+  int pre;       // unit prefix, E + 1 ints
+  int ipl;       // indptr, E + 1 ints
+  int rowmap;    // one batch's sorted_pairs, kMxRowMap ints
+  int tile_ctr;  // the segment's tile counter
+  int act;       // kEpi 3: the share's SwiGLU outputs, fp32 [tokens][columns]
+};
+
+// A segment of a workgroup's share: expert, first token of its batch, first
+// tile and tile count (e < 0: none).
+struct MxSeg {
+  int e, b0, t0, len;
+};
+
+// Exclusive prefix of the unit counts, ceil(cnt_e / tpb) * ntiles, into pre,
+// and indptr into ipl unless it is null.  Run by one wave.
+__device__ __forceinline__ void mx_unit_prefix(const int* __restrict__ indptr, int E, int tpb,
+                                               int ntiles, int* pre, int* ipl) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  if (lane == 0) pre[0] = 0;
+  for (int b = 0; b < E; b += 64) {
+    const int i = b + lane;
+    int v = 0;
+    if (i < E) {
+      const int a0 = indptr[i], a1 = indptr[i + 1];
+      v = (a1 - a0 + tpb - 1) / tpb * ntiles;
+      if (ipl) {
+        ipl[i] = a0;
+        if (i == E - 1) ipl[E] = a1;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, kWave);
+      if (lane >= o) v += t;
+    }
+    if (i < E) pre[i + 1] = carry + v;
+    carry += __shfl(v, 63, kWave);
+  }
+}
+
+// One grouped GEMV pass over the units counted in L.pre (indptr in L.ipl).
+// align: with one segment per workgroup, shares of a batch start and end at
+// multiples of `align` tiles.  kWait: wait(e, b0, nb) runs before each
+// segment's staging, called by every thread and ending in a workgroup
+// barrier; the first segment's first tile loads are issued before it.
+// first: the share's first segment.
+template <int P, int kEpi, int NCT, bool kWait, class WaitFn>
+__device__ __forceinline__ void mx_pass(
+    uint8_t* lds, const MxLds& L, const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs,
+    int Kp, const int* __restrict__ sorted_pairs, int k_top, int arow_mode, int orow_mode,
+    const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, int N, int G, int E, int groups_cap, float alpha,
+    float limit, float* __restrict__ out, int out_ld, int xcds, int align, WaitFn&& wait,
+    MxSeg& first) {
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
@@ -163,39 +209,14 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   const int r = lane & 15, g = lane >> 4;
   const int ntiles = N >> 4;
   const int tpb = groups_cap * TPG;
-  // LDS: [groups_cap A operand groups][per-wave scale staging][E+1 unit
-  // prefix][E+1 indptr][sorted_pairs of one batch, kMxRowMap ints]
-  uint8_t* const sstage = lds + groups_cap * kMxGroupBytes + wave * (16 * G);
-  int* const pre = (int*)(lds + groups_cap * kMxGroupBytes + nwaves * (16 * G));
-  int* const ipl = pre + (E + 1);
-  int* const rowmap = ipl + (E + 1);
-  // the segment's tile counter (see the tile loop)
+  uint8_t* const sstage = lds + L.sstage + wave * (16 * G);
+  int* const pre = (int*)(lds + L.pre);
+  int* const ipl = (int*)(lds + L.ipl);
+  int* const rowmap = (int*)(lds + L.rowmap);
   __attribute__((address_space(3))) int* const tile_ctr =
-      (__attribute__((address_space(3))) int*)(rowmap + kMxRowMap);
+      (__attribute__((address_space(3))) int*)(int*)(lds + L.tile_ctr);
+  first.e = -1;
 
-  // Exclusive prefix of the unit counts: ceil(cnt_e / tpb) * ntiles.
-  if (wave == 0) {
-    int carry = 0;
-    if (lane == 0) pre[0] = 0;
-    for (int b = 0; b < E; b += 64) {
-      const int i = b + lane;
-      int v = 0;
-      if (i < E) {
-        const int a0 = indptr[i], a1 = indptr[i + 1];
-        v = (a1 - a0 + tpb - 1) / tpb * ntiles;
-        ipl[i] = a0;
-        if (i == E - 1) ipl[E] = a1;
-      }
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(v, o, kWave);
-        if (lane >= o) v += t;
-      }
-      if (i < E) pre[i + 1] = carry + v;
-      carry += __shfl(v, 63, kWave);
-    }
-  }
-  __syncthreads();
   const int64_t total = pre[E];
   // Workgroups go to the XCDs round-robin (workgroup b on XCD b % xcds).
   // Numbering them XCD-major hands each XCD one contiguous run of unit
@@ -223,8 +244,9 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
       i = vb - rmd * (q + 1) - (b - rmd) * q;
       w = q;
     }
-    ubeg = b * ntiles + ntiles * i / w;
-    uend = b * ntiles + ntiles * (i + 1) / w;
+    const int na = ntiles / align;
+    ubeg = b * ntiles + align * (na * i / w);
+    uend = b * ntiles + align * (na * (i + 1) / w);
   } else {
     ubeg = (int)(total * vb / gridDim.x);
     uend = (int)(total * (vb + 1) / gridDim.x);
@@ -284,14 +306,11 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     if (lane < G) *(u32x4*)(sstage + lane * 16) = sc0;
     if (lane + 64 < G) *(u32x4*)(sstage + (lane + 64) * 16) = sc1;
   };
-  const uint32_t sstage_off = groups_cap * kMxGroupBytes + wave * (16 * G) + r * G;
+  const uint32_t sstage_off = L.sstage + wave * (16 * G) + r * G;
   auto scale_b = [&](uint32_t ss, int c) -> uint32_t { return lds[ss + blk_of(c, g)]; };
 
-  struct Seg {
-    int e, b0, t0, len;
-  };
   auto seg_at = [&](int u) {
-    Seg sgm;
+    MxSeg sgm;
     sgm.e = expert_of(u);
     const int off = u - pre[sgm.e];
     sgm.b0 = off / ntiles * tpb;
@@ -309,6 +328,9 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   // the data, so a batch's whole staging is in flight at once.
   constexpr bool kDirect = kEpi != 2 && NCT == 23;
   static_assert(mx_group_bytes(23) % 1024 == 0, "group windows");
+  // kWait: the pieces were written by other workgroups of this launch with
+  // device-scope stores; device-scope (sc1) loads read them coherently (a
+  // 128-byte line may hold bytes of several writers and of other batches).
   auto fill_direct = [&](int start, int b0, int nb) {
     constexpr int kWin = kMxGroupBytes / 1024;
     const int nwin = ((nb + TPG - 1) / TPG) * kWin;
@@ -327,12 +349,34 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
       const uint8_t* src = in_rows ? q + prow * Kp + (within < Kp ? within : 0)
                                    : qs + prow * kMxSclRow + within;
       __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(lds + wi * 1024), 16, 0,
-                                       0);
+                                       kWait ? kCpolSc1 : 0);
     }
   };
 
-  Seg sg = seg_at(ubeg);
-  if constexpr (kDirect) {
+  MxSeg sg = seg_at(ubeg);
+  first = sg;
+  // kEpi 3 (one segment per share): the SwiGLU outputs of the share's
+  // columns, [token of the batch][column - act_c0]
+  float* const act_t = (float*)(lds + L.act);
+  const int act_c0 = sg.t0 * 8, act_ld = (uend - ubeg) * 8;
+  if constexpr (kDirect && kWait) {
+    // the first tile's loads go out before the wait, the staging after it
+    const int start = ipl[sg.e], nb = min(tpb, ipl[sg.e + 1] - start - sg.b0);
+    if (arow_mode != 2 && (int)threadIdx.x < nb)
+      rowmap[threadIdx.x] = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
+    const bool rm_lane = arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
+    int rm = 0;
+    if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
+    if (threadIdx.x == 0) *tile_ctr = 0;
+    __builtin_amdgcn_sched_barrier(0);
+    issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
+    __builtin_amdgcn_sched_barrier(0);
+    wait(sg.e, sg.b0, nb);  // its barrier also publishes the row map
+    fill_direct(start, sg.b0, nb);
+    wait_vmcnt<0>();
+    if (rm_lane) rowmap[threadIdx.x] = rm;
+    lds_barrier();
+  } else if constexpr (kDirect) {
     // The first batch is staged before any tile is requested: loads complete
     // in issue order, so the first MFMAs then wait for their own tile only
     // rather than for a whole chip-wide round of tile loads.
@@ -345,7 +389,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     const bool rm_lane = arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
     int rm = 0;
     if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
-    if (threadIdx.x == 0) *tile_ctr = nwaves;
+    if (threadIdx.x == 0) *tile_ctr = 0;
     __builtin_amdgcn_sched_barrier(0);
     issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
     __builtin_amdgcn_sched_barrier(0);
@@ -381,7 +425,8 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     // (direct staging stages the first segment above)
     if (!kDirect || u != ubeg) {
       if (u != ubeg) lds_barrier();  // the previous segment's operands are no longer read
-      if (threadIdx.x == 0) *tile_ctr = nwaves;  // read after the staging's barrier
+      if constexpr (kWait) wait(e, b0, nb);
+      if (threadIdx.x == 0) *tile_ctr = 0;  // read after the staging's barrier
       if (need_sp) {
         if ((int)threadIdx.x < nb) rowmap[threadIdx.x] = sorted_pairs[start + b0 + (int)threadIdx.x];
         lds_barrier();
@@ -474,7 +519,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     }
     const int ngroups = (nb + TPG - 1) / TPG;
     const int u_next = u + len;
-    Seg nx = {-1, 0, 0, 0};
+    MxSeg nx = {-1, 0, 0, 0};
     if (u_next < uend) nx = seg_at(u_next);
 
     // MFMAs of chunks [C0, C0 + NH) of one operand group, from register half w.
@@ -553,7 +598,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
             if (lane == 0)
               grab = __hip_atomic_fetch_add(tile_ctr, 1, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_WORKGROUP);
-            tl_next = __builtin_amdgcn_readfirstlane(grab);
+            tl_next = __builtin_amdgcn_readfirstlane(grab) + nwaves;
             int ne = e, nt = tile;
             if (tl_next < len) {
               nt = t0 + tl_next;
@@ -614,7 +659,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
             const float y0 = (acc[1] + acc[0]) + bn;
             const float y1 = (acc[3] + acc[2]) + bn;
             const int tt0 = gi * TPG + 2 * g;
-            if constexpr (kEpi == 1) {
+            if constexpr (kEpi == 1 || kEpi == 3) {
               const float l0 = __shfl_xor(y0, 1, kWave);  // odd rows hold the linear half
               const float l1 = __shfl_xor(y1, 1, kWave);
               if ((r & 1) == 0) {
@@ -628,8 +673,11 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
                     const float xl = fminf(fmaxf(ll[h], -limit), limit);
                     const float z = __fmul_rn(alpha, xg);
                     const float sig = 1.0f / (1.0f + expf(-z));
-                    out[(size_t)orow * out_ld + ((r0 + r) >> 1)] =
-                        __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+                    const float v = __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+                    if constexpr (kEpi == 1)
+                      out[(size_t)orow * out_ld + ((r0 + r) >> 1)] = v;
+                    else
+                      act_t[(tt0 + h) * act_ld + ((r0 + r) >> 1) - act_c0] = v;
                   }
                 }
               }
@@ -660,6 +708,187 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
     u = u_next;
     sg = nx;
   }
+}
+
+// arow_mode: piece row of sorted position j: 0 = sorted_pairs[j] / k_top
+// (token), 1 = sorted_pairs[j] (pair), 2 = j.  orow_mode: output row: 0 =
+// sorted_pairs[j], 1 = j.  kEpi: 0 = store y (N columns), 1 = interleaved
+// SwiGLU (N/2 columns), 2 = store y with the activations given as fp32 rows
+// (arow_mode 2), encoded into P pieces while they are staged; 3 = (P = 2,
+// one segment per share) the SwiGLU outputs kept in LDS (MxLds::act).
+template <int P, int kEpi, int NCT>
+__global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
+    const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
+    int arow_mode, int orow_mode, const uint8_t* __restrict__ blocks,
+    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G, int E,
+    int groups_cap, float alpha, float limit, float* __restrict__ out, int out_ld, int xcds) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  // LDS: [groups_cap A operand groups][per-wave scale staging][E+1 unit
+  // prefix][E+1 indptr][sorted_pairs of one batch, kMxRowMap ints][tile counter]
+  MxLds L;
+  L.sstage = groups_cap * mx_group_bytes(NCT);
+  L.pre = L.sstage + (int)(blockDim.x >> 6) * (16 * G);
+  L.ipl = L.pre + 4 * (E + 1);
+  L.rowmap = L.ipl + 4 * (E + 1);
+  L.tile_ctr = L.rowmap + 4 * kMxRowMap;
+  L.act = 0;
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0)
+    mx_unit_prefix(indptr, E, groups_cap * (16 / P), N >> 4, (int*)(lds + L.pre),
+                   (int*)(lds + L.ipl));
+  __syncthreads();
+  MxSeg first;
+  mx_pass<P, kEpi, NCT, false>(lds, L, q, qs, Kp, sorted_pairs, k_top, arow_mode, orow_mode,
+                               blocks, scales, bias, N, G, E, groups_cap, alpha, limit, out,
+                               out_ld, xcds, 1, [](int, int, int) {}, first);
+}
+
+// ---------------------------------------------------------------------------
+// Decode chain in one launch: mlp1 with the interleaved SwiGLU, the encoding
+// of act into three fp8 pieces, and mlp2 (model/mlp.py:387-395 with the
+// expert grouping of mxfp4_moe_mlp1/2_decode, model/mlp_optimized.py:
+// 214-660).  Phase 1 is the mlp1 pass (two pieces of t, 16 tokens per batch)
+// with one segment per workgroup whose share starts and ends on 32-column
+// blocks of act; its SwiGLU outputs stay in LDS, and the workgroup encodes
+// its blocks of act itself (as moe_pieces_kernel<3, true> would from the fp32
+// rows) and adds its tile count to done[e].  Phase 2 is the mlp2 pass over
+// those pieces; each workgroup issues its first tile's weight loads, then
+// waits until done[e] counts all of expert e's mlp1 tiles before staging, so
+// mlp2's start overlaps mlp1's tail.
+//
+// Coherence across the XCDs' L2s without writing back or invalidating them:
+// the act pieces are stored and (by the staging DMA) loaded with device
+// scope (sc1), the code sequence of agent-scope atomic stores and loads, and
+// the counts are agent-scope atomics.  A workgroup adds its count after a
+// barrier, which waits for all of its stores; a waiting workgroup issues its
+// staging only after its count load returned the target.
+//
+// Requirements (checked by the launcher): H == I with 23 chunks of 128, one
+// workgroup per CU and every workgroup resident at once (the grid is the CU
+// count and nothing else runs on the device: a workgroup waiting in phase 2
+// relies on the phase-1 work of the others), at most 64 mlp1 batches, and
+// done[0..E) zero at launch.  The wait is bounded (kDecodeSpinMax polls):
+// past the bound it gives up, so the launch always ends.
+constexpr int kDecodeGroups1 = 2;  // mlp1 batch: 2 groups of 8 tokens
+template <class T>
+__device__ __forceinline__ void store_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kDecodeSpinMax = 1 << 20;
+
+__global__ __launch_bounds__(768) void moe_mx_decode_kernel(
+    const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
+    const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
+    const uint8_t* __restrict__ blocks1, const uint8_t* __restrict__ scales1,
+    const uint16_t* __restrict__ bias1, const uint8_t* __restrict__ blocks2,
+    const uint8_t* __restrict__ scales2, const uint16_t* __restrict__ bias2, int H, int E,
+    int gcap2, float alpha, float limit, uint8_t* aq, uint8_t* aqs, float* __restrict__ y,
+    int* done, int xcds) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int kGroupBytes = mx_group_bytes(23);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int G = H >> 5, Kp = 23 * 128;
+  const int ntiles1 = (2 * H) >> 4, ntiles2 = H >> 4;
+  const int tpb1 = kDecodeGroups1 * 8;
+  // LDS: [kMxMaxGroups operand groups: phase 2's batch; phase 1's two groups
+  // and, in the third, its SwiGLU outputs][scale staging][phase-1 prefix]
+  // [indptr][row map][tile counter][phase-2 prefix]
+  MxLds L1;
+  L1.sstage = kMxMaxGroups * kGroupBytes;
+  L1.pre = L1.sstage + nwaves * (16 * G);
+  L1.ipl = L1.pre + 4 * (E + 1);
+  L1.rowmap = L1.ipl + 4 * (E + 1);
+  L1.tile_ctr = L1.rowmap + 4 * kMxRowMap;
+  L1.act = kDecodeGroups1 * kGroupBytes;
+  MxLds L2 = L1;
+  L2.pre = L1.tile_ctr + 16;
+  const int* const ipl = (const int*)(lds + L1.ipl);
+  if (wave == 0)
+    mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
+  else if (wave == 1)
+    mx_unit_prefix(indptr, E, gcap2 * 5, ntiles2, (int*)(lds + L2.pre), nullptr);
+  __syncthreads();
+
+  MxSeg s1;
+  mx_pass<2, 3, 23, false>(lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1,
+                           bias1, 2 * H, G, E, kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4,
+                           [](int, int, int) {}, s1);
+  lds_barrier();  // every wave's SwiGLU outputs are in LDS
+  if (s1.e >= 0) {
+    // Encode the share's act blocks: four threads per (token, 32-column
+    // block), 8 columns each; the share that ends at column H also writes the
+    // zero blocks up to 128 * 23 and clears the unused scale slots.
+    const int start = ipl[s1.e];
+    const int nb = min(tpb1, ipl[s1.e + 1] - start - s1.b0);
+    const int act_ld = s1.len * 8, nblk = act_ld >> 5, blk0 = s1.t0 >> 2;
+    const int nbt = nblk + (s1.t0 + s1.len == ntiles1 ? 4 * 23 - G : 0);
+    const int tasks = nb * nbt * 4;
+    const float* act = (const float*)(lds + L1.act);
+    for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
+      const int id = t0q + threadIdx.x;
+      const bool valid = id < tasks;
+      const int idc = valid ? id : (id & 3);
+      const int quarter = idc & 3, rb = idc >> 2;
+      const int tt = rb / nbt, bl = rb - tt * nbt;
+      const int blk = blk0 + bl, c = blk >> 2, gg = blk & 3;
+      const int k0 = blk * 32 + quarter * 8;
+      float rr[8];
+      if (bl < nblk) {
+        const f32x4* src = (const f32x4*)(act + tt * act_ld + bl * 32 + quarter * 8);
+        const f32x4 v0 = src[0], v1 = src[1];
+        rr[0] = v0[0]; rr[1] = v0[1]; rr[2] = v0[2]; rr[3] = v0[3];
+        rr[4] = v1[0]; rr[5] = v1[1]; rr[6] = v1[2]; rr[7] = v1[3];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rr[i] = 0.0f;
+      }
+      const size_t j = (size_t)(start + s1.b0 + tt);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+        const uint32_t sc = e8m0_for_amax(amax);
+        const float inv = __uint_as_float((254u - sc) << 23);
+        const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+        uint32_t lo, hi;
+        e4m3_piece8(rr, inv, scf, lo, hi);
+        if (!valid) continue;
+        const size_t prow = j * 3 + p;
+        store_dev((uint64_t*)(aq + prow * Kp + k0), ((uint64_t)hi << 32) | lo);
+        if (quarter == 0) {
+          uint8_t* run = aqs + prow * kMxSclRow + gg * kMxSclRun;
+          store_dev(run + c, (uint8_t)sc);
+          if (c == 22)
+            for (int z = 23; z < kMxSclRun; ++z) store_dev(run + z, (uint8_t)0);
+        }
+      }
+    }
+    // Publish: the barrier waits for every wave's stores (vmcnt(0)); being
+    // device-scope they are then visible to every XCD, so the count can go.
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(done + s1.e, s1.len, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Phase 2: wait for all of expert e's mlp1 tiles, then stage its pieces.
+  auto wait_mlp1 = [&](int e, int, int) {
+    if (threadIdx.x == 0) {
+      const int target = ntiles1 * ((ipl[e + 1] - ipl[e] + tpb1 - 1) / tpb1);
+      for (int it = 0; it < kDecodeSpinMax; ++it) {
+        if (__hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target)
+          break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    lds_barrier();  // the staging's sc1 loads are issued after the count was seen
+  };
+  MxSeg s2;
+  mx_pass<3, 0, 23, true>(lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2,
+                          bias2, H, G, E, gcap2, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2);
 }
 
 template <int P, int kEpi>
@@ -805,6 +1034,56 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
                                 orow_mode, b, s, bi, N, G, E, gcap, alpha, limit, o,
                                 out_ld, xcds);
   return moe::kErrUnsupported;
+}
+
+// The decode chain in one launch (moe_mx_decode_kernel): t pieces (2, rows
+// n) -> act pieces (3, rows nk, written) -> y (fp32 [nk][H], rows by pair).
+// done: E ints, zero at launch.  Returns kErrUnsupported when the shape or
+// the device does not meet the kernel's requirements (the caller then runs
+// mlp1, the encoding and mlp2 as separate launches).
+int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
+                         const void* sorted_pairs, int k_top, const void* blocks1,
+                         const void* scales1, const void* bias1, const void* blocks2,
+                         const void* scales2, const void* bias2, int E, int H, int I, int nk,
+                         float alpha, float limit, void* act_packed, void* y, void* done,
+                         hipStream_t stream) {
+  using namespace moe;
+  if (nk <= 0) return kOk;
+  if (H != I || (H + 127) / 128 != 23 || H % 32 || !done) return kErrUnsupported;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return kErrLaunch;
+  const int grid = kNumCUs;
+  if (cus < grid) return kErrUnsupported;  // every workgroup must be resident
+  constexpr int waves = 11, gcap2 = kMxMaxGroups;
+  const int G = H / 32;
+  const size_t lds = (size_t)kMxMaxGroups * mx_group_bytes(23) + waves * 16 * G +
+                     3 * (E + 1) * 4 + (kMxRowMap + 4) * 4;
+  if (lds > (size_t)kLdsBytes) return kErrUnsupported;
+  // Batches are bounded by (experts holding pairs) + nk / tokens per batch.
+  // Phase 1 needs one segment per workgroup whose share (at most
+  // 4 ceil(quads / floor(grid / batches)) tiles) fits the LDS act tile of 96.
+  const int64_t nb1 = (int64_t)min(E, nk) + nk / (kDecodeGroups1 * 8);
+  const int64_t nb2 = (int64_t)min(E, nk) + nk / (gcap2 * 5);
+  if (nb1 > grid || nb2 > grid) return kErrUnsupported;
+  const int quads = (2 * H / 16) / 4;
+  const int wmin = grid / (int)nb1;
+  if (4 * ((quads + wmin - 1) / wmin) > 96) return kErrUnsupported;
+  static const bool lds_ok =
+      hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
+  if (!lds_ok) return kErrLaunch;
+  const uint8_t* tq = (const uint8_t*)t_packed;
+  uint8_t* aq = (uint8_t*)act_packed;
+  hipLaunchKernelGGL(moe_mx_decode_kernel, dim3(grid), dim3(64 * waves), lds, stream, tq,
+                     tq + moe_pieces_q_bytes(n, H, 2), (const int*)indptr,
+                     (const int*)sorted_pairs, k_top, (const uint8_t*)blocks1,
+                     (const uint8_t*)scales1, (const uint16_t*)bias1, (const uint8_t*)blocks2,
+                     (const uint8_t*)scales2, (const uint16_t*)bias2, H, E, gcap2, alpha, limit,
+                     aq, aq + moe_pieces_q_bytes(nk, I, 3), (float*)y, (int*)done,
+                     grid % kNumXcds == 0 ? kNumXcds : 1);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 }  // extern "C"

@@ -576,12 +576,14 @@ __device__ __forceinline__ void select_range(const float* __restrict__ logits, i
 
 // Top-k + softmax of n <= 128 tokens and the grouping of their n*k pairs,
 // one workgroup (mlc-llm gating_softmax_topk + moe_cumsum / get_indices /
-// get_indptr, model/mlp_optimized.py:118-148).
+// get_indptr, model/mlp_optimized.py:118-148).  zero_e (if not null): E ints
+// set to zero, the completion counts of the decode launch that follows.
 __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
     const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out, int32_t* __restrict__ indptr,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos,
+    int32_t* __restrict__ zero_e) {
   __shared__ __align__(16) uint32_t keys[kSelLds];
   __shared__ int topi[kSelTok * 8];
   __shared__ float topv[kSelTok * 8];
@@ -593,6 +595,7 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
   for (int e = tid; e < E; e += 1024) {
     cnt[e] = 0;
     base[e] = 0;
+    if (zero_e) zero_e[e] = 0;
   }
   select_range(logits, 0, n, E, k, keys, topi, topv, idx_out, w_out, idx_lds, cnt);
   __syncthreads();
@@ -776,8 +779,9 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
 extern "C" int moe_select_chunks(int n) { return (n + moe::kSelChunk - 1) / moe::kSelChunk; }
 
 // Top-k + softmax of the logits, then the grouping of the pairs: one
-// workgroup for n <= 128, otherwise a select/count pass over chunks of
-// kSelChunk tokens (counts[chunks][E]) and a placement pass.
+// workgroup for n <= 128 (which zeroes counts[0..E) for the decode launch),
+// otherwise a select/count pass over chunks of kSelChunk tokens
+// (counts[chunks][E]) and a placement pass.
 extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out,
                                        void* w_out, void* counts, void* indptr,
                                        void* sorted_pairs, void* token_indices,
@@ -789,7 +793,7 @@ extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k,
           *ei = (int32_t*)expert_ids, *pp = (int32_t*)pair_pos;
   if (n <= 128) {
     hipLaunchKernelGGL(moe::moe_select_permute_kernel, dim3(1), dim3(1024), 0, stream, logits, n,
-                       E, k, pi, pw, ip, sp, ti, ei, pp);
+                       E, k, pi, pw, ip, sp, ti, ei, pp, (int32_t*)counts);
   } else {
     const int nch = moe_select_chunks(n);
     int32_t* cnt = (int32_t*)counts;

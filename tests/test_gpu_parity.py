@@ -351,6 +351,26 @@ def test_block_router_pieces_fused(native, block20b, n):
         assert np.array_equal(a, b), np.argwhere(a != b)[:4]
 
 
+@pytest.mark.parametrize("n,seed", [(1, 17), (64, 18), (100, 19)])
+def test_block_decode_act_pieces(native, block20b, n, seed):
+    """The decode launch encodes act in LDS, block by block, into the same three
+    pieces as moe_quantize_pieces of mlp1's fp32 output (rows by sorted pair)."""
+    p, blk = block20b
+    H, k = 2880, 4
+    nk = n * k
+    x = bf16_dev(O.make_input(seed, n)).view(1, n, H)
+    blk(x)
+    torch.cuda.synchronize()
+    ws = blk._workspace(n, x.device)
+    offs = native.workspace_layout(n, p.num_experts, k, H, 2880)
+    nb = native.pieces_bytes(nk, 2880, 3)
+    fused = PM.unpack(host(ws[offs[10]: offs[10] + nb]), nk, 2880, 3)
+    st = blk.forward_staged(x)
+    ref = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), nk, 2880, 3)
+    for a, b in zip(fused, ref):
+        assert np.array_equal(a, b), np.argwhere(a != b)[:4]
+
+
 def test_block_120b_shape(native):
     p = O.make_params(seed=3, num_experts=128)
     x = O.make_input(13, 48)
