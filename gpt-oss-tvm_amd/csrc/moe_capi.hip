@@ -296,6 +296,30 @@ int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorte
                        0.f, 0.f, y, (int)H, as_stream(stream));
 }
 
+int moe_mlp_decode(const void* t_pieces, const int32_t* indptr, const int32_t* sorted_pairs,
+                   int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
+                   const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                   const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                   const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float alpha,
+                   float limit, void* act_pieces, int32_t* done, float* y,
+                   moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (n > 128) return MOE_ERR_UNSUPPORTED;
+  if (!t_pieces || !indptr || !sorted_pairs || !mlp1_blocks || !mlp1_scales || !mlp1_bias ||
+      !mlp2_blocks || !mlp2_scales || !mlp2_bias || !act_pieces || !done || !y)
+    return MOE_ERR_NULL;
+  if (!aligned16(t_pieces) || !aligned16(mlp1_blocks) || !aligned16(mlp1_scales) ||
+      !aligned16(mlp2_blocks) || !aligned16(mlp2_scales) || !aligned16(act_pieces) ||
+      ((uintptr_t)y & 3u) || ((uintptr_t)done & 3u))
+    return MOE_ERR_ALIGN;
+  return moe_launch_mx_decode(t_pieces, (int)n, indptr, sorted_pairs, (int)k, mlp1_blocks,
+                              mlp1_scales, mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E,
+                              (int)H, (int)I, (int)(n * k), alpha, limit, act_pieces, y, done,
+                              as_stream(stream));
+}
+
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
                     int64_t N, uint16_t* out, moe_stream_t stream) {
   if (n < 0 || k < 1 || k > 8 || N <= 0 || N % 4 || n >= ((int64_t)1 << 31) / 8 ||

@@ -591,7 +591,8 @@ __device__ __forceinline__ void mx_pass(
           asm volatile("" : "+v"(acc));
           if constexpr (last) {
             // next first half: this segment's next tile, else this wave's first
-            // tile of the next segment, else (nothing left) this tile again.
+            // tile of the next segment, else (nothing left) expert 0's tile 0,
+            // the same for every such wave, so these loads hit in the caches.
             // Issued unconditionally: a branch here would make the waits of
             // the second half below count the new loads too.
             int grab = 0;
@@ -599,8 +600,9 @@ __device__ __forceinline__ void mx_pass(
               grab = __hip_atomic_fetch_add(tile_ctr, 1, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_WORKGROUP);
             tl_next = __builtin_amdgcn_readfirstlane(grab) + nwaves;
-            int ne = e, nt = tile;
+            int ne = 0, nt = 0;
             if (tl_next < len) {
+              ne = e;
               nt = t0 + tl_next;
             } else if (nx.e >= 0 && wave < nx.len) {
               ne = nx.e;

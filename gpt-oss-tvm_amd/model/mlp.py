@@ -170,12 +170,16 @@ class MLPBlock(torch.nn.Module):
                                     self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit, ws)
         return out.reshape(b, seq_len, dim)
 
-    def forward_staged(self, x: torch.Tensor, events: dict | None = None) -> dict:
+    def forward_staged(self, x: torch.Tensor, events: dict | None = None,
+                       fused_decode: bool = False) -> dict:
         """The same chain, one C call per stage, returning every intermediate.
 
         ``events`` (optional) maps stage names to (start, end) torch.cuda.Event
         pairs recorded around that stage on the current stream; the stages are
-        "router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine".
+        "router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine",
+        or with ``fused_decode`` (the decode chain in one launch, mlp_decode;
+        at most 128 tokens) "mlp_decode" in place of the middle three, and
+        "act" is None.
         """
         b, seq_len, dim = x.shape
         n = b * seq_len
@@ -195,6 +199,20 @@ class MLPBlock(torch.nn.Module):
         rec("pieces_t", 0)
         t_pk = _native.quantize_pieces(t, 2)
         rec("pieces_t", 1)
+        if fused_decode:
+            done = torch.zeros(self.num_experts, dtype=torch.int32, device=x.device)
+            rec("mlp_decode", 0)
+            y, act_pk = _native.mlp_decode(
+                t_pk, n, perm["indptr"], perm["sorted_pairs"], k, self.mlp1_weight_blocks,
+                self.mlp1_weight_scales, self.mlp1_bias, self.mlp2_weight_blocks,
+                self.mlp2_weight_scales, self.mlp2_bias, SWIGLU_ALPHA, self.swiglu_limit,
+                done=done)
+            rec("mlp_decode", 1)
+            rec("combine", 0)
+            out = _native.gemv_gating(y.view(n, k, self.hidden_size), w, x2)
+            rec("combine", 1)
+            return {"t": t, "idx": idx, "w": w, "perm": perm, "act": None,
+                    "act_pieces": act_pk, "y": y, "out": out.reshape(b, seq_len, dim)}
         rec("mlp1", 0)
         act = _native.mlp1_swiglu(t_pk, n, dim, perm["indptr"], perm["sorted_pairs"], k,
                                   self.mlp1_weight_blocks, self.mlp1_weight_scales, self.mlp1_bias,

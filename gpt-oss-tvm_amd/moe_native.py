@@ -45,6 +45,8 @@ _SIGS = {
     "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P],
                         _INT),
     "moe_mlp2": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
+    "moe_mlp_decode": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _F, _F,
+                        _P, _P, _P, _P], _INT),
     "moe_gemv_gating": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _INT),
     "moe_swiglu": ([_P, _I64, _I64, _F, _F, _P, _P], _INT),
     "moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
@@ -247,6 +249,38 @@ def mlp2(act_pieces, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):
     _check(_lib.moe_mlp2(_ptr(act_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H, inter,
                          _ptr(blocks), _ptr(scales), _ptr(bias), _ptr(y), _stream()), "moe_mlp2")
     return y
+
+
+def mlp_decode(t_pieces, n, indptr, sorted_pairs, k, w1, s1, b1, w2, s2, b2, alpha, limit,
+               act_pieces=None, done=None, y=None):
+    """mlp1 + SwiGLU + act pieces + mlp2 in one launch (n <= 128) -> (y, act_pieces).
+
+    Same results as mlp1_swiglu -> quantize_pieces(act, 3) -> mlp2.  Raises
+    RuntimeError ("unsupported parameter value") where the launch does not apply.
+    """
+    E, N2, G, _ = w1.shape
+    inter, H = N2 // 2, G * 32
+    _expect(t_pieces, "t_pieces", torch.uint8)
+    if t_pieces.numel() < pieces_bytes(n, H, 2):
+        raise ValueError("t_pieces: buffer smaller than pieces_bytes(n, H, 2)")
+    _expect(w1, "mlp1_weight_blocks", torch.uint8, (E, 2 * inter, H // 32, 16))
+    _expect(s1, "mlp1_weight_scales", torch.uint8, (E, 2 * inter, H // 32))
+    _expect(b1, "mlp1_bias", torch.bfloat16, (E, 2 * inter))
+    _expect(w2, "mlp2_weight_blocks", torch.uint8, (E, H, inter // 32, 16))
+    _expect(s2, "mlp2_weight_scales", torch.uint8, (E, H, inter // 32))
+    _expect(b2, "mlp2_bias", torch.bfloat16, (E, H))
+    dev = w1.device
+    if act_pieces is None:
+        act_pieces = torch.empty(pieces_bytes(n * k, inter, 3), dtype=torch.uint8, device=dev)
+    if done is None:
+        done = torch.zeros(E, dtype=torch.int32, device=dev)
+    if y is None:
+        y = torch.empty((n * k, H), dtype=torch.float32, device=dev)
+    _check(_lib.moe_mlp_decode(_ptr(t_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H,
+                               inter, _ptr(w1), _ptr(s1), _ptr(b1), _ptr(w2), _ptr(s2), _ptr(b2),
+                               alpha, limit, _ptr(act_pieces), _ptr(done), _ptr(y), _stream()),
+           "moe_mlp_decode")
+    return y, act_pieces
 
 
 def gemv_gating(y: torch.Tensor, w: torch.Tensor, x: torch.Tensor | None = None, out=None):

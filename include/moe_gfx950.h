@@ -170,6 +170,31 @@ MOE_API int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_
                      float* y, moe_stream_t stream);
 
 /*
+ * Decode chain: mlp1 with the SwiGLU epilogue, the encoding of act and mlp2 in
+ * one launch (the results of moe_mlp1_swiglu -> moe_quantize_pieces(act, 1, n*k,
+ * I, 3) -> moe_mlp2, bit for bit), for n <= 128.
+ * Replaces: mxfp4_moe_mlp1_decode + swiglu + mxfp4_moe_mlp2_decode,
+ * model/mlp_optimized.py:214-660 (fp32 semantics of model/mlp.py:387-395).
+ * t_pieces, indptr, sorted_pairs and the weights as for moe_mlp1_swiglu and
+ * moe_mlp2; act_pieces: moe_pieces_bytes(n*k, I, 3) bytes, written with the
+ * pieces moe_mlp2 takes; done: E int32, zero on entry (left holding per-expert
+ * tile counts) -> y [n*k, H] fp32, row = pair.  MOE_ERR_UNSUPPORTED unless
+ * H == I (2817..2944), n <= 128, the device has 256 or more CUs and the shape's
+ * batches fit the launch (always at gpt-oss-20b's E = 32); the caller then runs
+ * the three calls.  The launch keeps one workgroup on each of 256 CUs and its
+ * mlp2 phase waits for the other workgroups' mlp1 results: work running on the
+ * device at the same time delays it, and past a bound of about a second of
+ * waiting the result is wrong.
+ */
+MOE_API int moe_mlp_decode(const void* t_pieces, const int32_t* indptr,
+                           const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E,
+                           int64_t H, int64_t I, const uint8_t* mlp1_blocks,
+                           const uint8_t* mlp1_scales, const uint16_t* mlp1_bias,
+                           const uint8_t* mlp2_blocks, const uint8_t* mlp2_scales,
+                           const uint16_t* mlp2_bias, float alpha, float limit,
+                           void* act_pieces, int32_t* done, float* y, moe_stream_t stream);
+
+/*
  * Gate-weighted sum of the k expert outputs, plus the residual when x != NULL.
  * Replaces: moe_gemv_gating, model/mlp.py:340-369 (MLPBlock.run_gating, mlp.py:328-369)
  * and the residual add of mlp.py:402; the prefill combine scatter_output * w +
@@ -198,7 +223,8 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
 /* Byte offsets of the intermediates inside the block workspace, in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
  * t_pieces, act, act_pieces, y, logits (fp32 [n, E], bf16 values), counts
- * (int32 [ceil(n / 64), E], expert histogram per 64-token chunk). */
+ * (int32 [ceil(n / 64), E], expert histogram per 64-token chunk; for n <= 128
+ * its first E hold the decode chain's per-expert counts). */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                                  size_t offsets[14]);
 

@@ -371,6 +371,46 @@ def test_block_decode_act_pieces(native, block20b, n, seed):
         assert np.array_equal(a, b), np.argwhere(a != b)[:4]
 
 
+@pytest.mark.parametrize("n,seed", [(1, 21), (64, 22), (128, 23)])
+def test_mlp_decode_matches_three_calls(native, block20b, n, seed):
+    """moe_mlp_decode = mlp1_swiglu -> quantize_pieces(act, 3) -> mlp2, bit for bit,
+    on two calls in a row (the second reuses the outputs; its counters are re-zeroed)."""
+    p, blk = block20b
+    x = bf16_dev(O.make_input(seed, n)).view(1, n, 2880)
+    st = blk.forward_staged(x)
+    t_pk = native.quantize_pieces(st["t"], 2)
+    perm, k = st["perm"], 4
+    args = (t_pk, n, perm["indptr"], perm["sorted_pairs"], k, blk.mlp1_weight_blocks,
+            blk.mlp1_weight_scales, blk.mlp1_bias, blk.mlp2_weight_blocks,
+            blk.mlp2_weight_scales, blk.mlp2_bias, 1.702, blk.swiglu_limit)
+    nk = n * k
+    ref_pk = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), nk, 2880, 3)
+    done = torch.zeros(32, dtype=torch.int32, device="cuda")
+    y, pk = native.mlp_decode(*args, done=done)
+    for _ in range(2):
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y), host(st["y"]))
+        # codes, then scale runs (the 256-byte alignment pads are not written)
+        for a, b in zip(PM.unpack(host(pk), nk, 2880, 3), ref_pk):
+            assert np.array_equal(a, b), np.argwhere(a != b)[:4]
+        done.zero_()
+        y, pk = native.mlp_decode(*args, act_pieces=pk, done=done, y=y)
+    cnt = host(torch.diff(perm["indptr"]))
+    assert np.array_equal(host(done), 360 * ((cnt + 15) // 16))  # mlp1 tiles per expert
+
+
+def test_mlp_decode_unsupported(native, block20b):
+    p, blk = block20b
+    n = 129
+    x = bf16_dev(O.make_input(24, n)).view(1, n, 2880)
+    st = blk.forward_staged(x)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        native.mlp_decode(native.quantize_pieces(st["t"], 2), n, st["perm"]["indptr"],
+                          st["perm"]["sorted_pairs"], 4, blk.mlp1_weight_blocks,
+                          blk.mlp1_weight_scales, blk.mlp1_bias, blk.mlp2_weight_blocks,
+                          blk.mlp2_weight_scales, blk.mlp2_bias, 1.702, blk.swiglu_limit)
+
+
 def test_block_120b_shape(native):
     p = O.make_params(seed=3, num_experts=128)
     x = O.make_input(13, 48)
