@@ -20,7 +20,8 @@ int moe_launch_permute(const void* idx, int nk, int k, int E, void* indptr, void
                        void* token_indices, void* expert_ids, void* pair_pos, hipStream_t stream);
 int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
                              const void* gate_b, int n, int H, int E, float eps, void* t_out,
-                             float* logits, void* pq, void* pqs, hipStream_t stream);
+                             float* logits, void* pq, void* pqs, void* zero_e,
+                             hipStream_t stream);
 int moe_select_chunks(int n);
 int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out, void* w_out,
                             void* counts, void* indptr, void* sorted_pairs, void* token_indices,
@@ -41,6 +42,7 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                        int out_ld, void* out_qs, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
                       hipStream_t stream);
+int moe_mx_decode_check(int E, int H, int I, int nk);
 int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* sorted_pairs, int k_top, const void* blocks1,
                          const void* scales1, const void* bias1, const void* blocks2,
@@ -394,20 +396,18 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   const int nk = (int)(n * k);
   float* logits = (float*)(ws + off[12]);
   int32_t* counts = (int32_t*)(ws + off[13]);
-  // norm, t, its pieces and the logits; then top-k, softmax and grouping
+  const bool gemm = (int64_t)nk >= kGemmMinTokens * E;
+  // norm, t, its pieces and the logits (and counts[0..E) = 0 for the decode
+  // launch); then top-k, softmax and grouping
+  void* t_qs = (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT);
   if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
-                                     logits, t_pk,
-                                     (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT), s)))
+                                     logits, t_pk, t_qs, counts, s)))
     return rc;
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
                                     ei, pp, s)))
     return rc;
-  // With the tiled GEMM, mlp1's epilogue writes act's three pieces directly
-  // (a 192-column tile holds whole 32-element blocks of act): no fp32 act
-  // round trip and no separate encoding pass.
-  const bool gemm = (int64_t)nk >= kGemmMinTokens * E;
-  // Decode: mlp1, the encoding of act and mlp2 in one launch (counts[0..E)
-  // were zeroed by the selection above).
+  // Decode (at most 128 tokens, the shape and device fit): mlp1, the encoding
+  // of act and mlp2 in one launch.
   if (!gemm && n <= 128) {
     rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
                               mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
@@ -415,6 +415,9 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
     if (rc == MOE_OK) return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }
+  // With the tiled GEMM, mlp1's epilogue writes act's three pieces directly
+  // (a 192-column tile holds whole 32-element blocks of act): no fp32 act
+  // round trip and no separate encoding pass.
   bool act_encoded = false;
   if (gemm && ((uintptr_t)mlp1_bias & 15u) == 0) {
     rc = moe_launch_mx_gemm(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,

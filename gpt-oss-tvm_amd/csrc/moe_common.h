@@ -177,6 +177,20 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // which drains a load pipeline at each barrier.  The memory clobber keeps the
 // compiler from moving memory accesses across it.  LDS written by
 // global_load_lds must be covered by a vmcnt wait before it.
+// Ranking keys of bf16 logits: the order-preserving unsigned image of the
+// value in the high 16 bits, 0xFFFF - expert in the low 16, so that a larger
+// key means (value larger, or value equal and expert lower).  Logits are bf16
+// values (low 16 bits zero); -inf pads rank below every finite logit.
+__device__ __forceinline__ uint32_t rank_key(float v, int e) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (u & 0xFFFF0000u) | (uint32_t)(0xFFFF - e);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t hi = key & 0xFFFF0000u;
+  return __uint_as_float((hi & 0x80000000u) ? (hi ^ 0x80000000u) : (~hi & 0xFFFF0000u));
+}
+
 // Cache-policy operand of the global_load_lds builtin: sc1 = device scope.
 constexpr int kCpolSc1 = 16;
 

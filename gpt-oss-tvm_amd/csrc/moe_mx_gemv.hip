@@ -185,6 +185,57 @@ __device__ __forceinline__ void mx_unit_prefix(const int* __restrict__ indptr, i
   }
 }
 
+// The workgroup's share [ubeg, uend) of the units counted in pre (E + 1
+// prefix, LDS).  Workgroups go to the XCDs round-robin (workgroup b on XCD
+// b % xcds); numbering them XCD-major hands each XCD one contiguous run of
+// unit ranges, so the workgroups that stage an expert's activations share an
+// L2.  Units lie batch after batch (ntiles each).  With no more batches than
+// workgroups, every batch gets floor or ceil of grid / batches workgroups and
+// each of those an equal share of its tiles, starting and ending on
+// multiples of `align` tiles: one segment (one staging) per workgroup.  A
+// share that straddled two batches would stage twice and finish last.  With
+// more batches than workgroups, the units are split evenly and a share may
+// span several segments.
+__device__ __forceinline__ void mx_share(const int* pre, int E, int ntiles, int align, int xcds,
+                                         int& ubeg, int& uend) {
+  const int total = pre[E];  // < 2^31 (the launchers check)
+  const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
+                                (int)(blockIdx.x / xcds)
+                          : (int)blockIdx.x;
+  const int nbatches = (int)(total / ntiles);
+  if (nbatches > 0 && nbatches <= (int)gridDim.x) {
+    const int q = (int)gridDim.x / nbatches, rmd = (int)gridDim.x % nbatches;
+    int b, i, w;
+    if (vb < rmd * (q + 1)) {
+      b = vb / (q + 1);
+      i = vb - b * (q + 1);
+      w = q + 1;
+    } else {
+      b = rmd + (vb - rmd * (q + 1)) / q;
+      i = vb - rmd * (q + 1) - (b - rmd) * q;
+      w = q;
+    }
+    const int na = ntiles / align;
+    ubeg = b * ntiles + align * (na * i / w);
+    uend = b * ntiles + align * (na * (i + 1) / w);
+  } else {
+    // floor(total * vb / grid) in 32-bit steps: total = a grid + r, r < grid
+    const int g = (int)gridDim.x, a = (int)total / g, r = (int)total - a * g;
+    ubeg = a * vb + r * vb / g;
+    uend = a * (vb + 1) + r * (vb + 1) / g;
+  }
+}
+
+// The largest e with pre[e] <= u: the expert of unit u.
+__device__ __forceinline__ int mx_expert_of(const int* pre, int E, int u) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= u) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 // One grouped GEMV pass over the units counted in L.pre (indptr in L.ipl).
 // align: with one segment per workgroup, shares of a batch start and end at
 // multiples of `align` tiles.  kWait: wait(e, b0, nb) runs before each
@@ -217,49 +268,10 @@ __device__ __forceinline__ void mx_pass(
       (__attribute__((address_space(3))) int*)(int*)(lds + L.tile_ctr);
   first.e = -1;
 
-  const int64_t total = pre[E];
-  // Workgroups go to the XCDs round-robin (workgroup b on XCD b % xcds).
-  // Numbering them XCD-major hands each XCD one contiguous run of unit
-  // ranges, so the workgroups that stage an expert's activations share an L2.
-  const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
-                                (int)(blockIdx.x / xcds)
-                          : (int)blockIdx.x;
-  // Units lie batch after batch (ntiles each).  With no more batches than
-  // workgroups, every batch gets floor or ceil of grid / batches workgroups
-  // and each of those an equal share of its tiles: one segment (one staging)
-  // per workgroup.  A share that straddled two batches would stage twice and
-  // finish last.  With more batches than workgroups, the units are split
-  // evenly and a share may span several segments.
-  const int nbatches = (int)(total / ntiles);
   int ubeg, uend;
-  if (nbatches > 0 && nbatches <= (int)gridDim.x) {
-    const int q = (int)gridDim.x / nbatches, rmd = (int)gridDim.x % nbatches;
-    int b, i, w;
-    if (vb < rmd * (q + 1)) {
-      b = vb / (q + 1);
-      i = vb - b * (q + 1);
-      w = q + 1;
-    } else {
-      b = rmd + (vb - rmd * (q + 1)) / q;
-      i = vb - rmd * (q + 1) - (b - rmd) * q;
-      w = q;
-    }
-    const int na = ntiles / align;
-    ubeg = b * ntiles + align * (na * i / w);
-    uend = b * ntiles + align * (na * (i + 1) / w);
-  } else {
-    ubeg = (int)(total * vb / gridDim.x);
-    uend = (int)(total * (vb + 1) / gridDim.x);
-  }
+  mx_share(pre, E, ntiles, align, xcds, ubeg, uend);
   if (ubeg >= uend) return;
-  auto expert_of = [&](int u) {  // largest e with pre[e] <= u
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (pre[mid] <= u) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-  };
+  auto expert_of = [&](int u) { return mx_expert_of(pre, E, u); };
 
   // Two-stage pipeline per wave: a tile's weights come in two halves of
   // H0 and H1 chunks held in wa / wb.  While one half's MFMAs run, the other
@@ -299,6 +311,19 @@ __device__ __forceinline__ void mx_pass(
     static_for<0, H1>([&](auto cv) {
       constexpr int c = decltype(cv)::value;
       wb[c] = *(const u32x4*)(wp + blk_of(H0 + c, gl) * 16);
+    });
+  };
+  // kWait: chunks [c0, c1) of a tile pulled into the caches while the pass
+  // waits, by direct-to-LDS loads into the third operand group (free until
+  // the staging, whose loads are issued later and so land later).
+  auto warm = [&](int e, int tile, auto c0v, auto c1v) {
+    int gl = g;
+    asm volatile("" : "+v"(gl));
+    const uint8_t* wp = blocks + ((size_t)e * N + (tile << 4) + r) * G * 16;
+    static_for<decltype(c0v)::value, decltype(c1v)::value>([&](auto cv) {
+      constexpr int c = decltype(cv)::value;
+      __builtin_amdgcn_global_load_lds((const void*)(wp + blk_of(c, gl) * 16),
+                                       (lds_ptr_t)(lds + 2 * kMxGroupBytes + c * 1024), 16, 0, 0);
     });
   };
   // The scale bytes pass through LDS to reach the lane that needs each one.
@@ -370,6 +395,8 @@ __device__ __forceinline__ void mx_pass(
     if (threadIdx.x == 0) *tile_ctr = 0;
     __builtin_amdgcn_sched_barrier(0);
     issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
+    if (wave < sg.len)
+      warm(sg.e, sg.t0 + wave, std::integral_constant<int, H0>{}, std::integral_constant<int, NCT>{});
     __builtin_amdgcn_sched_barrier(0);
     wait(sg.e, sg.b0, nb);  // its barrier also publishes the row map
     fill_direct(start, sg.b0, nb);
@@ -777,7 +804,6 @@ __device__ __forceinline__ void store_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 constexpr int kDecodeSpinMax = 1 << 20;
-
 __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
@@ -806,16 +832,18 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   MxLds L2 = L1;
   L2.pre = L1.tile_ctr + 16;
   const int* const ipl = (const int*)(lds + L1.ipl);
+  constexpr int tpb2 = kMxMaxGroups * 5;  // (gcap2 == kMxMaxGroups)
   if (wave == 0)
     mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
   else if (wave == 1)
-    mx_unit_prefix(indptr, E, gcap2 * 5, ntiles2, (int*)(lds + L2.pre), nullptr);
+    mx_unit_prefix(indptr, E, tpb2, ntiles2, (int*)(lds + L2.pre), nullptr);
   __syncthreads();
 
   MxSeg s1;
-  mx_pass<2, 3, 23, false>(lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1,
-                           bias1, 2 * H, G, E, kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4,
-                           [](int, int, int) {}, s1);
+  auto no_wait = [](int, int, int) {};
+  mx_pass<2, 3, 23, false, decltype(no_wait)&>(
+      lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1, bias1, 2 * H, G, E,
+      kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1);
   lds_barrier();  // every wave's SwiGLU outputs are in LDS
   if (s1.e >= 0) {
     // Encode the share's act blocks: four threads per (token, 32-column
@@ -889,8 +917,9 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     lds_barrier();  // the staging's sc1 loads are issued after the count was seen
   };
   MxSeg s2;
-  mx_pass<3, 0, 23, true>(lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2,
-                          bias2, H, G, E, gcap2, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2);
+  mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
+      lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
+      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2);
 }
 
 template <int P, int kEpi>
@@ -1038,31 +1067,26 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   return moe::kErrUnsupported;
 }
 
-// The decode chain in one launch (moe_mx_decode_kernel): t pieces (2, rows
-// n) -> act pieces (3, rows nk, written) -> y (fp32 [nk][H], rows by pair).
-// done: E ints, zero at launch.  Returns kErrUnsupported when the shape or
-// the device does not meet the kernel's requirements (the caller then runs
-// mlp1, the encoding and mlp2 as separate launches).
-int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
-                         const void* sorted_pairs, int k_top, const void* blocks1,
-                         const void* scales1, const void* bias1, const void* blocks2,
-                         const void* scales2, const void* bias2, int E, int H, int I, int nk,
-                         float alpha, float limit, void* act_packed, void* y, void* done,
-                         hipStream_t stream) {
+static size_t decode_lds_bytes(int E, int H) {
   using namespace moe;
-  if (nk <= 0) return kOk;
-  if (H != I || (H + 127) / 128 != 23 || H % 32 || !done) return kErrUnsupported;
+  return (size_t)kMxMaxGroups * mx_group_bytes(23) + 11 * 16 * (H / 32) + 3 * (E + 1) * 4 +
+         (kMxRowMap + 4) * 4;
+}
+
+// kOk when moe_launch_mx_decode can run this shape on the current device,
+// else kErrUnsupported (the caller then runs mlp1, the encoding and mlp2 as
+// separate launches).
+int moe_mx_decode_check(int E, int H, int I, int nk) {
+  using namespace moe;
+  if (H != I || (H + 127) / 128 != 23 || H % 32) return kErrUnsupported;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return kErrLaunch;
   const int grid = kNumCUs;
   if (cus < grid) return kErrUnsupported;  // every workgroup must be resident
-  constexpr int waves = 11, gcap2 = kMxMaxGroups;
-  const int G = H / 32;
-  const size_t lds = (size_t)kMxMaxGroups * mx_group_bytes(23) + waves * 16 * G +
-                     3 * (E + 1) * 4 + (kMxRowMap + 4) * 4;
-  if (lds > (size_t)kLdsBytes) return kErrUnsupported;
+  constexpr int gcap2 = kMxMaxGroups;
+  if (decode_lds_bytes(E, H) > (size_t)kLdsBytes) return kErrUnsupported;
   // Batches are bounded by (experts holding pairs) + nk / tokens per batch.
   // Phase 1 needs one segment per workgroup whose share (at most
   // 4 ceil(quads / floor(grid / batches)) tiles) fits the LDS act tile of 96.
@@ -1072,6 +1096,26 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
   const int quads = (2 * H / 16) / 4;
   const int wmin = grid / (int)nb1;
   if (4 * ((quads + wmin - 1) / wmin) > 96) return kErrUnsupported;
+  return kOk;
+}
+
+// The decode chain in one launch (moe_mx_decode_kernel): t pieces (2, rows
+// n) -> act pieces (3, rows nk, written) -> y (fp32 [nk][H], rows by pair).
+// done: E ints, zero at launch.
+int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
+                         const void* sorted_pairs, int k_top, const void* blocks1,
+                         const void* scales1, const void* bias1, const void* blocks2,
+                         const void* scales2, const void* bias2, int E, int H, int I, int nk,
+                         float alpha, float limit, void* act_packed, void* y, void* done,
+                         hipStream_t stream) {
+  using namespace moe;
+  if (nk <= 0) return kOk;
+  if (!done) return kErrUnsupported;
+  const int rc = moe_mx_decode_check(E, H, I, nk);
+  if (rc != kOk) return rc;
+  const int grid = kNumCUs;
+  constexpr int waves = 11, gcap2 = kMxMaxGroups;
+  const size_t lds = decode_lds_bytes(E, H);
   static const bool lds_ok =
       hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;

@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
     float eps, uint16_t* __restrict__ t_out, float* __restrict__ logits,
-    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs, int epw) {
+    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs, int epw, int32_t* __restrict__ zero_e) {
   constexpr int kChunks = 64 * S;                // 16-byte chunks of a row, at most
   constexpr int J = (kChunks + 64 * W - 1) / (64 * W);  // chunks per thread and token
   __shared__ u32x4 t_lds[TT][kChunks];
@@ -279,6 +279,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   const int tok0 = blockIdx.x * TT;
   const int ntok = min(TT, n - tok0);
   const int e0 = (int)blockIdx.y * epw * W + wave;  // the wave's first expert
+  if (zero_e && blockIdx.x == 0 && blockIdx.y == 0 && tid < E) zero_e[tid] = 0;
   const int H8 = H >> 3;
   const int NC = (H + 127) >> 7;
 
@@ -421,26 +422,14 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   }
 }
 
-// Ranking keys of bf16 logits: the order-preserving unsigned image of the
-// value in the high 16 bits, 0xFFFF - expert in the low 16, so that a larger
-// key means (value larger, or value equal and expert lower).  Logits are bf16
-// values (low 16 bits zero); -inf pads rank below every finite logit.
-__device__ __forceinline__ uint32_t rank_key(float v, int e) {
-  const uint32_t b = __float_as_uint(v);
-  const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return (u & 0xFFFF0000u) | (uint32_t)(0xFFFF - e);
-}
-__device__ __forceinline__ float key_value(uint32_t key) {
-  const uint32_t hi = key & 0xFFFF0000u;
-  return __uint_as_float((hi & 0x80000000u) ? (hi ^ 0x80000000u) : (~hi & 0xFFFF0000u));
-}
 
 // Placement of pairs [p0, p1) of a stable counting sort by expert, given
 // base[e] (LDS) = the sorted position of the chunk's first pair of expert e.
 // Within a round of 1024 pairs a pair's rank among same-expert pairs comes
 // from ballots, so pairs keep flattened (token, slot) order inside each
 // expert, exactly as np.argsort(kind="stable").  Pairs whose expert id is out
-// of range are not placed (pair_pos = -1).  All 1024 threads call it.
+// of range are not placed (pair_pos = -1).  All threads of the workgroup (at
+// most 1024) call it; a round is blockDim.x pairs.
 __device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, int k, int E,
                                             int* base, int* wcnt,
                                             int32_t* __restrict__ sorted_pairs,
@@ -448,13 +437,14 @@ __device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, 
                                             int32_t* __restrict__ expert_ids,
                                             int32_t* __restrict__ pair_pos) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nthr = blockDim.x;
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int round0 = p0; round0 < p1; round0 += 1024) {
+  for (int round0 = p0; round0 < p1; round0 += nthr) {
     const int p = round0 + tid;
     const bool inb = p < p1;
     const int v = inb ? idx[p] : -1;
     const bool ok = inb && v >= 0 && v < E;
-    for (int i = tid; i < 16 * E; i += 1024) wcnt[(i / E) * 256 + (i % E)] = 0;
+    for (int i = tid; i < 16 * E; i += nthr) wcnt[(i / E) * 256 + (i % E)] = 0;
     __syncthreads();
     uint64_t same = __ballot(ok);
 #pragma unroll
@@ -477,7 +467,7 @@ __device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, 
       pair_pos[p] = -1;
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 1024) {
+    for (int e = tid; e < E; e += nthr) {
       int s = 0;
       for (int w = 0; w < 16; ++w) s += wcnt[w * 256 + e];
       base[e] += s;
@@ -576,14 +566,12 @@ __device__ __forceinline__ void select_range(const float* __restrict__ logits, i
 
 // Top-k + softmax of n <= 128 tokens and the grouping of their n*k pairs,
 // one workgroup (mlc-llm gating_softmax_topk + moe_cumsum / get_indices /
-// get_indptr, model/mlp_optimized.py:118-148).  zero_e (if not null): E ints
-// set to zero, the completion counts of the decode launch that follows.
+// get_indptr, model/mlp_optimized.py:118-148).
 __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
     const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out, int32_t* __restrict__ indptr,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos,
-    int32_t* __restrict__ zero_e) {
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
   __shared__ __align__(16) uint32_t keys[kSelLds];
   __shared__ int topi[kSelTok * 8];
   __shared__ float topv[kSelTok * 8];
@@ -595,7 +583,6 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
   for (int e = tid; e < E; e += 1024) {
     cnt[e] = 0;
     base[e] = 0;
-    if (zero_e) zero_e[e] = 0;
   }
   select_range(logits, 0, n, E, k, keys, topi, topv, idx_out, w_out, idx_lds, cnt);
   __syncthreads();
@@ -740,12 +727,14 @@ extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* 
 }
 
 // Logits of the n tokens into logits[n][E] (fp32 holding bf16 values), t,
-// and (pq != null, H % 32 == 0) the two fp8 pieces of t.  Eight experts per
-// wave (n <= 128) or all E per workgroup; TT tokens per workgroup share each gate row read.
+// and (pq != null, H % 32 == 0) the two fp8 pieces of t.  One expert per
+// wave (n <= 128) or all E per workgroup; TT tokens per workgroup share each
+// gate row read.  zero_e (if not null): E ints set to zero by workgroup (0, 0)
+// (the decode launch's completion counts).
 extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
                                         const void* gate_b, int n, int H, int E, float eps,
                                         void* t_out, float* logits, void* pq, void* pqs,
-                                        hipStream_t stream) {
+                                        void* zero_e, hipStream_t stream) {
   if (n == 0) return moe::kOk;
   if (H > 4096 || H % 8 || E > 256 || (pq && H % 32)) return moe::kErrUnsupported;
   const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
@@ -760,7 +749,7 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
 #define MOE_LG(PC, S, TT)                                                                        \
   hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT>), dim3((n + TT - 1) / TT, ey), \
                      dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs,   \
-                     epw)
+                     epw, (int32_t*)zero_e)
 #define MOE_LG_TT(PC, S, TTBIG)              \
   if (n <= 128) MOE_LG(PC, S, 1);            \
   else if (n <= 1024) MOE_LG(PC, S, 4);      \
@@ -779,9 +768,8 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
 extern "C" int moe_select_chunks(int n) { return (n + moe::kSelChunk - 1) / moe::kSelChunk; }
 
 // Top-k + softmax of the logits, then the grouping of the pairs: one
-// workgroup for n <= 128 (which zeroes counts[0..E) for the decode launch),
-// otherwise a select/count pass over chunks of kSelChunk tokens
-// (counts[chunks][E]) and a placement pass.
+// workgroup for n <= 128, otherwise a select/count pass over chunks of
+// kSelChunk tokens (counts[chunks][E]) and a placement pass.
 extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out,
                                        void* w_out, void* counts, void* indptr,
                                        void* sorted_pairs, void* token_indices,
@@ -793,7 +781,7 @@ extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k,
           *ei = (int32_t*)expert_ids, *pp = (int32_t*)pair_pos;
   if (n <= 128) {
     hipLaunchKernelGGL(moe::moe_select_permute_kernel, dim3(1), dim3(1024), 0, stream, logits, n,
-                       E, k, pi, pw, ip, sp, ti, ei, pp, (int32_t*)counts);
+                       E, k, pi, pw, ip, sp, ti, ei, pp);
   } else {
     const int nch = moe_select_chunks(n);
     int32_t* cnt = (int32_t*)counts;

@@ -200,11 +200,15 @@ def test_many_tokens_per_expert(native):
 
 @pytest.mark.parametrize("E,H,I,n,seed", [(8, 128, 64, 2000, 31), (32, 256, 64, 1030, 32),
                                           (128, 128, 64, 700, 33), (32, 2880, 64, 64, 34),
-                                          (32, 2880, 64, 1, 35), (12, 192, 64, 257, 36)])
+                                          (32, 2880, 64, 1, 35), (12, 192, 64, 257, 36),
+                                          (32, 2880, 2880, 1, 37), (32, 2880, 2880, 64, 38),
+                                          (32, 2880, 2880, 128, 39)])
 def test_block_internal_routing(native, E, H, I, n, seed):
     """The block's own router and grouping (logits kernel, then one workgroup of
-    top-k + grouping for n k <= 4096, or the chunked two-pass grouping above):
-    t, indices, weights and every grouping array bit-exact, output in tolerance."""
+    top-k + grouping for n k <= 4096, or the chunked two-pass grouping above;
+    at the 20B shape with n <= 128, top-k inside the logits launch and the
+    grouping inside the decode launch): t, indices, weights and every grouping
+    array bit-exact, output in tolerance."""
     p = O.make_params(seed, num_experts=E, hidden=H, inter=I)
     x = O.make_input(seed + 100, n, hidden=H)
     tr = O.block_forward(x, p)
