@@ -191,7 +191,8 @@ def main() -> int:
     value = n / (dt / args.steps)
     log(f"timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {value:.0f} tok/s")
 
-    mfma_bound = args.config.startswith("prefill") and E == 32
+    # both prefill configs average 48 or more pairs per expert: the tiled GEMM
+    mfma_bound = args.config.startswith("prefill")
     # At decode the block runs mlp1, the act encoding and mlp2 as one launch
     # (moe_mlp_decode) where the shape allows it: that launch is the one timed.
     fused = False
