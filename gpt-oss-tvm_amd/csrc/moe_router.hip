@@ -728,7 +728,7 @@ extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* 
 
 // Logits of the n tokens into logits[n][E] (fp32 holding bf16 values), t,
 // and (pq != null, H % 32 == 0) the two fp8 pieces of t.  One expert per
-// wave (n <= 128) or all E per workgroup; TT tokens per workgroup share each
+// wave (n <= 1024) or all E per workgroup; TT tokens per workgroup share each
 // gate row read.  zero_e (if not null): E ints set to zero by workgroup (0, 0)
 // (the decode launch's completion counts).
 extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
@@ -742,9 +742,10 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
   uint16_t* pt = (uint16_t*)t_out;
   uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
   constexpr int W = 8;
-  // experts per wave: one for n <= 128 (more workgroups per token), all of
-  // them above (the token's norm and t computed once)
-  const int epw = n <= 128 ? 1 : (E + W - 1) / W;
+  // experts per wave: one up to 1024 tokens (more workgroups per token
+  // tile), all of them above, where 8 tokens per workgroup share each gate
+  // row read (the tile's norm and t then computed once)
+  const int epw = n <= 1024 ? 1 : (E + W - 1) / W;
   const int ey = (E + W * epw - 1) / (W * epw);
 #define MOE_LG(PC, S, TT)                                                                        \
   hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT>), dim3((n + TT - 1) / TT, ey), \
