@@ -415,6 +415,27 @@ def test_mlp_decode_unsupported(native, block20b):
                           blk.mlp2_weight_scales, blk.mlp2_bias, 1.702, blk.swiglu_limit)
 
 
+@pytest.mark.parametrize("n,mode", [(64, "four"), (128, "four"), (100, "zipf")])
+def test_block_decode_skewed_routing(native, n, mode):
+    """The one-launch decode chain with heavy experts: every token on experts
+    0..3 (64 or 128 tokens each: several mlp1 batches of 16 and mlp2 batches of
+    15 per expert, so the completion counts span batches), or Zipf routing."""
+    H = 2880
+    if mode == "four":
+        p = O.make_params(25, num_experts=32)
+        gb = np.full(32, -10.0, np.float32)
+        gb[:4] = [10, 9, 8, 7]
+        p.gate_b[:] = O.f32_to_bf16(gb)
+    else:
+        p = O.make_params(26, num_experts=32, zipf_beta=1.0)
+    x = O.make_input(27, n)
+    tr = O.block_forward(x, p)
+    if mode == "four":
+        assert np.all(np.sort(tr.idx, axis=1) == [0, 1, 2, 3])
+    m = _check_block(make_block(p), x, tr)
+    print(f"decode {mode} n={n}: {m}")
+
+
 def test_block_120b_shape(native):
     p = O.make_params(seed=3, num_experts=128)
     x = O.make_input(13, 48)
