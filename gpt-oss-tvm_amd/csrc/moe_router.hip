@@ -246,9 +246,8 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
 // Router logits: workgroup (bx, by) of W waves computes the logits of tokens
 // [TT bx, TT bx + TT) for experts [W epw by, W epw (by + 1)): wave w takes
 // experts W (epw by + i) + w, i < epw, one after another (the next gate row
-// loads while the current one's dots run).  Small n spreads the experts over
-// several workgroups per token (epw = 1); larger n gives each workgroup all
-// of them, so the norm and t of a token are computed once.
+// loads while the current one's dots run).  Up to 1024 tokens epw = 1: the
+// experts spread over several workgroups per token.
 //  1  the threads load the token rows and the norm weight cooperatively (one
 //     16-byte chunk per thread and token); each wave loads its gate row;
 //  2  per token, fp64 sum of squares: per thread, fixed-order wave tree, then
@@ -262,7 +261,16 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
 //     fp32.
 // A product below 2^-126 in magnitude is rounded to an fp32 subnormal; no
 // logit above 2^-100 can change by it.
-template <bool kPieces, int S, int W, int TT>
+// kMfma (TT = 16, large n): step 3 runs on the fp64 matrix cores instead.
+// The workgroup covers experts [16 bpw by, 16 bpw (by + 1)) in blocks of 16;
+// wave w takes block w % bpw over the K slice w / bpw of W / bpw equal
+// slices.  v_mfma_f64_16x16x4 multiplies bf16 values widened to fp64 (exact
+// products) and accumulates in fp64: lane l feeds token row l % 16 and expert
+// column l % 16 at K position l / 16 of each step; the four lane groups walk
+// interleaved 16-byte chunks of the slice (any K order serves, as long as
+// both operands use the same).  The slices' partial sums are added in slice
+// order through LDS, then rounded as above.
+template <bool kPieces, int S, int W, int TT, bool kMfma>
 __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
@@ -289,7 +297,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
 #pragma unroll
     for (int i = 0; i < S; ++i) dst[i] = gr[min(lane + 64 * i, H8 - 1)];
   };
-  load_gate(e0, gv);
+  if constexpr (!kMfma) load_gate(e0, gv);
   // rows past n repeat the last token (computed, never stored)
   u32x4 xv[TT][J], wv[J];
 #pragma unroll
@@ -382,6 +390,82 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     }
   }
   __syncthreads();
+
+  if constexpr (kMfma) {
+    static_assert(TT == 16, "one MFMA row per token");
+    typedef double d4 __attribute__((ext_vector_type(4)));
+    const int bpw = epw;            // expert blocks per workgroup (divides W)
+    const int KS = W / bpw;         // K slices per block
+    const int ks = wave / bpw, wl = wave - ks * bpw;
+    const int eb = (int)blockIdx.y * bpw + wl;
+    const int r16 = lane & 15, g = lane >> 4;
+    const u32x4* gr = (const u32x4*)(gate_w + (size_t)min(eb * 16 + r16, E - 1) * H);
+    constexpr int NI = 16 * S;      // steps of four chunks over the padded row
+    constexpr int U = 4;            // steps per batch; divides NI / KS for KS <= 8
+    const int j0 = ks * (NI / KS), j1 = j0 + NI / KS;
+    d4 acc = {0.0, 0.0, 0.0, 0.0};
+    if (eb * 16 < E) {  // wave-uniform
+      // chunks past H8 are zero in both operands
+      auto fetch = [&](int j, u32x4* bb, u32x4* aa) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = 4 * (j + u) + g;
+          const bool in = c < H8;
+          const u32x4 bv = gr[min(c, H8 - 1)];
+          const u32x4 av = t_lds[r16][min(c, H8 - 1)];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            bb[u][d] = in ? bv[d] : 0u;
+            aa[u][d] = in ? av[d] : 0u;
+          }
+        }
+      };
+      u32x4 bc[U], ac[U];
+      fetch(j0, bc, ac);
+      for (int j = j0; j < j1; j += U) {
+        u32x4 bn[U], an[U];
+        if (j + U < j1) fetch(j + U, bn, an);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint32_t aw = ac[u][q >> 1], bw = bc[u][q >> 1];
+            const double a = (double)__uint_as_float((q & 1) ? (aw & 0xFFFF0000u) : (aw << 16));
+            const double b = (double)__uint_as_float((q & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+          }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          bc[u] = bn[u];
+          ac[u] = an[u];
+        }
+      }
+    }
+    // acc[i] of lane l: token row 4 i + l / 16, expert column l % 16
+    auto finish = [&](double d, int tt, int ex) {
+      if (tt < ntok && ex < E) {
+        const float v = bf2f(f64_to_bf16_via_f32(d));
+        logits[(size_t)(tok0 + tt) * E + ex] = bf2f(f2bf(__fadd_rn(v, bf2f(gate_b[ex]))));
+      }
+    };
+    if (KS == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) finish(acc[i], 4 * i + g, eb * 16 + r16);
+    } else {
+      __syncthreads();  // t_lds is free: [KS][bpw][16][16] partial sums
+      double* part = (double*)&t_lds[0][0];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[((ks * bpw + wl) * 16 + 4 * i + g) * 16 + r16] = acc[i];
+      __syncthreads();
+      for (int u = tid; u < bpw * 256; u += 64 * W) {
+        const int b = u >> 8, rc = u & 255;
+        double sum = part[b * 256 + rc];
+        for (int kk = 1; kk < KS; ++kk) sum += part[(kk * bpw + b) * 256 + rc];
+        finish(sum, rc >> 4, ((int)blockIdx.y * bpw + b) * 16 + (rc & 15));
+      }
+    }
+    return;
+  }
 
   for (int ei = 0; ei < epw; ++ei) {
     const int e = e0 + ei * W;
@@ -745,20 +829,30 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
   // experts per wave: one up to 1024 tokens (more workgroups per token
   // tile), all of them above, where 8 tokens per workgroup share each gate
   // row read (the tile's norm and t then computed once)
-  const int epw = n <= 1024 ? 1 : (E + W - 1) / W;
-  const int ey = (E + W * epw - 1) / (W * epw);
-#define MOE_LG(PC, S, TT)                                                                        \
-  hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT>), dim3((n + TT - 1) / TT, ey), \
-                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs,   \
-                     epw, (int32_t*)zero_e)
-#define MOE_LG_TT(PC, S, TTBIG)              \
-  if (n <= 128) MOE_LG(PC, S, 1);            \
-  else if (n <= 1024) MOE_LG(PC, S, 4);      \
-  else MOE_LG(PC, S, TTBIG)
+  // Above 1024 tokens: 16 tokens per workgroup on the fp64 matrix cores,
+  // epw = expert blocks of 16 per workgroup, the largest power of two up to
+  // min(blocks, W) that still gives 256 workgroups (one per CU: the t tile
+  // takes 96-128 KB of LDS)
+  const bool mfma = n > 1024;
+  int epw = 1;
+  if (mfma) {
+    const int nblk = (E + 15) / 16, gx = (n + 15) / 16;
+    while (epw * 2 <= std::min(nblk, W)) epw *= 2;
+    while (epw > 1 && gx * ((nblk + epw - 1) / epw) < 256) epw /= 2;
+  }
+  const int ey = mfma ? ((E + 15) / 16 + epw - 1) / epw : (E + W - 1) / W;
+#define MOE_LG(PC, S, TT, MF)                                                                     \
+  hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT, MF>),                           \
+                     dim3((n + TT - 1) / TT, ey), dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, \
+                     E, eps, pt, logits, q, qs, epw, (int32_t*)zero_e)
+#define MOE_LG_TT(PC, S)                        \
+  if (n <= 128) MOE_LG(PC, S, 1, false);        \
+  else if (n <= 1024) MOE_LG(PC, S, 4, false);  \
+  else MOE_LG(PC, S, 16, true)
   if (H <= 64 * 6 * 8) {
-    if (pq) { MOE_LG_TT(true, 6, 8); } else { MOE_LG_TT(false, 6, 8); }
+    if (pq) { MOE_LG_TT(true, 6); } else { MOE_LG_TT(false, 6); }
   } else {
-    if (pq) { MOE_LG_TT(true, 8, 4); } else { MOE_LG_TT(false, 8, 4); }
+    if (pq) { MOE_LG_TT(true, 8); } else { MOE_LG_TT(false, 8); }
   }
 #undef MOE_LG_TT
 #undef MOE_LG

@@ -202,7 +202,9 @@ def test_many_tokens_per_expert(native):
                                           (128, 128, 64, 700, 33), (32, 2880, 64, 64, 34),
                                           (32, 2880, 64, 1, 35), (12, 192, 64, 257, 36),
                                           (32, 2880, 2880, 1, 37), (32, 2880, 2880, 64, 38),
-                                          (32, 2880, 2880, 128, 39)])
+                                          (32, 2880, 2880, 128, 39), (32, 2880, 64, 4096, 40),
+                                          (128, 2880, 64, 1100, 41), (128, 256, 64, 4100, 42),
+                                          (40, 192, 64, 1500, 43)])
 def test_block_internal_routing(native, E, H, I, n, seed):
     """The block's own router and grouping (logits kernel, then one workgroup of
     top-k + grouping for n k <= 4096, or the chunked two-pass grouping above;
