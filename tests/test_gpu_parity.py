@@ -206,11 +206,12 @@ def test_many_tokens_per_expert(native):
                                           (128, 2880, 64, 1100, 41), (128, 256, 64, 4100, 42),
                                           (40, 192, 64, 1500, 43)])
 def test_block_internal_routing(native, E, H, I, n, seed):
-    """The block's own router and grouping (logits kernel, then one workgroup of
-    top-k + grouping for n k <= 4096, or the chunked two-pass grouping above;
-    at the 20B shape with n <= 128, top-k inside the logits launch and the
-    grouping inside the decode launch): t, indices, weights and every grouping
-    array bit-exact, output in tolerance."""
+    """The block's own router and grouping (logits kernel — VALU fp64 dots up
+    to 1024 tokens, fp64 MFMA dots above — then one workgroup of top-k +
+    grouping for n k <= 4096, or the chunked two-pass grouping above; at the
+    20B shape with n <= 128 the experts run in the one decode launch): t,
+    indices, weights and every grouping array bit-exact, output in
+    tolerance."""
     p = O.make_params(seed, num_experts=E, hidden=H, inter=I)
     x = O.make_input(seed + 100, n, hidden=H)
     tr = O.block_forward(x, p)
