@@ -135,7 +135,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode64", choices=sorted(CONFIGS))
     ap.add_argument("--weight-sets", type=int, default=3)
-    ap.add_argument("--cpu-tokens", type=int, default=24)
+    ap.add_argument("--cpu-tokens", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 512 MiB (the known-size kernel that "
