@@ -123,7 +123,7 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
       nk * (size_t)H * 4,     // y        fp32 [n*k, H]
       (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
-      // counts int32 [chunks of 64 tokens, E]; for n <= 128 its first E hold
+      // counts int32 [chunks of 16 tokens, E]; for n <= 128 its first E hold
       // the decode launch's per-expert mlp1 completion counts
       (size_t)moe_select_chunks((int)n) * E * 4,
   };

@@ -1000,22 +1000,35 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   // MOE_MX_WAVES / MOE_MX_WG_PER_CU override (tuning runs).
   static const int waves_env = [] {
     const char* v = getenv("MOE_MX_WAVES");
-    const int w = v ? atoi(v) : 11;
-    return w < 1 ? 1 : w > 12 ? 12 : w;
+    const int w = v ? atoi(v) : 0;
+    return w < 1 ? 0 : w > 12 ? 12 : w;
   }();
-  // the generic (24-chunk) kernel is built for at most 8 waves
-  const int waves = NC == 23 ? waves_env : min(waves_env, 8);
+  const int tpg = 16 / pieces;
+  const int gbytes = moe::mx_group_bytes(NC == 23 ? 23 : moe::kMxMaxChunks);
+  // scale staging, unit prefix, indptr, one batch's sorted_pairs, tile counter
+  auto fixed_of = [&](int w) {
+    return w * 16 * G + 2 * (E + 1) * 4 + (moe::kMxRowMap + 4) * 4;
+  };
+  const int want = min(moe::kMxMaxGroups, (max_tokens + tpg - 1) / tpg);
+  // 11 waves, fewer (down to 8) where each wave's scale staging would leave
+  // LDS for fewer token groups than the batch needs (E = 128 at 11 waves:
+  // two groups, 16-token batches; at 10: three): a group more per staging
+  // serves more tokens per weight read than a wave more in flight.  The
+  // generic (24-chunk) kernel is built for at most 8 waves.
+  int waves = waves_env;
+  if (waves == 0) {
+    waves = 11;
+    while (waves > 8 && (moe::kLdsBytes - fixed_of(waves)) / gbytes < want) --waves;
+  }
+  if (NC != 23) waves = min(waves, 8);
   static const int wg_per_cu = [] {
     const char* v = getenv("MOE_MX_WG_PER_CU");
     const int t = v ? atoi(v) : 1;
     return t < 1 ? 1 : t;
   }();
-  const int tpg = 16 / pieces;
-  const int gbytes = moe::mx_group_bytes(NC == 23 ? 23 : moe::kMxMaxChunks);
-  // scale staging, unit prefix, indptr, one batch's sorted_pairs, tile counter
-  const int fixed = waves * 16 * G + 2 * (E + 1) * 4 + (moe::kMxRowMap + 4) * 4;
+  const int fixed = fixed_of(waves);
   const int gfit = (moe::kLdsBytes - fixed) / gbytes;
-  const int gcap = min(min(moe::kMxMaxGroups, gfit), (max_tokens + tpg - 1) / tpg);
+  const int gcap = min(want, gfit);
   if (gcap < 1) return moe::kErrUnsupported;
   const size_t lds = (size_t)gcap * gbytes + fixed;
   // Upper bound of the work units (16-row tiles x token batches) over the

@@ -676,8 +676,10 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
               pair_pos);
 }
 
-// Tokens per chunk of the large-n grouping.
-constexpr int kSelChunk = 64;
+// Tokens per chunk of the large-n grouping.  Ranking costs E^2 key
+// compares per token (16 K at E = 128), so small chunks: 16 workgroups at
+// 256 tokens rather than 4.
+constexpr int kSelChunk = 16;
 
 // Large n, first pass: top-k + softmax of the kSelChunk tokens of chunk
 // blockIdx.x and the chunk's expert histogram, counts[chunk][E].

@@ -115,5 +115,5 @@ def test_workspace_layout(native):
     offs = native.workspace_layout(n, E, k, H, I)
     assert len(offs) == 14 and offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert offs[11] + n * k * H * 4 <= offs[12]             # y before logits
-    assert offs[13] + (n + 63) // 64 * E * 4 <= total       # counts last
+    assert offs[13] + (n + 15) // 16 * E * 4 <= total       # counts last
     assert native.workspace_bytes(n, E, k, H + 1, I) == 0
