@@ -1080,10 +1080,21 @@ int moe_launch_mx_gemv(const void* packed, int rows, int pieces, const void* ind
   return moe::kErrUnsupported;
 }
 
+// Waves per workgroup of the decode launch (MOE_DECODE_WAVES overrides, 8-12:
+// tuning runs).
+static int decode_waves() {
+  static const int w = [] {
+    const char* v = getenv("MOE_DECODE_WAVES");
+    const int x = v ? atoi(v) : 11;
+    return x < 8 ? 8 : x > 12 ? 12 : x;
+  }();
+  return w;
+}
+
 static size_t decode_lds_bytes(int E, int H) {
   using namespace moe;
-  return (size_t)kMxMaxGroups * mx_group_bytes(23) + 11 * 16 * (H / 32) + 3 * (E + 1) * 4 +
-         (kMxRowMap + 4) * 4;
+  return (size_t)kMxMaxGroups * mx_group_bytes(23) + decode_waves() * 16 * (H / 32) +
+         3 * (E + 1) * 4 + (kMxRowMap + 4) * 4;
 }
 
 // kOk when moe_launch_mx_decode can run this shape on the current device,
@@ -1127,7 +1138,8 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
   const int rc = moe_mx_decode_check(E, H, I, nk);
   if (rc != kOk) return rc;
   const int grid = kNumCUs;
-  constexpr int waves = 11, gcap2 = kMxMaxGroups;
+  const int waves = decode_waves();
+  constexpr int gcap2 = kMxMaxGroups;
   const size_t lds = decode_lds_bytes(E, H);
   static const bool lds_ok =
       hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
