@@ -6,6 +6,7 @@
 // as called at model/mlp_optimized.py:119-148.
 #include <algorithm>
 #include <climits>
+#include <cstdlib>
 
 #include "moe_common.h"
 
@@ -835,7 +836,11 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
   // epw = expert blocks of 16 per workgroup, the largest power of two up to
   // min(blocks, W) that still gives 256 workgroups (one per CU: the t tile
   // takes 96-128 KB of LDS)
-  const bool mfma = n > 1024;
+  static const int mfma_min = [] {  // MOE_ROUTER_MFMA_MIN overrides (tuning runs)
+    const char* v = getenv("MOE_ROUTER_MFMA_MIN");
+    return v ? atoi(v) : 1024;
+  }();
+  const bool mfma = n > mfma_min;
   int epw = 1;
   if (mfma) {
     const int nblk = (E + 15) / 16, gx = (n + 15) / 16;
@@ -848,9 +853,9 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
                      dim3((n + TT - 1) / TT, ey), dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, \
                      E, eps, pt, logits, q, qs, epw, (int32_t*)zero_e)
 #define MOE_LG_TT(PC, S)                        \
-  if (n <= 128) MOE_LG(PC, S, 1, false);        \
-  else if (n <= 1024) MOE_LG(PC, S, 4, false);  \
-  else MOE_LG(PC, S, 16, true)
+  if (mfma) MOE_LG(PC, S, 16, true);            \
+  else if (n <= 128) MOE_LG(PC, S, 1, false);   \
+  else MOE_LG(PC, S, 4, false)
   if (H <= 64 * 6 * 8) {
     if (pq) { MOE_LG_TT(true, 6); } else { MOE_LG_TT(false, 6); }
   } else {
