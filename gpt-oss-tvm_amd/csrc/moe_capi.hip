@@ -41,14 +41,15 @@ int moe_launch_mx_gemm(const void* packed, int rows, int pieces, const void* ind
                        int K, int rows_active, int swiglu, float alpha, float limit, void* out,
                        int out_ld, void* out_qs, hipStream_t stream);
 int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N, void* out,
-                      hipStream_t stream);
+                      const void* status, hipStream_t stream);
 int moe_mx_decode_check(int E, int H, int I, int nk);
+int moe_decode_spin_limit_exchange(int polls);
 int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* sorted_pairs, int k_top, const void* blocks1,
                          const void* scales1, const void* bias1, const void* blocks2,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
-                         hipStream_t stream);
+                         void* status, hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
                       hipStream_t stream);
 }
@@ -96,7 +97,8 @@ int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indpt
                             alpha, limit, out, out_ld, s);
 }
 
-constexpr int kNumRegions = 14;
+constexpr int kNumRegions = 15;
+constexpr int kRegionSync = 14;  // decode launch: E completion counts, then the status word
 constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
 // fp8 pieces of the fp32 SwiGLU output act, mlp2's operand: three carry
 // about 12 significant bits (relative to each 32-block's largest magnitude),
@@ -123,9 +125,11 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
       nk * (size_t)H * 4,     // y        fp32 [n*k, H]
       (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
-      // counts int32 [chunks of 16 tokens, E]; for n <= 128 its first E hold
-      // the decode launch's per-expert mlp1 completion counts
+      // counts int32 [chunks of 16 tokens, E] (the large-n grouping)
       (size_t)moe_select_chunks((int)n) * E * 4,
+      // sync int32 [E + 1]: the decode launch's per-expert mlp1 completion
+      // counts and its status word (zeroed by the logits kernel)
+      (size_t)(E + 1) * 4,
   };
   size_t o = 0;
   for (int i = 0; i < kNumRegions; ++i) {
@@ -150,6 +154,8 @@ const char* moe_status_string(int status) {
     case MOE_ERR_UNSUPPORTED: return "unsupported parameter value";
     case MOE_ERR_LAUNCH: return "kernel launch failed";
     case MOE_ERR_WORKSPACE: return "workspace too small";
+    case MOE_ERR_INCOMPLETE:
+      return "the decode launch's bounded wait gave up: outputs are NaN";
     default: return "unknown status";
   }
 }
@@ -319,7 +325,7 @@ int moe_mlp_decode(const void* t_pieces, const int32_t* indptr, const int32_t* s
   return moe_launch_mx_decode(t_pieces, (int)n, indptr, sorted_pairs, (int)k, mlp1_blocks,
                               mlp1_scales, mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E,
                               (int)H, (int)I, (int)(n * k), alpha, limit, act_pieces, y, done,
-                              as_stream(stream));
+                              done + E, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -330,7 +336,7 @@ int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_
   if (n == 0) return MOE_OK;
   if (!y || !w || !out) return MOE_ERR_NULL;
   if (!aligned16(y) || ((uintptr_t)out & 7u) || (x && ((uintptr_t)x & 7u))) return MOE_ERR_ALIGN;
-  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)N, out, as_stream(stream));
+  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)N, out, nullptr, as_stream(stream));
 }
 
 int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, float limit, float* out,
@@ -350,7 +356,7 @@ size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I
 }
 
 int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                         size_t offsets[14]) {
+                         size_t offsets[15]) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (!offsets) return MOE_ERR_NULL;
@@ -396,12 +402,13 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   const int nk = (int)(n * k);
   float* logits = (float*)(ws + off[12]);
   int32_t* counts = (int32_t*)(ws + off[13]);
+  int32_t* sync = (int32_t*)(ws + off[kRegionSync]);  // [E] counts, [E] status
   const bool gemm = (int64_t)nk >= kGemmMinTokens * E;
-  // norm, t, its pieces and the logits (and counts[0..E) = 0 for the decode
-  // launch); then top-k, softmax and grouping
+  // norm, t, its pieces and the logits (and sync[0..E] = 0: the decode
+  // launch's counts and status); then top-k, softmax and grouping
   void* t_qs = (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT);
   if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
-                                     logits, t_pk, t_qs, counts, s)))
+                                     logits, t_pk, t_qs, sync, s)))
     return rc;
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
                                     ei, pp, s)))
@@ -411,8 +418,10 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   if (!gemm && n <= 128) {
     rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
                               mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
-                              (int)I, nk, alpha, limit, act_pk, y, counts, s);
-    if (rc == MOE_OK) return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
+                              (int)I, nk, alpha, limit, act_pk, y, sync, sync + E, s);
+    // a nonzero status (a wait gave up) makes the gating write NaN rows
+    if (rc == MOE_OK)
+      return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s);
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }
   // With the tiled GEMM, mlp1's epilogue writes act's three pieces directly
@@ -454,7 +463,26 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
                                  0.f, y, (int)H, s)))
       return rc;
   }
-  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, s);
+  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, nullptr, s);
+}
+
+int moe_set_decode_spin_limit(int polls) { return moe_decode_spin_limit_exchange(polls); }
+
+int moe_block_status(const void* workspace, int64_t n, int64_t E, int64_t k, int64_t H,
+                     int64_t I, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!workspace) return MOE_ERR_NULL;
+  size_t off[kNumRegions], total;
+  layout(n, E, k, H, I, off, &total);
+  int32_t status = 0;
+  hipStream_t s = as_stream(stream);
+  if (hipMemcpyAsync(&status, (const char*)workspace + off[kRegionSync] + (size_t)E * 4, 4,
+                     hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return MOE_ERR_LAUNCH;
+  return status == 0 ? MOE_OK : MOE_ERR_INCOMPLETE;
 }
 
 }  // extern "C"

@@ -11,13 +11,24 @@
 namespace moe {
 
 // One thread per 4 output columns of one token; grid (ceil(N/1024), n).
+// status (if not null): nonzero when the producer of y reported incomplete
+// results (the decode launch's bounded wait gave up); every output is then
+// written as NaN, so a wrong result cannot pass for a right one.
 __global__ __launch_bounds__(256) void moe_gating_kernel(const float* __restrict__ y,
                                                          const uint16_t* __restrict__ w,
                                                          const uint16_t* __restrict__ x, int k,
-                                                         int N, uint16_t* __restrict__ out) {
+                                                         int N, uint16_t* __restrict__ out,
+                                                         const int* __restrict__ status) {
+  // multiply and add round separately, as the reference writes them: no
+  // contraction into fma (__fmul_rn / __fadd_rn alone do not prevent it)
+#pragma clang fp contract(off)
   const int tok = blockIdx.y;
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= N) return;
+  if (status && *status != 0) {
+    *(uint2*)(out + (size_t)tok * N + c) = make_uint2(0x7FC07FC0u, 0x7FC07FC0u);
+    return;
+  }
   // all k loads first (k <= 8), then the in-order sum
   f32x4 v[8];
   float wr[8];
@@ -33,7 +44,7 @@ __global__ __launch_bounds__(256) void moe_gating_kernel(const float* __restrict
   for (int r = 0; r < 8; ++r) {
     if (r < k) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[r][i], wr[r]));
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + v[r][i] * wr[r];
     }
   }
   uint16_t o[4];
@@ -64,11 +75,12 @@ __global__ __launch_bounds__(256) void moe_swiglu_kernel(const float2* __restric
 }  // namespace moe
 
 extern "C" int moe_launch_gating(const void* y, const void* w, const void* x, int n, int k, int N,
-                                 void* out, hipStream_t stream) {
+                                 void* out, const void* status, hipStream_t stream) {
   if (n == 0) return moe::kOk;
   const dim3 grid((N / 4 + 255) / 256, n);
   hipLaunchKernelGGL(moe::moe_gating_kernel, grid, dim3(256), 0, stream, (const float*)y,
-                     (const uint16_t*)w, (const uint16_t*)x, k, N, (uint16_t*)out);
+                     (const uint16_t*)w, (const uint16_t*)x, k, N, (uint16_t*)out,
+                     (const int*)status);
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }
 

@@ -22,6 +22,7 @@ enum Status : int {
   kErrUnsupported = -4,
   kErrLaunch = -5,
   kErrWorkspace = -6,
+  kErrIncomplete = -7,
 };
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }

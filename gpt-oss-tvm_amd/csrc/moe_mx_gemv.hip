@@ -25,6 +25,7 @@
 //      i.e. one whole MXFP4 block: block 4 * chunk + g of that row
 //   scale_a / scale_b of lane (r, g) = the E8M0 of K block g of row / column r
 //   D  column r (weight row), elements i = 0..3 -> rows 4 g + i
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -788,22 +789,26 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
 // Coherence across the XCDs' L2s without writing back or invalidating them:
 // the act pieces are stored and (by the staging DMA) loaded with device
 // scope (sc1), the code sequence of agent-scope atomic stores and loads, and
-// the counts are agent-scope atomics.  A workgroup adds its count after a
-// barrier, which waits for all of its stores; a waiting workgroup issues its
-// staging only after its count load returned the target.
+// the counts are agent-scope atomics.  Every wave waits for its own stores
+// to complete (vmcnt(0): on gfx9 the count covers stores, and a completed
+// sc1 store is visible at device scope) before the workgroup barrier after
+// which one thread adds the count; a waiting workgroup issues its staging
+// only after its count load returned the target.  The barrier alone would
+// not order them: a workgroup-scope fence waits for LDS traffic only.
 //
 // Requirements (checked by the launcher): H == I with 23 chunks of 128, one
 // workgroup per CU and every workgroup resident at once (the grid is the CU
 // count and nothing else runs on the device: a workgroup waiting in phase 2
 // relies on the phase-1 work of the others), at most 64 mlp1 batches, and
-// done[0..E) zero at launch.  The wait is bounded (kDecodeSpinMax polls):
-// past the bound it gives up, so the launch always ends.
+// done[0..E) and *status zero at launch.  The wait is bounded (spin_max
+// polls): a workgroup that gives up adds 1 to *status and goes on, so the
+// launch always ends; its y rows are then wrong and the status says so.
 constexpr int kDecodeGroups1 = 2;  // mlp1 batch: 2 groups of 8 tokens
 template <class T>
 __device__ __forceinline__ void store_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-constexpr int kDecodeSpinMax = 1 << 20;
+constexpr int kDecodeSpinMax = 1 << 20;  // about a second of polling
 __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
@@ -811,7 +816,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint16_t* __restrict__ bias1, const uint8_t* __restrict__ blocks2,
     const uint8_t* __restrict__ scales2, const uint16_t* __restrict__ bias2, int H, int E,
     int gcap2, float alpha, float limit, uint8_t* aq, uint8_t* aqs, float* __restrict__ y,
-    int* done, int xcds) {
+    int* done, int* status, int spin_max, int xcds) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kGroupBytes = mx_group_bytes(23);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -897,8 +902,9 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
         }
       }
     }
-    // Publish: the barrier waits for every wave's stores (vmcnt(0)); being
-    // device-scope they are then visible to every XCD, so the count can go.
+    // Publish: each wave waits until its device-scope stores have completed
+    // (visible to every XCD), then the barrier, then the count.
+    wait_vmcnt<0>();
     __syncthreads();
     if (threadIdx.x == 0)
       __hip_atomic_fetch_add(done + s1.e, s1.len, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -908,11 +914,16 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   auto wait_mlp1 = [&](int e, int, int) {
     if (threadIdx.x == 0) {
       const int target = ntiles1 * ((ipl[e + 1] - ipl[e] + tpb1 - 1) / tpb1);
-      for (int it = 0; it < kDecodeSpinMax; ++it) {
-        if (__hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target)
+      bool seen = false;
+      for (int it = 0; it < spin_max; ++it) {
+        if (__hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+          seen = true;
           break;
+        }
         __builtin_amdgcn_s_sleep(2);
       }
+      // gave up: the staged pieces may be incomplete; report it
+      if (!seen) __hip_atomic_fetch_add(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     lds_barrier();  // the staging's sc1 loads are issued after the count was seen
   };
@@ -1097,6 +1108,9 @@ static size_t decode_lds_bytes(int E, int H) {
          3 * (E + 1) * 4 + (kMxRowMap + 4) * 4;
 }
 
+// Polls of the decode launch's bounded wait (moe_set_decode_spin_limit).
+static std::atomic<int> g_decode_spin_max{moe::kDecodeSpinMax};
+
 // kOk when moe_launch_mx_decode can run this shape on the current device,
 // else kErrUnsupported (the caller then runs mlp1, the encoding and mlp2 as
 // separate launches).
@@ -1111,6 +1125,17 @@ int moe_mx_decode_check(int E, int H, int I, int nk) {
   if (cus < grid) return kErrUnsupported;  // every workgroup must be resident
   constexpr int gcap2 = kMxMaxGroups;
   if (decode_lds_bytes(E, H) > (size_t)kLdsBytes) return kErrUnsupported;
+  // one workgroup of this size and LDS must fit on a CU (registers included)
+  static const bool lds_ok =
+      hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
+  if (!lds_ok) return kErrLaunch;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)moe_mx_decode_kernel,
+                                                   64 * decode_waves(),
+                                                   decode_lds_bytes(E, H)) != hipSuccess)
+    return kErrLaunch;
+  if (per_cu < 1) return kErrUnsupported;
   // Batches are bounded by (experts holding pairs) + nk / tokens per batch.
   // Phase 1 needs one segment per workgroup whose share (at most
   // 4 ceil(quads / floor(grid / batches)) tiles) fits the LDS act tile of 96.
@@ -1125,26 +1150,23 @@ int moe_mx_decode_check(int E, int H, int I, int nk) {
 
 // The decode chain in one launch (moe_mx_decode_kernel): t pieces (2, rows
 // n) -> act pieces (3, rows nk, written) -> y (fp32 [nk][H], rows by pair).
-// done: E ints, zero at launch.
+// done: E ints and status: one int, all zero at launch; status counts the
+// workgroups whose bounded wait gave up (their y rows are wrong).
 int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* sorted_pairs, int k_top, const void* blocks1,
                          const void* scales1, const void* bias1, const void* blocks2,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
-                         hipStream_t stream) {
+                         void* status, hipStream_t stream) {
   using namespace moe;
   if (nk <= 0) return kOk;
-  if (!done) return kErrUnsupported;
+  if (!done || !status) return kErrUnsupported;
   const int rc = moe_mx_decode_check(E, H, I, nk);
   if (rc != kOk) return rc;
   const int grid = kNumCUs;
   const int waves = decode_waves();
   constexpr int gcap2 = kMxMaxGroups;
   const size_t lds = decode_lds_bytes(E, H);
-  static const bool lds_ok =
-      hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
-  if (!lds_ok) return kErrLaunch;
   const uint8_t* tq = (const uint8_t*)t_packed;
   uint8_t* aq = (uint8_t*)act_packed;
   hipLaunchKernelGGL(moe_mx_decode_kernel, dim3(grid), dim3(64 * waves), lds, stream, tq,
@@ -1153,8 +1175,15 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                      (const uint8_t*)scales1, (const uint16_t*)bias1, (const uint8_t*)blocks2,
                      (const uint8_t*)scales2, (const uint16_t*)bias2, H, E, gcap2, alpha, limit,
                      aq, aq + moe_pieces_q_bytes(nk, I, 3), (float*)y, (int*)done,
+                     (int*)status, g_decode_spin_max.load(std::memory_order_relaxed),
                      grid % kNumXcds == 0 ? kNumXcds : 1);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// Bound of the decode launch's wait, in polls (about 1 us each); a negative
+// value restores the default.  Returns the previous bound.
+int moe_decode_spin_limit_exchange(int polls) {
+  return g_decode_spin_max.exchange(polls < 0 ? moe::kDecodeSpinMax : polls);
 }
 
 }  // extern "C"

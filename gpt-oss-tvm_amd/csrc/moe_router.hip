@@ -288,7 +288,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   const int tok0 = blockIdx.x * TT;
   const int ntok = min(TT, n - tok0);
   const int e0 = (int)blockIdx.y * epw * W + wave;  // the wave's first expert
-  if (zero_e && blockIdx.x == 0 && blockIdx.y == 0 && tid < E) zero_e[tid] = 0;
+  if (zero_e && blockIdx.x == 0 && blockIdx.y == 0 && tid <= E) zero_e[tid] = 0;
   const int H8 = H >> 3;
   const int NC = (H + 127) >> 7;
 
@@ -816,8 +816,8 @@ extern "C" int moe_launch_router(const void* x, const void* norm_w, const void* 
 // Logits of the n tokens into logits[n][E] (fp32 holding bf16 values), t,
 // and (pq != null, H % 32 == 0) the two fp8 pieces of t.  One expert per
 // wave (n <= 1024) or all E per workgroup; TT tokens per workgroup share each
-// gate row read.  zero_e (if not null): E ints set to zero by workgroup (0, 0)
-// (the decode launch's completion counts).
+// gate row read.  zero_e (if not null): E + 1 ints set to zero by workgroup
+// (0, 0) (the decode launch's completion counts and its status word).
 extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate_w,
                                         const void* gate_b, int n, int H, int E, float eps,
                                         void* t_out, float* logits, void* pq, void* pqs,

@@ -200,7 +200,7 @@ class MLPBlock(torch.nn.Module):
         t_pk = _native.quantize_pieces(t, 2)
         rec("pieces_t", 1)
         if fused_decode:
-            done = torch.zeros(self.num_experts, dtype=torch.int32, device=x.device)
+            done = torch.zeros(self.num_experts + 1, dtype=torch.int32, device=x.device)
             rec("mlp_decode", 0)
             y, act_pk = _native.mlp_decode(
                 t_pk, n, perm["indptr"], perm["sorted_pairs"], k, self.mlp1_weight_blocks,

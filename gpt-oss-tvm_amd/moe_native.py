@@ -53,6 +53,8 @@ _SIGS = {
     "moe_workspace_layout": ([_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)], _INT),
     "moe_block_forward": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                            _F, _F, _F, _P, _P, _SZ, _P], _INT),
+    "moe_block_status": ([_P, _I64, _I64, _I64, _I64, _I64, _P], _INT),
+    "moe_set_decode_spin_limit": ([_INT], _INT),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -257,6 +259,9 @@ def mlp_decode(t_pieces, n, indptr, sorted_pairs, k, w1, s1, b1, w2, s2, b2, alp
 
     Same results as mlp1_swiglu -> quantize_pieces(act, 3) -> mlp2.  Raises
     RuntimeError ("unsupported parameter value") where the launch does not apply.
+    done: int32 [E + 1], zero on entry; afterwards done[:E] holds the per-expert
+    mlp1 tile counts and done[E] the status word (nonzero: a bounded wait gave
+    up and y is incomplete).
     """
     E, N2, G, _ = w1.shape
     inter, H = N2 // 2, G * 32
@@ -273,7 +278,8 @@ def mlp_decode(t_pieces, n, indptr, sorted_pairs, k, w1, s1, b1, w2, s2, b2, alp
     if act_pieces is None:
         act_pieces = torch.empty(pieces_bytes(n * k, inter, 3), dtype=torch.uint8, device=dev)
     if done is None:
-        done = torch.zeros(E, dtype=torch.int32, device=dev)
+        done = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    _expect(done, "done", torch.int32, (E + 1,))
     if y is None:
         y = torch.empty((n * k, H), dtype=torch.float32, device=dev)
     _check(_lib.moe_mlp_decode(_ptr(t_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E, H,
@@ -313,8 +319,12 @@ def workspace_bytes(n, E, k, H, inter) -> int:
     return int(_lib.moe_workspace_bytes(n, E, k, H, inter))
 
 
+WORKSPACE_REGIONS = ("t", "idx", "w", "indptr", "sorted_pairs", "token_indices", "expert_ids",
+                     "pair_pos", "t_pieces", "act", "act_pieces", "y", "logits", "counts", "sync")
+
+
 def workspace_layout(n, E, k, H, inter) -> list[int]:
-    offs = (_SZ * 14)()
+    offs = (_SZ * len(WORKSPACE_REGIONS))()
     _check(_lib.moe_workspace_layout(n, E, k, H, inter, offs), "moe_workspace_layout")
     return list(offs)
 
@@ -334,3 +344,16 @@ def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
         _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
         workspace.numel(), _stream()), "moe_block_forward")
     return out
+
+
+def block_status(workspace, n, E, k, H, inter) -> int:
+    """Status of the last block_forward on this workspace: 0, or the negative
+    MOE_ERR_INCOMPLETE code when its decode launch's bounded wait gave up (its
+    outputs are NaN).  Synchronises the current stream."""
+    return int(_lib.moe_block_status(_ptr(workspace), n, E, k, H, inter, _stream()))
+
+
+def set_decode_spin_limit(polls: int) -> int:
+    """Bound of the decode launch's wait in polls (negative: the default); returns
+    the previous bound.  Tests set 0 to force the reported give-up path."""
+    return int(_lib.moe_set_decode_spin_limit(polls))

@@ -15,7 +15,12 @@
  *     the default stream;
  *   - the return value is MOE_OK or a negative MOE_ERR_* code; on error no
  *     kernel was launched and no output was written.  Nothing throws across
- *     the ABI.
+ *     the ABI.  One failure can only be seen after the kernels ran: the
+ *     decode launch (moe_mlp_decode, and moe_block_forward for n <= 128)
+ *     waits for other workgroups of its own launch, and if that bounded wait
+ *     gives up it reports so in a device status word; the block then writes
+ *     NaN to every output element and moe_block_status() returns
+ *     MOE_ERR_INCOMPLETE.
  *
  * Tensor conventions: bf16 tensors are uint16_t bit patterns, row-major,
  * 16-byte aligned.  MXFP4 weights stay in the checkpoint layout of
@@ -46,6 +51,7 @@ extern "C" {
 #define MOE_ERR_UNSUPPORTED (-4) /* valid but unsupported parameter value */
 #define MOE_ERR_LAUNCH (-5)      /* the HIP runtime rejected a launch */
 #define MOE_ERR_WORKSPACE (-6)   /* workspace smaller than moe_workspace_bytes() */
+#define MOE_ERR_INCOMPLETE (-7)  /* the decode launch's bounded wait gave up (outputs are NaN) */
 
 typedef void* moe_stream_t; /* a hipStream_t */
 
@@ -177,14 +183,17 @@ MOE_API int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_
  * model/mlp_optimized.py:214-660 (fp32 semantics of model/mlp.py:387-395).
  * t_pieces, indptr, sorted_pairs and the weights as for moe_mlp1_swiglu and
  * moe_mlp2; act_pieces: moe_pieces_bytes(n*k, I, 3) bytes, written with the
- * pieces moe_mlp2 takes; done: E int32, zero on entry (left holding per-expert
- * tile counts) -> y [n*k, H] fp32, row = pair.  MOE_ERR_UNSUPPORTED unless
- * H == I (2817..2944), n <= 128, the device has 256 or more CUs and the shape's
- * batches fit the launch (always at gpt-oss-20b's E = 32); the caller then runs
- * the three calls.  The launch keeps one workgroup on each of 256 CUs and its
- * mlp2 phase waits for the other workgroups' mlp1 results: work running on the
- * device at the same time delays it, and past a bound of about a second of
- * waiting the result is wrong.
+ * pieces moe_mlp2 takes; done: E + 1 int32, zero on entry (left holding the
+ * per-expert tile counts in done[0..E) and the status word in done[E]) ->
+ * y [n*k, H] fp32, row = pair.  MOE_ERR_UNSUPPORTED unless H == I
+ * (2817..2944), n <= 128, the device has 256 or more CUs, one workgroup of the
+ * launch fits on a CU, and the shape's batches fit the launch (always at
+ * gpt-oss-20b's E = 32); the caller then runs the three calls.  The launch keeps
+ * one workgroup on each of 256 CUs and its mlp2 phase waits for the other
+ * workgroups' mlp1 results: work running on the device at the same time delays
+ * it.  The wait is bounded (about a second, moe_set_decode_spin_limit); a
+ * workgroup that gives up adds 1 to done[E], and the y rows it wrote are then
+ * wrong: done[E] == 0 after the launch means y is complete.
  */
 MOE_API int moe_mlp_decode(const void* t_pieces, const int32_t* indptr,
                            const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E,
@@ -200,6 +209,7 @@ MOE_API int moe_mlp_decode(const void* t_pieces, const int32_t* indptr,
  * and the residual add of mlp.py:402; the prefill combine scatter_output * w +
  * moe_sum + x of model/mlp_optimized.py:168-172.
  * y [n, k, N] fp32, w [n, k] bf16, x [n, N] bf16 or NULL -> out [n, N] bf16.
+ * N % 4 == 0.
  */
 MOE_API int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
                     int64_t N, uint16_t* out, moe_stream_t stream);
@@ -223,10 +233,11 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
 /* Byte offsets of the intermediates inside the block workspace, in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
  * t_pieces, act, act_pieces, y, logits (fp32 [n, E], bf16 values), counts
- * (int32 [ceil(n / 64), E], expert histogram per 64-token chunk; for n <= 128
- * its first E hold the decode chain's per-expert counts). */
+ * (int32 [ceil(n / 16), E], expert histogram per 16-token chunk, n > 128),
+ * sync (int32 [E + 1]: the decode launch's per-expert counts, then its status
+ * word). */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                                 size_t offsets[14]);
+                                 size_t offsets[15]);
 
 MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                       const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,
@@ -235,6 +246,25 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
                       const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
                       float alpha, float limit, uint16_t* out, void* workspace,
                       size_t workspace_bytes, moe_stream_t stream);
+
+/*
+ * Status of the last moe_block_forward that used this workspace (same shape
+ * arguments): MOE_OK, or MOE_ERR_INCOMPLETE when its decode launch's bounded
+ * wait gave up (the outputs of that call are NaN).  Unlike every other entry
+ * point this one waits: it synchronises `stream` to read the status word.
+ * No reference counterpart: TVM's kernels have no cross-workgroup waits
+ * (model/mlp_optimized.py:214-660 launches each stage separately).
+ */
+MOE_API int moe_block_status(const void* workspace, int64_t n, int64_t E, int64_t k, int64_t H,
+                             int64_t I, moe_stream_t stream);
+
+/*
+ * Bound of the decode launch's wait in polls (about 1 us each; default 2^20,
+ * a negative value restores it).  Returns the previous bound.  Process-wide;
+ * meant for tests, which set 0 to make every wait give up at once and check
+ * that the failure is reported.  No reference counterpart (as above).
+ */
+MOE_API int moe_set_decode_spin_limit(int polls);
 
 #ifdef __cplusplus
 }

@@ -52,7 +52,7 @@ def test_status_codes_match_header(native):
     codes = header_codes()
     assert codes["MOE_OK"] == 0
     for name in ("MOE_ERR_NULL", "MOE_ERR_SHAPE", "MOE_ERR_ALIGN", "MOE_ERR_UNSUPPORTED",
-                 "MOE_ERR_LAUNCH", "MOE_ERR_WORKSPACE"):
+                 "MOE_ERR_LAUNCH", "MOE_ERR_WORKSPACE", "MOE_ERR_INCOMPLETE"):
         assert codes[name] < 0
         assert native.status_string(codes[name]) not in ("unknown status", "ok")
     assert native.lib().moe_version() >= 100
@@ -113,7 +113,25 @@ def test_workspace_layout(native):
     n, E, k, H, I = 64, 32, 4, 2880, 2880
     total = native.workspace_bytes(n, E, k, H, I)
     offs = native.workspace_layout(n, E, k, H, I)
-    assert len(offs) == 14 and offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert len(offs) == 15 and offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert offs[11] + n * k * H * 4 <= offs[12]             # y before logits
-    assert offs[13] + (n + 15) // 16 * E * 4 <= total       # counts last
+    assert offs[13] + (n + 15) // 16 * E * 4 <= offs[14]    # counts, then sync
+    assert offs[14] + (E + 1) * 4 <= total                  # sync last: E counts + status
     assert native.workspace_bytes(n, E, k, H + 1, I) == 0
+
+
+def test_decode_spin_limit_hook(native):
+    """Host-side only: the bound is swapped and restored (negative = default)."""
+    prev = native.set_decode_spin_limit(5)
+    assert native.set_decode_spin_limit(-1) == 5
+    assert native.set_decode_spin_limit(prev) == 1 << 20
+    assert native.set_decode_spin_limit(prev) == prev
+
+
+def test_block_status_validates(native):
+    L = native.lib()
+    codes = header_codes()
+    assert L.moe_block_status(None, 4, 32, 4, 2880, 2880, None) == codes["MOE_ERR_NULL"]
+    assert L.moe_block_status(ctypes.c_void_p(0x1000), 4, 32, 4, 2882, 2880, None) \
+        == codes["MOE_ERR_SHAPE"]
+    assert L.moe_block_status(None, 0, 32, 4, 2880, 2880, None) == codes["MOE_OK"]

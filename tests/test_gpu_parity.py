@@ -392,7 +392,7 @@ def test_mlp_decode_matches_three_calls(native, block20b, n, seed):
             blk.mlp2_weight_scales, blk.mlp2_bias, 1.702, blk.swiglu_limit)
     nk = n * k
     ref_pk = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), nk, 2880, 3)
-    done = torch.zeros(32, dtype=torch.int32, device="cuda")
+    done = torch.zeros(33, dtype=torch.int32, device="cuda")
     y, pk = native.mlp_decode(*args, done=done)
     for _ in range(2):
         torch.cuda.synchronize()
@@ -403,7 +403,8 @@ def test_mlp_decode_matches_three_calls(native, block20b, n, seed):
         done.zero_()
         y, pk = native.mlp_decode(*args, act_pieces=pk, done=done, y=y)
     cnt = host(torch.diff(perm["indptr"]))
-    assert np.array_equal(host(done), 360 * ((cnt + 15) // 16))  # mlp1 tiles per expert
+    assert np.array_equal(host(done[:32]), 360 * ((cnt + 15) // 16))  # mlp1 tiles per expert
+    assert int(done[32]) == 0  # status: no wait gave up
 
 
 def test_mlp_decode_unsupported(native, block20b):
@@ -455,3 +456,85 @@ def test_block_deterministic_and_empty(native, block20b):
     assert np.array_equal(a, b)
     empty = blk(torch.empty((1, 0, 2880), dtype=torch.bfloat16, device="cuda"))
     assert empty.shape == (1, 0, 2880)
+
+
+# ---------------------------------------------------------------------------
+# the decode launch's bounded wait: a give-up is reported, never silent
+# ---------------------------------------------------------------------------
+
+def test_decode_wait_give_up_is_reported(native, block20b):
+    """With the wait bound set to 0 polls from the host, every phase-2
+    workgroup of the decode launch gives up at once (all kernels still run to
+    their end): moe_block_status reports MOE_ERR_INCOMPLETE, every output is
+    NaN, and the standalone launch's status word counts the give-ups.  With
+    the default bound restored the same calls are correct again."""
+    p, blk = block20b
+    n, H = 64, 2880
+    x = O.make_input(28, n)
+    xd = bf16_dev(x).view(1, n, H)
+    prev = native.set_decode_spin_limit(0)
+    try:
+        out = blk(xd)
+        ws = blk._workspace(n, xd.device)
+        assert native.block_status(ws, n, 32, 4, H, 2880) == -7
+        assert torch.isnan(out.float()).all()
+        st = blk.forward_staged(xd)
+        t_pk = native.quantize_pieces(st["t"], 2)
+        done = torch.zeros(33, dtype=torch.int32, device="cuda")
+        native.mlp_decode(t_pk, n, st["perm"]["indptr"], st["perm"]["sorted_pairs"], 4,
+                          blk.mlp1_weight_blocks, blk.mlp1_weight_scales, blk.mlp1_bias,
+                          blk.mlp2_weight_blocks, blk.mlp2_weight_scales, blk.mlp2_bias, 1.702,
+                          blk.swiglu_limit, done=done)
+        torch.cuda.synchronize()
+        assert int(done[32]) > 0
+    finally:
+        native.set_decode_spin_limit(prev)
+    assert native.set_decode_spin_limit(-1) == prev
+    out = host_bf16(blk(xd).view(n, H))
+    assert native.block_status(blk._workspace(n, xd.device), n, 32, 4, H, 2880) == 0
+    m = O.compare_outputs(out, O.block_forward(x, p).out)
+    assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
+
+
+# ---------------------------------------------------------------------------
+# standalone SwiGLU and gating exports
+# ---------------------------------------------------------------------------
+
+def test_swiglu_standalone(native):
+    """moe_swiglu against the oracle's closed form (model/mlp.py:29-60): the
+    clamps are exact (glu clamped above only, at 7; linear to [-7, 7]), zeros
+    of either factor give exact zeros, and elsewhere the result is within 4
+    ulp (the kernel's sigmoid is the device expf, the oracle's correctly
+    rounded).  A sign or clamp mistake is off by far more."""
+    rng = np.random.default_rng(5)
+    special = np.array([[0.0, 3.0], [2.0, -1.0], [7.0, 7.0], [7.5, 9.0], [100.0, -100.0],
+                        [-100.0, 2.0], [-7.5, 0.5], [np.inf, 1.0], [3.0, np.inf],
+                        [3.0, -np.inf], [-0.0, 5.0], [6.9999995, -6.9999995]], np.float32)
+    rand = (rng.standard_normal((4096, 2)) * 4).astype(np.float32)
+    x = np.concatenate([special, rand]).reshape(-1, 2 * 4)  # rows of d = 4 pairs
+    got = host(native.swiglu(f32_dev(x), 1.702, 7.0))
+    ref = O.swiglu(x)
+    # exact where the sigmoid does not enter: zero factors
+    zero = (x[:, 0::2] == 0) | (x[:, 1::2] == -1)
+    assert np.array_equal(got[zero], ref[zero])
+    # the clamps: glu >= 7 behaves as 7, lin beyond +-7 as +-7
+    xc = x.copy()
+    xc[:, 0::2] = np.minimum(xc[:, 0::2], 7.0)
+    xc[:, 1::2] = np.clip(xc[:, 1::2], -7.0, 7.0)
+    assert np.array_equal(host(native.swiglu(f32_dev(xc), 1.702, 7.0)), got)
+    np.testing.assert_allclose(got, ref, rtol=4 * 2.0 ** -23, atol=1e-37)
+
+
+def test_gemv_gating_without_residual(native):
+    """moe_gemv_gating with x == NULL (the reference's run_gating alone,
+    model/mlp.py:328-369) and with x (+ residual, mlp.py:402): bit-exact
+    against the oracle's in-order fp32 sum, k = 4 and k = 2."""
+    rng = np.random.default_rng(6)
+    for n, k, N in ((7, 4, 2880), (33, 2, 64)):
+        y = (rng.standard_normal((n, k, N)) * 5).astype(np.float32)
+        w = O.f32_to_bf16(rng.random((n, k)).astype(np.float32))
+        x = O.make_input(9, n, hidden=N)
+        got = host_bf16(native.gemv_gating(f32_dev(y), bf16_dev(w)))
+        assert np.array_equal(got, O.gating(y, w))
+        got = host_bf16(native.gemv_gating(f32_dev(y), bf16_dev(w), bf16_dev(x)))
+        assert np.array_equal(got, O.residual_add(x, O.gating(y, w)))
