@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/moe_gfx950.h"
 
 extern "C" {
@@ -154,6 +156,8 @@ const char* moe_status_string(int status) {
     case MOE_ERR_UNSUPPORTED: return "unsupported parameter value";
     case MOE_ERR_LAUNCH: return "kernel launch failed";
     case MOE_ERR_WORKSPACE: return "workspace too small";
+    case MOE_ERR_TOO_LARGE:
+      return "n too large for moe_block_forward_noalloc's static scratch (48 MiB)";
     case MOE_ERR_INCOMPLETE:
       return "the decode launch's bounded wait gave up: outputs are NaN";
     default: return "unknown status";
@@ -467,6 +471,68 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
 }
 
 int moe_set_decode_spin_limit(int polls) { return moe_decode_spin_limit_exchange(polls); }
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// moe_block_forward_noalloc: the block with its workspace in a static device
+// array instead of a caller buffer, for callers that cannot allocate.  Each
+// GPU the library runs on holds its own copy of `scratch` (48 MiB) until the
+// process ends.  In host code the array's name is not a device address: the
+// address of this device's copy comes from hipGetSymbolAddress, looked up
+// once per device with that device current, and only that address is ever
+// handed to kernels.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)48 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<uintptr_t> g_scratch_addr[kMaxDevices];  // 0: not looked up yet
+
+// Device address of the current device's scratch.
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MOE_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_UNSUPPORTED;
+  uintptr_t a = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (a == 0) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return MOE_ERR_LAUNCH;
+    a = (uintptr_t)p;
+    g_scratch_addr[dev].store(a, std::memory_order_release);  // same value if raced
+  }
+  *out = (void*)a;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_block_forward_noalloc(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H,
+                              int64_t I, const uint16_t* norm_w, const uint16_t* gate_w,
+                              const uint16_t* gate_b, const uint8_t* mlp1_blocks,
+                              const uint8_t* mlp1_scales, const uint16_t* mlp1_bias,
+                              const uint8_t* mlp2_blocks, const uint8_t* mlp2_scales,
+                              const uint16_t* mlp2_bias, float eps, float alpha, float limit,
+                              uint16_t* out, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  size_t off[kNumRegions], total;
+  layout(n, E, k, H, I, off, &total);
+  if (total > kScratchBytes) return MOE_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  // every region the kernels read is written earlier in the same call (the
+  // counters are zeroed by the first kernel), so stale contents of the last
+  // call do no harm
+  return moe_block_forward(x, n, E, k, H, I, norm_w, gate_w, gate_b, mlp1_blocks, mlp1_scales,
+                           mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, eps, alpha, limit, out,
+                           ws, kScratchBytes, stream);
+}
 
 int moe_block_status(const void* workspace, int64_t n, int64_t E, int64_t k, int64_t H,
                      int64_t I, moe_stream_t stream) {

@@ -54,6 +54,8 @@ _SIGS = {
     "moe_block_forward": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                            _F, _F, _F, _P, _P, _SZ, _P], _INT),
     "moe_block_status": ([_P, _I64, _I64, _I64, _I64, _I64, _P], _INT),
+    "moe_block_forward_noalloc": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _F, _F, _F, _P, _P], _INT),
     "moe_set_decode_spin_limit": ([_INT], _INT),
 }
 for _name, (_args, _ret) in _SIGS.items():
@@ -343,6 +345,25 @@ def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
         _ptr(params["mlp2_weight_blocks"]), _ptr(params["mlp2_weight_scales"]),
         _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
         workspace.numel(), _stream()), "moe_block_forward")
+    return out
+
+
+def block_forward_noalloc(x, params: dict, k, eps, alpha, limit, out):
+    """The block with the library's static scratch as workspace (no allocation
+    by the library; ``out`` [n, H] bf16 is the caller's).  Same results as
+    block_forward."""
+    n, H = x.shape
+    E = params["gate.weight"].shape[0]
+    inter = params["mlp2_weight_blocks"].shape[2] * 32
+    _expect(x, "x", torch.bfloat16)
+    _expect(out, "out", torch.bfloat16, (n, H))
+    _check(_lib.moe_block_forward_noalloc(
+        _ptr(x), n, E, k, H, inter, _ptr(params["norm.weight"]), _ptr(params["gate.weight"]),
+        _ptr(params["gate.bias"]), _ptr(params["mlp1_weight_blocks"]),
+        _ptr(params["mlp1_weight_scales"]), _ptr(params["mlp1_bias"]),
+        _ptr(params["mlp2_weight_blocks"]), _ptr(params["mlp2_weight_scales"]),
+        _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _stream()),
+        "moe_block_forward_noalloc")
     return out
 
 

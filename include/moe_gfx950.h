@@ -52,6 +52,7 @@ extern "C" {
 #define MOE_ERR_LAUNCH (-5)      /* the HIP runtime rejected a launch */
 #define MOE_ERR_WORKSPACE (-6)   /* workspace smaller than moe_workspace_bytes() */
 #define MOE_ERR_INCOMPLETE (-7)  /* the decode launch's bounded wait gave up (outputs are NaN) */
+#define MOE_ERR_TOO_LARGE (-8)   /* beyond moe_block_forward_noalloc's static scratch */
 
 typedef void* moe_stream_t; /* a hipStream_t */
 
@@ -246,6 +247,31 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
                       const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
                       float alpha, float limit, uint16_t* out, void* workspace,
                       size_t workspace_bytes, moe_stream_t stream);
+
+/*
+ * moe_block_forward without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  No reference counterpart: the reference's Relax VM
+ * allocates every intermediate itself.  The workspace is a static device
+ * array of 48 MiB held by each GPU the library runs on until the process
+ * ends; nothing is allocated (no hipMalloc/hipFree) by this call.  Limit:
+ * moe_workspace_bytes(n, E, k, H, I) <= 48 MiB (n <= 357 tokens at
+ * gpt-oss-20b's shape, n <= 356 at 120b's), else MOE_ERR_TOO_LARGE with no
+ * launch.  Same results as moe_block_forward.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams or host
+ * threads) race and give wrong results; calls in order on one stream are
+ * safe.  The array keeps the last call's contents, and nothing in it needs to
+ * start at zero.  moe_block_status does not apply (the status word lives in
+ * the static array; the outputs are NaN if the decode launch gave up).
+ */
+MOE_API int moe_block_forward_noalloc(const uint16_t* x, int64_t n, int64_t E, int64_t k,
+                                      int64_t H, int64_t I, const uint16_t* norm_w,
+                                      const uint16_t* gate_w, const uint16_t* gate_b,
+                                      const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                                      const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                                      const uint8_t* mlp2_scales, const uint16_t* mlp2_bias,
+                                      float eps, float alpha, float limit, uint16_t* out,
+                                      moe_stream_t stream);
 
 /*
  * Status of the last moe_block_forward that used this workspace (same shape
