@@ -1111,31 +1111,48 @@ static size_t decode_lds_bytes(int E, int H) {
 // Polls of the decode launch's bounded wait (moe_set_decode_spin_limit).
 static std::atomic<int> g_decode_spin_max{moe::kDecodeSpinMax};
 
+// Whether the current device can hold the decode launch (256 or more CUs;
+// one workgroup of 64 * decode_waves() threads with the whole LDS fits on a
+// CU, registers included), found once per device so that launches made
+// under graph capture query nothing: kOk, kErrUnsupported or kErrLaunch.
+static int decode_device_fit() {
+  using namespace moe;
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> fit[kMaxDevices];  // 0: not known yet, else status + 1
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return kErrLaunch;
+  if (dev < 0 || dev >= kMaxDevices) return kErrUnsupported;
+  const int known = fit[dev].load(std::memory_order_acquire);
+  if (known) return known - 1;
+  int rc = kOk, cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    rc = kErrLaunch;
+  else if (cus < kNumCUs)
+    rc = kErrUnsupported;  // every workgroup must be resident
+  else if (hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               kLdsBytes) != hipSuccess ||
+           hipOccupancyMaxActiveBlocksPerMultiprocessor(
+               &per_cu, (const void*)moe_mx_decode_kernel, 64 * decode_waves(), kLdsBytes) !=
+               hipSuccess)
+    rc = kErrLaunch;
+  else if (per_cu < 1)
+    rc = kErrUnsupported;
+  fit[dev].store(rc + 1, std::memory_order_release);
+  return rc;
+}
+
 // kOk when moe_launch_mx_decode can run this shape on the current device,
 // else kErrUnsupported (the caller then runs mlp1, the encoding and mlp2 as
 // separate launches).
 int moe_mx_decode_check(int E, int H, int I, int nk) {
   using namespace moe;
   if (H != I || (H + 127) / 128 != 23 || H % 32) return kErrUnsupported;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return kErrLaunch;
-  const int grid = kNumCUs;
-  if (cus < grid) return kErrUnsupported;  // every workgroup must be resident
-  constexpr int gcap2 = kMxMaxGroups;
   if (decode_lds_bytes(E, H) > (size_t)kLdsBytes) return kErrUnsupported;
-  // one workgroup of this size and LDS must fit on a CU (registers included)
-  static const bool lds_ok =
-      hipFuncSetAttribute((const void*)moe_mx_decode_kernel,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
-  if (!lds_ok) return kErrLaunch;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)moe_mx_decode_kernel,
-                                                   64 * decode_waves(),
-                                                   decode_lds_bytes(E, H)) != hipSuccess)
-    return kErrLaunch;
-  if (per_cu < 1) return kErrUnsupported;
+  const int fit = decode_device_fit();
+  if (fit != kOk) return fit;
+  const int grid = kNumCUs;
+  constexpr int gcap2 = kMxMaxGroups;
   // Batches are bounded by (experts holding pairs) + nk / tokens per batch.
   // Phase 1 needs one segment per workgroup whose share (at most
   // 4 ceil(quads / floor(grid / batches)) tiles) fits the LDS act tile of 96.

@@ -77,6 +77,8 @@ class MLPBlock(torch.nn.Module):
                  device: str | torch.device = "cuda"):
         super().__init__()
         assert config
+        self.config = config
+        self.rms_norm_eps = rms_norm_eps
         if dtype is None:
             dtype = config.dtype
         self.dtype = dtype
@@ -121,6 +123,23 @@ class MLPBlock(torch.nn.Module):
             "mlp2_weight_scales": self.mlp2_weight_scales, "mlp2_bias": self.mlp2_bias,
         }
 
+    def with_gate_bias(self, bias: torch.Tensor) -> "MLPBlock":
+        """A block that shares every parameter of this one except the router
+        bias (``gate.bias`` [E] bf16, copied): a view of the same layer whose
+        tokens route differently.  Used to build synthetic workloads whose token
+        groups have different routing profiles; allocates only the bias."""
+        twin = MLPBlock(self.config, self.rms_norm_eps, self.dtype, device="meta")
+        twin.norm.weight = self.norm.weight
+        twin.gate.weight = self.gate.weight
+        for name in ("mlp1_weight_blocks", "mlp1_weight_scales", "mlp2_weight_blocks",
+                     "mlp2_weight_scales", "mlp1_bias", "mlp2_bias"):
+            setattr(twin, name, getattr(self, name))
+        b = bias.to(device=self.gate.bias.device, dtype=self.gate.bias.dtype)
+        if tuple(b.shape) != tuple(self.gate.bias.shape):
+            raise ValueError(f"gate bias: expected shape {tuple(self.gate.bias.shape)}")
+        twin.gate.bias = torch.nn.Parameter(b.clone().contiguous(), requires_grad=False)
+        return twin
+
     # -- reference operator methods -----------------------------------------
 
     def run_einsum(self, input_tensor: torch.Tensor, expert_indices: torch.Tensor,
@@ -147,12 +166,21 @@ class MLPBlock(torch.nn.Module):
 
     # -- forward --------------------------------------------------------------
 
-    def _workspace(self, n: int, device) -> torch.Tensor:
-        need = _native.workspace_bytes(n, self.num_experts, self.experts_per_token,
+    def workspace_bytes(self, n: int) -> int:
+        """Bytes of block workspace a call on n tokens needs (moe_workspace_bytes)."""
+        return _native.workspace_bytes(n, self.num_experts, self.experts_per_token,
                                        self.hidden_size, self.intermediate_size)
+
+    def _workspace(self, n: int, device) -> torch.Tensor:
+        need = self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
             self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
         return self._ws
+
+    def reserve(self, n: int) -> None:
+        """Size the module's workspace for calls of up to n tokens now, so that
+        forward() allocates no workspace later (e.g. under graph capture)."""
+        self._workspace(n, self.mlp1_weight_blocks.device)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x [b, s, hidden] bf16 -> x + MoE(RMSNorm(x)) (model/mlp.py:371-402).
@@ -169,6 +197,19 @@ class MLPBlock(torch.nn.Module):
         out = _native.block_forward(x2, self.packed_params(), self.experts_per_token,
                                     self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit, ws)
         return out.reshape(b, seq_len, dim)
+
+    def forward_into(self, x2d: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
+        """forward on x2d [n, hidden] into the caller's ``out`` [n, hidden] with the
+        caller's ``workspace`` (uint8, at least workspace_bytes(n), 256-byte
+        aligned): nothing is allocated, so the call can be captured in a graph.
+        Calls that share a workspace must not overlap (one stream, in order)."""
+        n = x2d.shape[0]
+        if workspace.numel() < self.workspace_bytes(n):
+            raise ValueError(f"workspace: need {self.workspace_bytes(n)} bytes, "
+                             f"got {workspace.numel()}")
+        return _native.block_forward(x2d, self.packed_params(), self.experts_per_token,
+                                     self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit,
+                                     workspace, out=out)
 
     def forward_staged(self, x: torch.Tensor, events: dict | None = None,
                        fused_decode: bool = False) -> dict:

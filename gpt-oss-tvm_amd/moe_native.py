@@ -336,8 +336,11 @@ def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
     n, H = x.shape
     E = params["gate.weight"].shape[0]
     inter = params["mlp2_weight_blocks"].shape[2] * 32
+    _expect(x, "x", torch.bfloat16)
     if out is None:
         out = torch.empty_like(x)
+    _expect(out, "out", torch.bfloat16, (n, H))
+    _expect(workspace, "workspace", torch.uint8)
     _check(_lib.moe_block_forward(
         _ptr(x), n, E, k, H, inter, _ptr(params["norm.weight"]), _ptr(params["gate.weight"]),
         _ptr(params["gate.bias"]), _ptr(params["mlp1_weight_blocks"]),

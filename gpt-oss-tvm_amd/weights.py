@@ -6,9 +6,20 @@ kept as uint8 (weights.py:88-89) -- packed, with no bf16 expansion -- and
 parameter names are mapped to checkpoint names with the same rules
 (weights.py:102-113): drop ``model.``, ``norm.weight`` -> ``norm.scale``,
 ``weight_blocks`` -> ``weight.blocks``, ``weight_scales`` -> ``weight.scales``.
+A layer's MoE parameters live under ``block.{i}.mlp.`` (the reference's
+``GPTOssForCausalLM.model.block[i].mlp``, model/transformer.py:41-42, with
+``model.`` dropped by the first rule).
 
 Tensors land in torch-ROCm device memory; no DLPack hop is needed because the
 kernels take raw device pointers.
+
+Loading is checked before anything is copied: every tensor must exist, match
+its parameter's shape and dtype, and every E8M0 scale byte must lie in
+[2, 252].  Inside that range the expert matmuls (which feed the scale bytes
+to the block-scaled MFMA) give exactly the reference's dequantised weights
+(model/mlp.py:297-298, ``exp2(s - 127)``); outside it they do not (s = 255
+is +inf in the reference and NaN in the hardware's E8M0; s in {0, 1, 253,
+254} reach fp32 subnormals or overflow), so such a checkpoint is refused.
 """
 from __future__ import annotations
 
@@ -20,6 +31,9 @@ from safetensors import safe_open
 
 # Bytes per MXFP4 block: 32 e2m1 values packed in 16 bytes (weights.py:35).
 BYTES_PER_BLOCK = 16
+
+# E8M0 scale bytes for which the fused matmuls reproduce the reference exactly.
+SCALE_MIN, SCALE_MAX = 2, 252
 
 _RENAMES = (
     ("model.", ""),
@@ -34,6 +48,11 @@ def convert_key(name: str) -> str:
     for old, new in _RENAMES:
         name = name.replace(old, new)
     return name
+
+
+def mlp_prefix(layer: int) -> str:
+    """Parameter-name prefix of layer ``layer``'s MoE block (before convert_key)."""
+    return f"model.block.{layer}.mlp."
 
 
 class TorchCheckpoint:
@@ -68,21 +87,52 @@ class TorchCheckpoint:
         return [self.get_tensor(convert_key(name)) for name, _ in params]
 
     def load_into(self, module: torch.nn.Module, prefix: str = "") -> None:
-        """Copy the checkpoint tensors of ``module``'s parameters into them (shape/dtype checked)."""
+        """Copy the checkpoint tensors of ``module``'s parameters into them.
+
+        ``prefix`` is prepended to each parameter name before the mapping
+        (``mlp_prefix(i)`` for layer i's MoE block).  Everything is validated
+        first -- presence (KeyError), shape and dtype (ValueError), the E8M0
+        scale range (ValueError) -- so a refused checkpoint leaves the module
+        untouched.
+        """
         named = [(prefix + name, p) for name, p in module.named_parameters()]
-        for (name, p), src in zip(named, self.load_packed_params(named)):
+        srcs = self.load_packed_params(named)
+        for (name, p), src in zip(named, srcs):
             if tuple(src.shape) != tuple(p.shape) or src.dtype != p.dtype:
-                raise ValueError(f"{name}: checkpoint has {tuple(src.shape)} {src.dtype}, "
-                                 f"parameter is {tuple(p.shape)} {p.dtype}")
-            with torch.no_grad():
+                raise ValueError(f"{convert_key(name)}: checkpoint has {tuple(src.shape)} "
+                                 f"{src.dtype}, parameter is {tuple(p.shape)} {p.dtype}")
+            if name.endswith("weight_scales") and src.numel():
+                lo, hi = int(src.min()), int(src.max())
+                if lo < SCALE_MIN or hi > SCALE_MAX:
+                    raise ValueError(
+                        f"{convert_key(name)}: E8M0 scale bytes span [{lo}, {hi}], outside "
+                        f"[{SCALE_MIN}, {SCALE_MAX}] where the MXFP4 matmuls reproduce the "
+                        "reference dequantisation (model/mlp.py:297-298)")
+        with torch.no_grad():
+            for (_, p), src in zip(named, srcs):
                 p.copy_(src)
+
+
+def load_mlp_blocks(ckpt: TorchCheckpoint, config, layers: Iterable[int] | None = None,
+                    device: str | torch.device | None = None) -> list:
+    """One MLPBlock per layer (all ``config.num_hidden_layers`` by default),
+    parameters loaded from ``block.{i}.mlp.*`` of the checkpoint."""
+    from model.mlp import MLPBlock
+
+    dev = ckpt.device if device is None else torch.device(device)
+    out = []
+    for i in (range(config.num_hidden_layers) if layers is None else layers):
+        blk = MLPBlock(config, device=dev)
+        ckpt.load_into(blk, prefix=mlp_prefix(i))
+        out.append(blk)
+    return out
 
 
 def scale_range(module: torch.nn.Module) -> tuple[int, int]:
     """(min, max) E8M0 scale byte over a block's MXFP4 weights.
 
     The fused matmuls dequantise exactly while 2 <= s <= 252 (every e2m1 value
-    times 2^(s-127) is a normal bf16); real checkpoints can be checked with this.
+    times 2^(s-127) is a normal bf16); load_into refuses checkpoints outside.
     """
     lo, hi = 255, 0
     for name, p in module.named_parameters():
