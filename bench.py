@@ -10,15 +10,25 @@ HBM.  Three independent weight sets (3 x 424 MB, beyond the 256 MB MALL) are
 rotated so that every step streams its experts from HBM.
 
 Besides the JSON contract fields the line carries
-  roofline      for the dominant kernel (at decode the one-launch chain
-                moe_mx_decode_kernel, else mlp1): algorithmic bytes per launch
-                / its average duration, from HIP events recorded on the launch
-                stream around that kernel in a second timed pass, vs 8 TB/s;
-                traffic from rocprofv3 FETCH_SIZE + WRITE_SIZE when a
-                measured summary is committed under profiles/;
+  roofline      for the dominant kernel of the workload (at decode the
+                one-launch chain moe_mx_decode_kernel; at prefill the mlp1
+                GEMM): algorithmic bytes (or flops) per launch / its average
+                duration from HIP events recorded on the launch stream around
+                that kernel in a second timed pass, against 8 TB/s (or the
+                2.5 PFLOP/s dense bf16 peak); traffic from rocprofv3
+                FETCH_SIZE + WRITE_SIZE when a measured summary is committed
+                under profiles/;
+  secondary     the other BASELINE workloads, each timed the same way with
+                fewer steps: configs 0 (decode 1), 2 (prefill 4096, Zipf
+                routing), 3a/3b (120B decode 256 / prefill 2048) and 4 (24
+                chained layers, a mixed decode + prefill step captured in one
+                HIP graph and replayed);
   cpu_baseline  the serial C restatement of the reference block (the CPU
                 oracle) timed on this host's cores on a bounded sample of the
-                same tokens and weights; its outputs double as a parity check.
+                same tokens and weights, one thread (the reference's llvm
+                build is serial) and, under "all_cores", OpenMP over every
+                core this process may use; its outputs double as a parity
+                check.
 Only one GPU is used; --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -37,6 +47,12 @@ for _p in (REPO, os.path.join(REPO, "gpt-oss-tvm_amd")):
 METRIC = "MoE-layer tok/s at 20B shape; decode HBM GB/s %peak; prefill MFMA util"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+# Arithmetic of the path: MXFP4 weights (e2m1 + E8M0) times the activations
+# as fp8 e4m3 pieces (2 for t, 3 for act) on the block-scaled MFMA, fp32
+# accumulation; router dots fp64; bf16 in and out.
+DTYPE = "mxfp4 x fp8-pieces MFMA, fp32 accumulate (bf16 in/out)"
+PIECES_T, PIECES_ACT = 2, 3
 
 # name -> (experts, tokens, zipf beta, BASELINE config label)
 CONFIGS = {
@@ -46,12 +62,21 @@ CONFIGS = {
     "decode256_120b": (128, 256, 0.0, "config 3a: gpt-oss-120b MoE block, decode batch 256"),
     "prefill2048_120b": (128, 2048, 0.0, "config 3b: gpt-oss-120b MoE block, 2048-token prefill"),
 }
+MIXED = ("mixed24", "config 4: 24 chained gpt-oss-20b MoE blocks, one mixed step of 32 decode "
+         "tokens (uniform routing) + a 2048-token prefill chunk (Zipf routing), one HIP graph")
 H = I = 2880
 K_TOP = 4
+PER_EXPERT_BYTES = (2 * I * (H // 32) * 17 + 2 * I * 2) + (H * (I // 32) * 17 + H * 2)  # 13,236,480
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def zipf_bias(E: int, beta: float, device):
+    import torch
+    pr = torch.arange(1, E + 1, device=device, dtype=torch.float64) ** -1.1
+    return (beta * torch.log(pr / pr.sum())).float()
 
 
 def make_block(E: int, seed: int, zipf_beta: float, device):
@@ -77,8 +102,7 @@ def make_block(E: int, seed: int, zipf_beta: float, device):
             p.copy_(torch.randn(p.shape, generator=g, device=device) * std)
         b = torch.randn(E, generator=g, device=device) * 0.01
         if zipf_beta:
-            pr = torch.arange(1, E + 1, device=device, dtype=torch.float64) ** -1.1
-            b = b + zipf_beta * torch.log(pr / pr.sum()).float()
+            b = b + zipf_bias(E, zipf_beta, device)
         blk.gate.bias.copy_(b)
         blk.norm.weight.fill_(1.0)
     return blk
@@ -98,8 +122,210 @@ def read_traffic(workload: str, kernel: str):
     return None
 
 
-def cpu_baseline(blk, x, n_sample: int):
-    """Serial C restatement of model/mlp.py on the first n_sample tokens (weight set 0)."""
+def block_bytes(n: int, touched: float, E: int) -> float:
+    """Compulsory HBM bytes of one block call: touched experts'
+    weights, router and norm weights, x in and out."""
+    return touched * PER_EXPERT_BYTES + E * H * 2 + 2 * E + 2 * H + n * H * 4
+
+
+def block_flops(n: int, E: int) -> float:
+    return n * (2 * K_TOP * (2 * I * H + H * I) + 2 * H * E)
+
+
+def timed_steps(fn, steps: int, warmup: int) -> float:
+    """Seconds per call over `steps` calls after `warmup` (synchronised on both sides)."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def staged_pass(blocks, xs, steps: int, stages, fused: bool, pieces_epilogue: bool) -> dict:
+    """Per-stage HIP events on the launch stream.  A spin kernel is queued first
+    so the host runs ahead of the GPU and the events time the kernels, not
+    gaps left by Python between launches."""
+    import torch
+    recs = []
+    nw = len(blocks)
+    torch.cuda._sleep(int(2.4e9 * 0.4e-3 * steps))
+    for i in range(steps):
+        ev = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for s in stages}
+        blocks[i % nw].forward_staged(xs[i % nw], events=ev, fused_decode=fused,
+                                      pieces_epilogue=pieces_epilogue)
+        recs.append(ev)
+    torch.cuda.synchronize()
+    return {s: sum(r[s][0].elapsed_time(r[s][1]) for r in recs) / len(recs) * 1e3 for s in stages}
+
+
+def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) -> tuple:
+    """Time one single-block workload; returns (result dict, blocks, xs)."""
+    import torch
+    E, n, beta, label = CONFIGS[name]
+    log(f"workload {name}: E={E} n={n} zipf_beta={beta}")
+    blocks = [make_block(E, 1000 + i, beta, dev) for i in range(weight_sets)]
+    gx = torch.Generator(device=dev)
+    gx.manual_seed(7)
+    xs = [torch.randn((1, n, H), generator=gx, device=dev).to(torch.bfloat16)
+          for _ in range(weight_sets)]
+    for blk in blocks:
+        blk.reserve(n)
+    torch.cuda.synchronize()
+
+    touched, loads = [], []
+    for blk, x in zip(blocks, xs):
+        st = blk.forward_staged(x)
+        cnt = torch.diff(st["perm"]["indptr"])
+        touched.append(int((cnt > 0).sum()))
+        loads.append(float((cnt.max().float() / cnt.float().mean()).item()))
+    avg_touched = sum(touched) / len(touched)
+
+    nw = len(blocks)
+    sec = timed_steps(lambda i: blocks[i % nw](xs[i % nw]), steps, warmup)
+    us = sec * 1e6
+    log(f"{name}: {us:.1f} us/block, {n / sec:.0f} tok/s")
+
+    nk = n * K_TOP
+    gemm = nk >= 48 * E
+    fused = False
+    if not gemm and n <= 128:
+        try:
+            blocks[0].forward_staged(xs[0], fused_decode=True)
+            fused = True
+        except RuntimeError as e:
+            log(f"mlp_decode not used: {e}")
+    torch.cuda.synchronize()
+    if fused:
+        stages = ("router", "permute", "pieces_t", "mlp_decode", "combine")
+    else:
+        stages = ("router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine")
+    stage_us = staged_pass(blocks, xs, min(steps, 100), stages, fused, gemm)
+    log(f"{name} stage us: " + ", ".join(f"{s}={v:.1f}" for s, v in stage_us.items()))
+
+    bb = block_bytes(n, avg_touched, E)
+    bf = block_flops(n, E)
+    res = {
+        "workload": label, "tokens": n, "experts": E, "us_per_block": round(us, 2),
+        "tok_s": round(n / sec, 1), "touched_experts": avg_touched,
+        "max_over_mean_load": round(sum(loads) / len(loads), 2),
+        "block_hbm_frac": round(bb / sec / 1e9 / HBM_PEAK_GBS, 4),
+        "block_bf16_mfma_frac": round(bf / sec / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "stages_us": {s: round(v, 2) for s, v in stage_us.items()},
+    }
+    if fused:
+        # SURVEY 8(d): touched experts' weights plus 4 bytes per token (the
+        # token in and out); the act pieces written and read back inside the
+        # launch are intermediates, listed apart and not counted
+        alg = avg_touched * PER_EXPERT_BYTES + n * H * 4
+        t = stage_us["mlp_decode"]
+        achieved = alg / (t * 1e-6) / 1e9
+        roof = {"bound": "hbm",
+                "kernel": "moe_mx_decode_kernel (mlp1 + SwiGLU + act pieces + mlp2)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": read_traffic(name, "moe::moe_mx_decode_kernel"),
+                "algorithmic_bytes": int(alg),
+                "intermediate_bytes": int(2 * nk * I * PIECES_ACT + nk * H * 4),
+                "avg_us": round(t, 2)}
+    elif not gemm:
+        alg = avg_touched * (2 * I * (H // 32) * 17 + 2 * I * 2) + n * H * PIECES_T
+        t = stage_us["mlp1"]
+        achieved = alg / (t * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": "moe_mx_gemv_kernel<2,1,23> (mlp1)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": read_traffic(name, "moe::moe_mx_gemv_kernel<2, 1, 23>"),
+                "algorithmic_bytes": int(alg), "avg_us": round(t, 2)}
+    else:
+        f1 = 2 * nk * 2 * I * H
+        t = stage_us["mlp1"]
+        achieved = f1 / (t * 1e-6) / 1e12
+        roof = {"bound": "mfma", "kernel": "moe_mx_gemm_kernel<2,2> (mlp1, act pieces epilogue)",
+                "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                # the MFMA executes every fp8 piece: algorithmic x pieces, at
+                # the fp8 (fp8 x fp4) dense rate
+                "fp8_hw_frac": round(achieved * PIECES_T / FP8_PEAK_TFLOPS, 4),
+                "traffic": read_traffic(name, "moe::moe_mx_gemm_kernel<2, 2>"),
+                "algorithmic_flops": int(f1), "avg_us": round(t, 2)}
+        t2 = stage_us["mlp2"]
+        f2 = 2 * nk * H * I
+        res["mlp2"] = {"avg_us": round(t2, 2),
+                       "frac": round(f2 / (t2 * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                       "fp8_hw_frac": round(f2 * PIECES_ACT / (t2 * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+    res["roofline"] = roof
+    res["algorithmic_bytes"] = int(bb)
+    res["algorithmic_flops"] = int(bf)
+    return res, blocks, xs
+
+
+def run_mixed(steps: int, warmup: int, dev, layers: int = 24, n_dec: int = 32,
+              n_pre: int = 2048) -> dict:
+    """Config 4: `layers` chained 20B blocks (independent seeded weights), one
+    mixed step = the decode group (layer's own router bias) and the prefill
+    group (that bias + the Zipf profile at beta 0.5) layer by layer, captured
+    in one HIP graph (MoEStack: nothing allocated inside) and replayed."""
+    import torch
+
+    from model.stack import MoEStack
+    log(f"workload mixed24: {layers} layers, {n_dec} decode + {n_pre} prefill tokens")
+    pairs = []
+    zb = zipf_bias(32, 0.5, dev)
+    for layer in range(layers):
+        dec = make_block(32, 2000 + layer, 0.0, dev)
+        pre = dec.with_gate_bias(dec.gate.bias.float() + zb)
+        pairs.append((dec, pre))
+    stack = MoEStack(pairs)
+    stack.reserve(n_dec, n_pre)
+    gx = torch.Generator(device=dev)
+    gx.manual_seed(9)
+    xd = torch.randn((1, n_dec, H), generator=gx, device=dev).to(torch.bfloat16)
+    xp = torch.randn((1, n_pre, H), generator=gx, device=dev).to(torch.bfloat16)
+    eager_s = timed_steps(lambda i: stack(xd, xp), max(3, steps // 2), 1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack(xd, xp)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack(xd, xp)
+    sec = timed_steps(lambda i: graph.replay(), steps, warmup)
+    n = n_dec + n_pre
+    log(f"mixed24: graph {sec * 1e3:.3f} ms/step ({n / sec:.0f} tok/s), eager {eager_s * 1e3:.3f} ms")
+    flops = layers * (block_flops(n_dec, 32) + block_flops(n_pre, 32))
+    # each group's call streams the layer's weights (all 32 experts touched)
+    bytes_ = layers * (block_bytes(n_dec, 32, 32) + block_bytes(n_pre, 32, 32))
+    res = {"workload": MIXED[1], "layers": layers, "tokens": n, "ms_per_step": round(sec * 1e3, 4),
+           "tok_s": round(n / sec, 1), "eager_ms_per_step": round(eager_s * 1e3, 4),
+           "bf16_mfma_frac": round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4),
+           "hbm_frac": round(bytes_ / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_flops": int(flops)}
+    del graph, stack, pairs
+    return res
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(blocks, xs, n_sample: int):
+    """Serial C restatement of model/mlp.py on the first n_sample tokens (weight
+    set 0), then the same restatement with OpenMP over (token, slot) on every
+    core this process may use, on all tokens of every weight set."""
     import numpy as np
     import torch
 
@@ -109,22 +335,38 @@ def cpu_baseline(blk, x, n_sample: int):
     def u16(t):
         return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
-    p = O.BlockParams(u16(blk.norm.weight), u16(blk.gate.weight), u16(blk.gate.bias),
-                      blk.mlp1_weight_blocks.cpu().numpy(), blk.mlp1_weight_scales.cpu().numpy(),
-                      u16(blk.mlp1_bias), blk.mlp2_weight_blocks.cpu().numpy(),
-                      blk.mlp2_weight_scales.cpu().numpy(), u16(blk.mlp2_bias))
-    xs = u16(x.reshape(-1, H))[:n_sample]
+    def params(blk):
+        return O.BlockParams(u16(blk.norm.weight), u16(blk.gate.weight), u16(blk.gate.bias),
+                             blk.mlp1_weight_blocks.cpu().numpy(), blk.mlp1_weight_scales.cpu().numpy(),
+                             u16(blk.mlp1_bias), blk.mlp2_weight_blocks.cpu().numpy(),
+                             blk.mlp2_weight_scales.cpu().numpy(), u16(blk.mlp2_bias))
+
+    ps = [params(b) for b in blocks]
+    xh = [u16(x.reshape(-1, H)) for x in xs]
     t0 = time.perf_counter()
-    out, _, idx, _ = moe_ref.block_forward(xs, p, k=K_TOP, nthreads=1)
+    out, _, idx, _ = moe_ref.block_forward(xh[0][:n_sample], ps[0], k=K_TOP, nthreads=1)
     dt = time.perf_counter() - t0
-    gpu_out = u16(blk(x.reshape(1, -1, H)).reshape(-1, H))[:n_sample]
+    gpu_out = u16(blocks[0](xs[0]).reshape(-1, H))[:n_sample]
     parity = O.compare_outputs(gpu_out, out)
-    gpu_idx = blk.route(x.reshape(-1, H))[1].cpu().numpy()[:n_sample]
+    gpu_idx = blocks[0].route(xs[0].reshape(-1, H))[1].cpu().numpy()[:n_sample]
     parity["routing_equal"] = bool(np.array_equal(gpu_idx, idx))
+    cores = len(os.sched_getaffinity(0))
+    tot = 0
+    t0 = time.perf_counter()
+    for x, p in zip(xh, ps):
+        moe_ref.block_forward(x, p, k=K_TOP, nthreads=cores)
+        tot += x.shape[0]
+    dt_all = time.perf_counter() - t0
+    model = cpu_model()
     return {
         "value": round(n_sample / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+        "cpu_model": model,
         "sample": (f"first {n_sample} tokens of the workload batch with weight set 0, serial C "
                    f"restatement of model/mlp.py (oracle/moe_ref.c, 1 thread), {dt:.1f} s"),
+        "all_cores": {"value": round(tot / dt_all, 3), "unit": "tok/s", "cores": cores,
+                      "kind": "port", "cpu_model": model,
+                      "sample": (f"all {tot} tokens of the {len(xs)} weight sets, the same "
+                                 f"restatement with OpenMP over (token, slot), {dt_all:.1f} s")},
     }, parity
 
 
@@ -137,6 +379,10 @@ def main() -> int:
     ap.add_argument("--weight-sets", type=int, default=3)
     ap.add_argument("--cpu-tokens", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="time only the primary workload")
+    ap.add_argument("--secondary", default="decode1,prefill4096,decode256_120b,prefill2048_120b,mixed24",
+                    help="comma-separated secondary workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 512 MiB (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
@@ -157,131 +403,48 @@ def main() -> int:
         log("copy calibration: 5 x 512 MiB device copies")
         return 0
 
-    from oracle import moe_oracle as O
-
     dev = torch.device("cuda:0")
-    E, n, beta, label = CONFIGS[args.config]
-    log(f"workload {args.config}: E={E} n={n} zipf_beta={beta}")
-    blocks = [make_block(E, 1000 + i, beta, dev) for i in range(args.weight_sets)]
-    gx = torch.Generator(device=dev)
-    gx.manual_seed(7)
-    xs = [torch.randn((1, n, H), generator=gx, device=dev).to(torch.bfloat16)
-          for _ in range(args.weight_sets)]
-    torch.cuda.synchronize()
-    log("weights ready")
-
-    # routing statistics (touched experts per weight set) for the algorithmic bytes
-    touched = []
-    for blk, x in zip(blocks, xs):
-        st = blk.forward_staged(x)
-        cnt = torch.diff(st["perm"]["indptr"])
-        touched.append(int((cnt > 0).sum()))
-    max_load = float((cnt.max().float() / cnt.float().mean()).item())
-
-    nw = len(blocks)
-    for i in range(args.warmup):
-        blocks[i % nw](xs[i % nw])
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        blocks[i % nw](xs[i % nw])
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    ms_per_step = dt / args.steps * 1e3
-    value = n / (dt / args.steps)
-    log(f"timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {value:.0f} tok/s")
-
-    # both prefill configs average 48 or more pairs per expert: the tiled GEMM
-    mfma_bound = args.config.startswith("prefill")
-    # At decode the block runs mlp1, the act encoding and mlp2 as one launch
-    # (moe_mlp_decode) where the shape allows it: that launch is the one timed.
-    fused = False
-    if not mfma_bound and n <= 128:
-        try:
-            blocks[0].forward_staged(xs[0], fused_decode=True)
-            fused = True
-        except RuntimeError as e:
-            log(f"mlp_decode not used: {e}")
-    torch.cuda.synchronize()
-
-    # second pass: per-stage HIP events on the launch stream.  A spin kernel is
-    # queued first so the host runs ahead of the GPU and the events time the
-    # kernels, not gaps left by Python between launches.
-    if fused:
-        stages = ("router", "permute", "pieces_t", "mlp_decode", "combine")
-    else:
-        stages = ("router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine")
-    recs = []
-    torch.cuda._sleep(int(2.4e9 * 0.4e-3 * args.steps))
-    for i in range(args.steps):
-        ev = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for s in stages}
-        blocks[i % nw].forward_staged(xs[i % nw], events=ev, fused_decode=fused)
-        recs.append(ev)
-    torch.cuda.synchronize()
-    stage_us = {s: sum(r[s][0].elapsed_time(r[s][1]) for r in recs) / len(recs) * 1e3
-                for s in stages}
-    log("stage us: " + ", ".join(f"{s}={v:.1f}" for s, v in stage_us.items()))
-
-    g1, g2 = H // 32, I // 32
-    mlp1_weight_bytes = 2 * I * g1 * 17 + 2 * I * 2
-    mlp2_weight_bytes = H * g2 * 17 + H * 2
-    avg_touched = sum(touched) / len(touched)
-    nk = n * K_TOP
-    flops_per_step = O.flops(n, K_TOP, E, H, I)
-    if fused:
-        # weights of the touched experts, t in (two 1-byte pieces per element),
-        # act's three pieces written and read back, y out (fp32)
-        alg = (avg_touched * (mlp1_weight_bytes + mlp2_weight_bytes) + n * H * 2 +
-               2 * nk * I * 3 + nk * H * 4)
-        achieved = alg / (stage_us["mlp_decode"] * 1e-6) / 1e9
-        roof = {"bound": "hbm",
-                "kernel": "moe_mx_decode_kernel (mlp1 + SwiGLU + act pieces + mlp2)",
-                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": read_traffic(args.config, "moe::moe_mx_decode_kernel"),
-                "algorithmic_bytes": int(alg), "avg_us": round(stage_us["mlp_decode"], 2)}
-    elif not mfma_bound:
-        alg = avg_touched * mlp1_weight_bytes + n * H * 2 + nk * I * 4
-        achieved = alg / (stage_us["mlp1"] * 1e-6) / 1e9
-        roof = {"bound": "hbm", "kernel": "moe_mx_gemv_kernel<2,1,23> (mlp1)",
-                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": read_traffic(args.config, "moe::moe_mx_gemv_kernel<2, 1, 23>"),
-                "algorithmic_bytes": int(alg), "avg_us": round(stage_us["mlp1"], 2)}
-    else:
-        f1 = 2 * nk * 2 * I * H
-        achieved = f1 / (stage_us["mlp1"] * 1e-6) / 1e12
-        roof = {"bound": "mfma", "kernel": "mlp1", "achieved": round(achieved, 2),
-                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                "traffic": read_traffic(args.config, "moe::moe_mx_gemm_kernel<2, 1>"),
-                "algorithmic_flops": int(f1),
-                "avg_us": round(stage_us["mlp1"], 2)}
-
-    block_bytes = O.algorithmic_bytes(n, round(avg_touched), E, H, I)
+    prim, blocks, xs = run_block_config(args.config, args.steps, args.warmup, args.weight_sets, dev)
+    E, n, _, label = CONFIGS[args.config]
+    us = prim["us_per_block"]
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "metric": METRIC, "value": prim["tok_s"], "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us * 1e-3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": DTYPE,
         "data": "synthetic (seeded random MXFP4 weights and bf16 N(0,1) tokens, BASELINE distributions)",
         "config": {"workload": label, "tokens": n, "experts": E, "top_k": K_TOP, "hidden": H,
-                   "intermediate": I, "weight_sets": nw, "touched_experts": avg_touched,
-                   "max_over_mean_load": round(max_load, 2)},
-        "block": {"hbm_gbs": round(block_bytes / (ms_per_step * 1e-3) / 1e9, 1),
-                  "hbm_frac": round(block_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                  "tflops": round(flops_per_step / (ms_per_step * 1e-3) / 1e12, 2),
-                  "algorithmic_bytes": int(block_bytes)},
-        "stages_us": {s: round(v, 2) for s, v in stage_us.items()},
-        "roofline": roof,
+                   "intermediate": I, "weight_sets": len(blocks),
+                   "touched_experts": prim["touched_experts"],
+                   "max_over_mean_load": prim["max_over_mean_load"]},
+        "block": {"hbm_gbs": round(prim["block_hbm_frac"] * HBM_PEAK_GBS, 1),
+                  "hbm_frac": prim["block_hbm_frac"],
+                  "tflops": round(prim["block_bf16_mfma_frac"] * BF16_PEAK_TFLOPS, 2),
+                  "algorithmic_bytes": prim["algorithmic_bytes"]},
+        "stages_us": prim["stages_us"],
+        "roofline": prim["roofline"],
     }
     if not args.no_cpu:
         ns = min(args.cpu_tokens, n)
-        log(f"cpu baseline on {ns} tokens")
-        cb, parity = cpu_baseline(blocks[0], xs[0], ns)
+        log(f"cpu baseline on {ns} tokens (+ all cores)")
+        cb, parity = cpu_baseline(blocks, xs, ns)
         line["cpu_baseline"] = cb
         line["parity_vs_cpu"] = parity
     else:
         line["cpu_baseline"] = None
+    del blocks, xs
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
+        sec = {}
+        for name in [s for s in args.secondary.split(",") if s and s != args.config]:
+            if name == MIXED[0]:
+                sec[name] = run_mixed(10, 2, dev)
+            else:
+                st = 30 if CONFIGS[name][1] >= 2048 else 100
+                res, b, x = run_block_config(name, st, 5, args.weight_sets, dev)
+                del b, x
+                sec[name] = res
+            torch.cuda.empty_cache()
+        line["secondary"] = sec
     print(json.dumps(line), flush=True)
     return 0
 

@@ -141,11 +141,35 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
   *total = o;
 }
 
+// mlp1 + SwiGLU with act written as its three fp8 pieces (rows by sorted
+// position).  With the tiled GEMM (48 or more pairs per expert on average)
+// the epilogue encodes act directly (a 192-column tile holds whole
+// 32-element blocks of act): no fp32 act round trip and no encoding pass.
+// Otherwise the grouped GEMV writes fp32 act and the pieces kernel encodes it.
+int mlp1_pieces(const void* t_pk, int64_t n, int64_t k, int64_t E, int64_t H, int64_t I,
+                const int32_t* indptr, const int32_t* sp, const void* blocks, const void* scales,
+                const void* bias, float alpha, float limit, float* act, void* act_pk,
+                hipStream_t s) {
+  const int nk = (int)(n * k);
+  int rc;
+  if ((int64_t)nk >= kGemmMinTokens * E && ((uintptr_t)bias & 15u) == 0) {
+    rc = moe_launch_mx_gemm(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, blocks, scales,
+                            bias, (int)E, (int)(2 * I), (int)H, nk, 2, alpha, limit, act_pk,
+                            (int)I, (char*)act_pk + moe_pieces_q_bytes(nk, I, kPiecesAct), s);
+    if (rc != MOE_ERR_UNSUPPORTED) return rc;
+  }
+  if ((rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, blocks, scales, bias,
+                          (int)E, (int)(2 * I), (int)H, (int)n, nk, 1, alpha, limit, act, (int)I,
+                          s)))
+    return rc;
+  return moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s);
+}
+
 }  // namespace
 
 extern "C" {
 
-int moe_version(void) { return 100; }
+int moe_version(void) { return 200; }
 
 const char* moe_status_string(int status) {
   switch (status) {
@@ -294,6 +318,23 @@ int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr, const int32_t* 
                        alpha, limit, act, (int)I, as_stream(stream));
 }
 
+int moe_mlp1_swiglu_pieces(const void* t_pieces, const int32_t* indptr,
+                           const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E,
+                           int64_t H, int64_t I, const uint8_t* blocks, const uint8_t* scales,
+                           const uint16_t* bias, float alpha, float limit, float* act,
+                           void* act_pieces, moe_stream_t stream) {
+  int rc = check_dims(n, E, k, H, I);
+  if (rc) return rc;
+  if (n == 0) return MOE_OK;
+  if (!t_pieces || !indptr || !sorted_pairs || !blocks || !scales || !bias || !act ||
+      !act_pieces)
+    return MOE_ERR_NULL;
+  if (!aligned16(t_pieces) || !aligned16(blocks) || !aligned16(act) || !aligned16(act_pieces))
+    return MOE_ERR_ALIGN;
+  return mlp1_pieces(t_pieces, n, k, E, H, I, indptr, sorted_pairs, blocks, scales, bias, alpha,
+                     limit, act, act_pieces, as_stream(stream));
+}
+
 int moe_mlp2(const void* act_pieces, const int32_t* indptr, const int32_t* sorted_pairs, int64_t n,
              int64_t k, int64_t E, int64_t H, int64_t I, const uint8_t* blocks,
              const uint8_t* scales, const uint16_t* bias, float* y, moe_stream_t stream) {
@@ -428,26 +469,16 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
       return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s);
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }
-  // With the tiled GEMM, mlp1's epilogue writes act's three pieces directly
-  // (a 192-column tile holds whole 32-element blocks of act): no fp32 act
-  // round trip and no separate encoding pass.
-  bool act_encoded = false;
-  if (gemm && ((uintptr_t)mlp1_bias & 15u) == 0) {
-    rc = moe_launch_mx_gemm(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
-                            mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, nk, 2, alpha,
-                            limit, act_pk, (int)I,
-                            (char*)act_pk + moe_pieces_q_bytes(nk, I, kPiecesAct), s);
-    if (rc == MOE_OK) act_encoded = true;
-    else if (rc != MOE_ERR_UNSUPPORTED) return rc;
-  }
-  if (!act_encoded &&
-      (rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
-                          mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk, 1, alpha,
-                          limit, act, (int)I, s)))
-    return rc;
   if (gemm) {
-    if (!act_encoded && (rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s)))
+    if ((rc = mlp1_pieces(t_pk, n, k, E, H, I, indptr, sp, mlp1_blocks, mlp1_scales, mlp1_bias,
+                          alpha, limit, act, act_pk, s)))
       return rc;
+  } else if ((rc = expert_matmul(t_pk, (int)n, kPiecesT, indptr, sp, (int)k, 0, 1, mlp1_blocks,
+                                 mlp1_scales, mlp1_bias, (int)E, (int)(2 * I), (int)H, (int)n, nk,
+                                 1, alpha, limit, act, (int)I, s))) {
+    return rc;
+  }
+  if (gemm) {
     if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
                             mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f,
                             y, (int)H, s)))

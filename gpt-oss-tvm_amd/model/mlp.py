@@ -212,7 +212,7 @@ class MLPBlock(torch.nn.Module):
                                      workspace, out=out)
 
     def forward_staged(self, x: torch.Tensor, events: dict | None = None,
-                       fused_decode: bool = False) -> dict:
+                       fused_decode: bool = False, pieces_epilogue: bool = False) -> dict:
         """The same chain, one C call per stage, returning every intermediate.
 
         ``events`` (optional) maps stage names to (start, end) torch.cuda.Event
@@ -220,7 +220,9 @@ class MLPBlock(torch.nn.Module):
         "router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine",
         or with ``fused_decode`` (the decode chain in one launch, mlp_decode;
         at most 128 tokens) "mlp_decode" in place of the middle three, and
-        "act" is None.
+        "act" is None.  With ``pieces_epilogue`` mlp1 writes act's fp8 pieces
+        itself (mlp1_swiglu_pieces, the block's prefill kernels): "pieces_act"
+        is then empty and "act" None.
         """
         b, seq_len, dim = x.shape
         n = b * seq_len
@@ -255,12 +257,20 @@ class MLPBlock(torch.nn.Module):
             return {"t": t, "idx": idx, "w": w, "perm": perm, "act": None,
                     "act_pieces": act_pk, "y": y, "out": out.reshape(b, seq_len, dim)}
         rec("mlp1", 0)
-        act = _native.mlp1_swiglu(t_pk, n, dim, perm["indptr"], perm["sorted_pairs"], k,
-                                  self.mlp1_weight_blocks, self.mlp1_weight_scales, self.mlp1_bias,
-                                  SWIGLU_ALPHA, self.swiglu_limit)
-        rec("mlp1", 1)
-        rec("pieces_act", 0)
-        act_pk = _native.quantize_pieces(act, 3)
+        if pieces_epilogue:
+            act_pk, _ = _native.mlp1_swiglu_pieces(
+                t_pk, n, dim, perm["indptr"], perm["sorted_pairs"], k, self.mlp1_weight_blocks,
+                self.mlp1_weight_scales, self.mlp1_bias, SWIGLU_ALPHA, self.swiglu_limit)
+            act = None
+            rec("mlp1", 1)
+            rec("pieces_act", 0)
+        else:
+            act = _native.mlp1_swiglu(t_pk, n, dim, perm["indptr"], perm["sorted_pairs"], k,
+                                      self.mlp1_weight_blocks, self.mlp1_weight_scales,
+                                      self.mlp1_bias, SWIGLU_ALPHA, self.swiglu_limit)
+            rec("mlp1", 1)
+            rec("pieces_act", 0)
+            act_pk = _native.quantize_pieces(act, 3)
         rec("pieces_act", 1)
         rec("mlp2", 0)
         y = _native.mlp2(act_pk, perm["indptr"], perm["sorted_pairs"], n, k,

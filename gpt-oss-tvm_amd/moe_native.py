@@ -44,6 +44,8 @@ _SIGS = {
     "moe_quantize_pieces": ([_P, _INT, _I64, _I64, _INT, _P, _P], _INT),
     "moe_mlp1_swiglu": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P, _P],
                         _INT),
+    "moe_mlp1_swiglu_pieces": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _F, _P,
+                                _P, _P], _INT),
     "moe_mlp2": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P], _INT),
     "moe_mlp_decode": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _F, _F,
                         _P, _P, _P, _P], _INT),
@@ -233,6 +235,33 @@ def mlp1_swiglu(t_pieces, n, H, indptr, sorted_pairs, k, blocks, scales, bias, a
                                 inter, _ptr(blocks), _ptr(scales), _ptr(bias), alpha, limit,
                                 _ptr(act), _stream()), "moe_mlp1_swiglu")
     return act
+
+
+def mlp1_swiglu_pieces(t_pieces, n, H, indptr, sorted_pairs, k, blocks, scales, bias, alpha,
+                       limit, act=None, act_pieces=None):
+    """mlp1 + SwiGLU -> act's three fp8 pieces (the block's prefill form).
+
+    Returns (act_pieces, act): act [n*k, I] fp32 is scratch, written only when
+    the grouped GEMV runs (fewer than 48 pairs per expert on average).
+    """
+    E, N2, G, _ = blocks.shape
+    inter = N2 // 2
+    _expect(t_pieces, "t_pieces", torch.uint8)
+    if t_pieces.numel() < pieces_bytes(n, H, 2):
+        raise ValueError("t_pieces: buffer smaller than pieces_bytes(n, H, 2)")
+    _expect(blocks, "mlp1_weight_blocks", torch.uint8, (E, 2 * inter, H // 32, 16))
+    _expect(scales, "mlp1_weight_scales", torch.uint8, (E, 2 * inter, H // 32))
+    _expect(bias, "mlp1_bias", torch.bfloat16, (E, 2 * inter))
+    if act is None:
+        act = torch.empty((n * k, inter), dtype=torch.float32, device=blocks.device)
+    if act_pieces is None:
+        act_pieces = torch.empty(pieces_bytes(n * k, inter, 3), dtype=torch.uint8,
+                                 device=blocks.device)
+    _check(_lib.moe_mlp1_swiglu_pieces(_ptr(t_pieces), _ptr(indptr), _ptr(sorted_pairs), n, k, E,
+                                       H, inter, _ptr(blocks), _ptr(scales), _ptr(bias), alpha,
+                                       limit, _ptr(act), _ptr(act_pieces), _stream()),
+           "moe_mlp1_swiglu_pieces")
+    return act_pieces, act
 
 
 def mlp2(act_pieces, indptr, sorted_pairs, n, k, blocks, scales, bias, y=None):

@@ -164,6 +164,24 @@ MOE_API int moe_mlp1_swiglu(const void* t_pieces, const int32_t* indptr,
                             moe_stream_t stream);
 
 /*
+ * mlp1 with the SwiGLU epilogue, its output act written as the three fp8 pieces
+ * moe_mlp2 takes (moe_quantize_pieces(act, 1, n*k, I, 3), rows by sorted
+ * position), as moe_block_forward runs it at prefill: with 48 or more pairs
+ * per expert on average the tiled GEMM's epilogue encodes act directly (act
+ * is not written); below that the grouped GEMV writes act, fp32 [n*k, I]
+ * (caller-owned scratch), and the encoding follows.
+ * Replaces: mxfp4_moe_mlp1_prefill, model/mlp_optimized.py:214-351 (its bf16
+ * act output becomes fp8 pieces here), with the fp32 semantics of
+ * model/mlp.py:387-390.  act_pieces: moe_pieces_bytes(n*k, I, 3) bytes.
+ */
+MOE_API int moe_mlp1_swiglu_pieces(const void* t_pieces, const int32_t* indptr,
+                                   const int32_t* sorted_pairs, int64_t n, int64_t k, int64_t E,
+                                   int64_t H, int64_t I, const uint8_t* blocks,
+                                   const uint8_t* scales, const uint16_t* bias, float alpha,
+                                   float limit, float* act, void* act_pieces,
+                                   moe_stream_t stream);
+
+/*
  * mlp2 over grouped pairs.
  * Replaces: mxfp4_moe_mlp2_{prefill,decode}, model/mlp_optimized.py:353-460, 573-660,
  * with the fp32 semantics of model/mlp.py:395.

@@ -538,3 +538,23 @@ def test_gemv_gating_without_residual(native):
         assert np.array_equal(got, O.gating(y, w))
         got = host_bf16(native.gemv_gating(f32_dev(y), bf16_dev(w), bf16_dev(x)))
         assert np.array_equal(got, O.residual_add(x, O.gating(y, w)))
+
+
+@pytest.mark.parametrize("n,seed", [(520, 29), (64, 30)])
+def test_mlp1_swiglu_pieces(native, block20b, n, seed):
+    """moe_mlp1_swiglu_pieces (the block's prefill mlp1: the tiled GEMM's
+    epilogue encodes act, n = 520; below 48 pairs per expert the GEMV and the
+    encoding pass, n = 64) = quantize_pieces(mlp1_swiglu(...), 3), bit for bit."""
+    p, blk = block20b
+    x = bf16_dev(O.make_input(seed, n)).view(1, n, 2880)
+    st = blk.forward_staged(x)
+    t_pk = native.quantize_pieces(st["t"], 2)
+    perm, k, nk = st["perm"], 4, n * 4
+    pk, _ = native.mlp1_swiglu_pieces(t_pk, n, 2880, perm["indptr"], perm["sorted_pairs"], k,
+                                      blk.mlp1_weight_blocks, blk.mlp1_weight_scales,
+                                      blk.mlp1_bias, 1.702, blk.swiglu_limit)
+    ref = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), nk, 2880, 3)
+    for a, b in zip(PM.unpack(host(pk), nk, 2880, 3), ref):
+        assert np.array_equal(a, b), np.argwhere(a != b)[:4]
+    st2 = blk.forward_staged(x, pieces_epilogue=True)
+    assert np.array_equal(host_bf16(st2["out"]), host_bf16(st["out"]))
