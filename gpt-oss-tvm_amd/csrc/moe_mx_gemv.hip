@@ -394,6 +394,9 @@ __device__ __forceinline__ void mx_pass(
     int rm = 0;
     if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
     if (threadIdx.x == 0) *tile_ctr = 0;
+    // the wait's first poll goes out ahead of the tile loads: loads return in
+    // issue order, so a poll issued after them would wait for all of them
+    wait.pre(sg.e);
     __builtin_amdgcn_sched_barrier(0);
     issue_h0(sg.e, sg.t0 + (wave < sg.len ? wave : 0));
     if (wave < sg.len)
@@ -816,7 +819,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint16_t* __restrict__ bias1, const uint8_t* __restrict__ blocks2,
     const uint8_t* __restrict__ scales2, const uint16_t* __restrict__ bias2, int H, int E,
     int gcap2, float alpha, float limit, uint8_t* aq, uint8_t* aqs, float* __restrict__ y,
-    int* done, int* status, int spin_max, int xcds) {
+    int* done, int* status, int spin_max, int prepoll, int xcds) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kGroupBytes = mx_group_bytes(23);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -911,22 +914,38 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   }
 
   // Phase 2: wait for all of expert e's mlp1 tiles, then stage its pieces.
-  auto wait_mlp1 = [&](int e, int, int) {
-    if (threadIdx.x == 0) {
-      const int target = ntiles1 * ((ipl[e + 1] - ipl[e] + tpb1 - 1) / tpb1);
-      bool seen = false;
-      for (int it = 0; it < spin_max; ++it) {
-        if (__hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
-          seen = true;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-      // gave up: the staged pieces may be incomplete; report it
-      if (!seen) __hip_atomic_fetch_add(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // One thread polls done[e], at most spin_max times, sleeping between
+  // polls; spin_max == 0 gives up without polling.  With prepoll the first
+  // poll is issued before the segment's tile loads (pre) and read here.
+  struct WaitMlp1 {
+    const int* ipl;
+    int* done;
+    int* status;
+    int spin_max, ntiles1, tpb1, prepoll;
+    int first;
+    __device__ __forceinline__ int target(int e) const {
+      return ntiles1 * ((ipl[e + 1] - ipl[e] + tpb1 - 1) / tpb1);
     }
-    lds_barrier();  // the staging's sc1 loads are issued after the count was seen
+    __device__ __forceinline__ void pre(int e) {
+      if (threadIdx.x == 0 && spin_max > 0 && prepoll)
+        first = __hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __device__ __forceinline__ void operator()(int e, int, int) {
+      if (threadIdx.x == 0) {
+        const int tg = target(e);
+        const bool pre_polled = prepoll && spin_max > 0;
+        bool seen = pre_polled && first >= tg;
+        for (int it = pre_polled ? 1 : 0; !seen && it < spin_max; ++it) {
+          seen = __hip_atomic_load(done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= tg;
+          if (!seen) __builtin_amdgcn_s_sleep(2);
+        }
+        // gave up: the staged pieces may be incomplete; report it
+        if (!seen) __hip_atomic_fetch_add(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      lds_barrier();  // the staging's sc1 loads are issued after the count was seen
+    }
   };
+  WaitMlp1 wait_mlp1{ipl, done, status, spin_max, ntiles1, tpb1, prepoll, 0};
   MxSeg s2;
   mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
       lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
@@ -1102,6 +1121,14 @@ static int decode_waves() {
   return w;
 }
 
+// The decode launch's first poll goes out before the phase-2 tile loads only
+// for batches of at most this many (token, expert) pairs.  There the mlp1
+// tiles are few and usually finished when phase 2 starts, and the early poll
+// spares the wait behind the tile loads (about 1.5 us of the 40 us launch at
+// one token, measured); with more pairs the extra round trip per segment
+// costs more than it saves (about 4 us of 110 us at 64 tokens).
+constexpr int kDecodePrepollMaxPairs = 16;
+
 static size_t decode_lds_bytes(int E, int H) {
   using namespace moe;
   return (size_t)kMxMaxGroups * mx_group_bytes(23) + decode_waves() * 16 * (H / 32) +
@@ -1193,7 +1220,7 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                      (const uint8_t*)scales2, (const uint16_t*)bias2, H, E, gcap2, alpha, limit,
                      aq, aq + moe_pieces_q_bytes(nk, I, 3), (float*)y, (int*)done,
                      (int*)status, g_decode_spin_max.load(std::memory_order_relaxed),
-                     grid % kNumXcds == 0 ? kNumXcds : 1);
+                     nk <= kDecodePrepollMaxPairs ? 1 : 0, grid % kNumXcds == 0 ? kNumXcds : 1);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
