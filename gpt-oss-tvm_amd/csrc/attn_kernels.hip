@@ -1,0 +1,549 @@
+// gpt-oss attention block kernels (gfx950): RMSNorm, QKV bias + YaRN RoPE +
+// paged KV append, decode attention (split over pages, merged with the sink
+// scaling), prefill / extend attention on bf16 MFMA, bias + residual, and the
+// embedding gather.
+//
+// Reference: model/attention.py:182-256 (AttentionBlock.forward), the masks of
+// tvm_fix.patch:36-47, mlc-llm's PagedKVCache page layout
+// [pages, 2 (k, v), kv_heads, page_size, head_dim] (model/transformer.py:
+// 153-175 creates it with page_size 16, engine.py:97-107).
+//
+// Shapes fixed by gpt-oss: head_dim 64, 64 query heads, 8 key/value heads
+// (GQA groups of 8), pages of 16 tokens.  The host checks them.
+#include "moe_common.h"
+
+namespace attn {
+
+using moe::bf16x8;
+using moe::bf2f;
+using moe::f2bf;
+using moe::f32x4;
+using moe::kWave;
+using moe::u32x4;
+
+constexpr int kD = 64;          // head_dim
+constexpr int kHq = 64;         // query heads
+constexpr int kHkv = 8;         // key/value heads
+constexpr int kGroup = kHq / kHkv;
+constexpr int kPage = 16;       // tokens per page
+constexpr int kQkvHeads = kHq + 2 * kHkv;
+// bytes of one (page, k or v, head) block: 16 tokens x 64 dims x bf16
+constexpr int kHeadBlock = kPage * kD * 2;
+constexpr int kPageBytes = 2 * kHkv * kHeadBlock;  // 32 KB per page per layer
+
+__device__ __forceinline__ const uint16_t* kv_row(const uint8_t* cache, int page, int kv, int hk,
+                                                  int slot) {
+  return (const uint16_t*)(cache + (size_t)page * kPageBytes + (size_t)(kv * kHkv + hk) * kHeadBlock +
+                           slot * (kD * 2));
+}
+
+// A sequence's page list: the page holding position pos.  The list index is
+// clamped to the sequence's pages and the page id to the pool, so a page table
+// that does not cover kv_len reads wrong keys instead of foreign memory (the
+// host sizes the tables; this only keeps a bad table from faulting).
+struct PageList {
+  const int* ids;
+  int count, pool;
+  __device__ __forceinline__ int page_of(int pos) const {
+    const int i = min(pos / kPage, count - 1);
+    return min(max(ids[max(i, 0)], 0), pool - 1);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// RMSNorm (attention.py:80, nn.RMSNorm): sum of squares of the bf16 inputs in
+// fp64 (exact for inputs spanning less than 2^37), r = fp32(1/sqrt(ss/H +
+// eps)) in fp64, t = bf16(fp32(x r) w).  One 256-thread workgroup per token.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x, int H,
+                                                       const uint16_t* __restrict__ w, float eps,
+                                                       uint16_t* __restrict__ out) {
+  __shared__ double part[4];
+  const int tok = blockIdx.x;
+  const uint16_t* xr = x + (size_t)tok * H;
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const double v = (double)bf2f(xr[i]);
+    ss += v * v;
+  }
+  ss = moe::wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float r = (float)(1.0 / sqrt(tot / (double)H + (double)eps));
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float xv = __fmul_rn(bf2f(xr[i]), r);
+    out[(size_t)tok * H + i] = f2bf(__fmul_rn(xv, bf2f(w[i])));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// QKV epilogue: bias (a second bf16 rounding after the matmul's, nn.Linear),
+// YaRN RoPE of q and k (attention.py:126-165), the new k and v written to
+// their cache slots (append_mha_kv), q written [token][head][dim].
+// cos/sin of fp32(position) * inv_freq are evaluated in fp64, rounded to fp32
+// and then to bf16 (the rope's .astype(dtype)), then scaled by the fp32
+// concentration; the rotation rounds each product and the difference / sum
+// separately (no contraction).  One thread per rotation pair (d, d + 32):
+// 256 threads = 8 heads of one token; grid (10, n).
+__global__ __launch_bounds__(256) void qkv_rope_append_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ bias,
+    const int* __restrict__ positions, const int* __restrict__ slots,
+    const float* __restrict__ inv_freq, float conc, uint8_t* __restrict__ cache, int num_pages,
+    uint16_t* __restrict__ q_out) {
+#pragma clang fp contract(off)
+  const int tok = blockIdx.y;
+  const int head = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int d = threadIdx.x & 31;
+  const size_t base = (size_t)tok * (kQkvHeads * kD) + head * kD;
+  float lo = bf2f(f2bf(bf2f(qkv[base + d]) + bf2f(bias[head * kD + d])));
+  float hi = bf2f(f2bf(bf2f(qkv[base + d + 32]) + bf2f(bias[head * kD + d + 32])));
+  const int slot = slots[tok];
+  if (head < kHq + kHkv) {
+    const float freq = (float)positions[tok] * inv_freq[d];
+    const double fd = (double)freq;
+    const float c = bf2f(f2bf((float)cos(fd))) * conc;
+    const float s = bf2f(f2bf((float)sin(fd))) * conc;
+    const float nlo = lo * c - hi * s;
+    const float nhi = lo * s + hi * c;
+    lo = nlo;
+    hi = nhi;
+  }
+  const uint16_t blo = f2bf(lo), bhi = f2bf(hi);
+  if (head < kHq) {
+    uint16_t* qo = q_out + ((size_t)tok * kHq + head) * kD;
+    qo[d] = blo;
+    qo[d + 32] = bhi;
+  } else if (slot >= 0 && slot < num_pages * kPage) {  // other slots are not written
+    const int kv = head < kHq + kHkv ? 0 : 1;
+    const int hk = head - kHq - kv * kHkv;
+    uint16_t* row = (uint16_t*)kv_row(cache, slot / kPage, kv, hk, slot % kPage);
+    row[d] = blo;
+    row[d + 32] = bhi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention, phase 1: workgroup (split s, kv head hk, sequence b)
+// takes keys [lo + 128 s, lo + 128 (s + 1)) of the sequence's attended range
+// [lo, kv_len) for the 8 query heads of hk, and writes the partial softmax
+// state of each head: m (max score), l (sum of exp(score - m)) and
+// o[64] = sum exp(score - m) v.  Scores in fp32 (q.k * sm_scale).
+constexpr int kDecChunk = 128;
+
+__global__ __launch_bounds__(256) void decode_partial_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ cache,
+    const int* __restrict__ page_indptr, const int* __restrict__ page_indices, int num_pages,
+    const int* __restrict__ kv_len, int window, float sm_scale, int splits,
+    float* __restrict__ part_o, float* __restrict__ part_ml) {
+  __shared__ float qs[kGroup][kD];
+  __shared__ float sc[kGroup][kDecChunk];
+  __shared__ float red[kGroup][2];
+  const int s = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x;
+  const int L = kv_len[b];
+  const int lo = window > 0 ? max(0, L - window) : 0;
+  const int k0 = lo + s * kDecChunk;
+  const int nk = max(0, min(kDecChunk, L - k0));
+  const size_t pidx = ((size_t)b * kHq + hk * kGroup) * splits + s;  // head h: + h * splits
+  if (nk == 0) {
+    if (t < kGroup) {
+      part_ml[(pidx + (size_t)t * splits) * 2 + 0] = -INFINITY;
+      part_ml[(pidx + (size_t)t * splits) * 2 + 1] = 0.0f;
+    }
+    return;
+  }
+  for (int i = t; i < kGroup * kD; i += 256)
+    qs[i / kD][i % kD] = bf2f(q[((size_t)b * kHq + hk * kGroup) * kD + i]);
+  __syncthreads();
+  const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
+                       num_pages};
+  {
+    // scores: thread -> key t % 128, heads 4 (t / 128) .. + 3
+    const int kk = t & (kDecChunk - 1);
+    const int h0 = (t >> 7) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (kk < nk) {
+      const int pos = k0 + kk;
+      const u32x4* kr = (const u32x4*)kv_row(cache, pages.page_of(pos), 0, hk, pos % kPage);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const u32x4 v = kr[c];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __uint_as_float(v[j] << 16), e1 = __uint_as_float(v[j] & 0xFFFF0000u);
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            acc[h] = fmaf(e1, qs[h0 + h][c * 8 + 2 * j + 1], fmaf(e0, qs[h0 + h][c * 8 + 2 * j], acc[h]));
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sc[h0 + h][kk] = kk < nk ? acc[h] * sm_scale : -INFINITY;
+  }
+  __syncthreads();
+  {
+    // per head max and exp: wave w takes heads 2w, 2w + 1 (2 scores per lane)
+    const int w = t >> 6, lane = t & 63;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int h = 2 * w + hh;
+      const float a = sc[h][lane], c = sc[h][lane + 64];
+      float m = fmaxf(a, c);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+      const float pa = lane < nk ? __expf(a - m) : 0.0f;
+      const float pc = lane + 64 < nk ? __expf(c - m) : 0.0f;
+      sc[h][lane] = pa;
+      sc[h][lane + 64] = pc;
+      const float l = moe::wave_sum(pa + pc);
+      if (lane == 0) {
+        red[h][0] = m;
+        red[h][1] = l;
+      }
+    }
+  }
+  __syncthreads();
+  {
+    // o[h][d]: thread -> dim t % 64, heads t / 64 and t / 64 + 4
+    const int d = t & 63, h0 = t >> 6;
+    float o0 = 0.f, o1 = 0.f;
+    for (int kk = 0; kk < nk; ++kk) {
+      const int pos = k0 + kk;
+      const float v = bf2f(kv_row(cache, pages.page_of(pos), 1, hk, pos % kPage)[d]);
+      o0 = fmaf(sc[h0][kk], v, o0);
+      o1 = fmaf(sc[h0 + 4][kk], v, o1);
+    }
+    part_o[(pidx + (size_t)h0 * splits) * kD + d] = o0;
+    part_o[(pidx + (size_t)(h0 + 4) * splits) * kD + d] = o1;
+    if (t < kGroup) {
+      part_ml[(pidx + (size_t)t * splits) * 2 + 0] = red[t][0];
+      part_ml[(pidx + (size_t)t * splits) * 2 + 1] = red[t][1];
+    }
+  }
+}
+
+// Sink scaling of attention.py:235-245: lse (natural log) -> s =
+// bf16(sigmoid(lse - sink)), out = bf16(bf16(o) * s).
+__device__ __forceinline__ float sink_factor(float lse, uint16_t sink) {
+  const float z = lse - bf2f(sink);
+  return bf2f(f2bf((float)(1.0 / (1.0 + exp(-(double)z)))));
+}
+
+// Decode attention, phase 2: one wave per (sequence, query head) merges the
+// splits (max, rescaled sums in split order), then lse, the sink factor and
+// the bf16 output.  Lane = dim.  A sequence whose attended range is longer
+// than the splits cover (the caller's bound was too small) gets NaN outputs.
+__global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restrict__ part_o,
+                                                          const float* __restrict__ part_ml,
+                                                          int splits,
+                                                          const int* __restrict__ kv_len,
+                                                          int window,
+                                                          const uint16_t* __restrict__ sinks,
+                                                          uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int L = kv_len[b];
+  const int span = window > 0 ? min(L, window) : L;
+  if (span > splits * kDecChunk || span <= 0) {
+    out[((size_t)b * kHq + h) * kD + d] = 0x7FC0;
+    return;
+  }
+  const size_t base = ((size_t)b * kHq + h) * splits;
+  float m = -INFINITY;
+  for (int s = 0; s < splits; ++s) m = fmaxf(m, part_ml[(base + s) * 2]);
+  float l = 0.f, o = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    const float ms = part_ml[(base + s) * 2];
+    if (ms == -INFINITY) continue;
+    const float f = __expf(ms - m);
+    l = fmaf(part_ml[(base + s) * 2 + 1], f, l);
+    o = fmaf(part_o[(base + s) * kD + d], f, o);
+  }
+  const float lse = m + __logf(l);
+  const float ob = bf2f(f2bf(o / l));
+  out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
+}
+
+// ---------------------------------------------------------------------------
+// Prefill / extend attention on v_mfma_f32_16x16x32_bf16.
+//
+// Workgroup = (query tile of 64 rows of one sequence, kv head hk): 8 waves,
+// wave w = query head 8 hk + w, so the 8 heads of a GQA group share each
+// key/value block staged in LDS.  Keys in blocks of 32 (two pages).
+//
+// The products are arranged so that only two facts of the MFMA's lane layout
+// matter: operand row (A) / column (B) = lane % 16, and result element i of
+// lane l = row 4 (l / 16) + i, column l % 16.  Which k each of a lane's 8
+// operand slots carries is the same for A and B, so pairing slot j of A with
+// slot j of B always multiplies matching k.
+//  * S^T = K Q^T (A = 16 keys x 32 dims, B = 32 dims x 16 queries): lane l of
+//    key subblock kb holds S[query l % 16][key 16 kb + 4 (l / 16) + i].
+//  * O^T += V^T P^T (A = 16 dims x 32 keys, B = 32 keys x 16 queries, P as
+//    two bf16 pieces): P's
+//    operand slot j of lane l carries key kj(l, j) = 4 (l / 16) + j (j < 4) or
+//    16 + 4 (l / 16) + j - 4 (j >= 4) -- exactly the scores lane l holds --
+//    and V^T's slot j of lane l carries the same key, read from a transposed
+//    LDS tile.
+constexpr int kPfQ = 64;      // query rows per wave
+constexpr int kPfKeys = 32;   // keys per block
+constexpr int kKRow = kD + 8;         // K tile row (bf16), padded
+constexpr int kVRow = kPfKeys + 4;    // V^T tile row (bf16), padded
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(512) void prefill_kernel(
+    const uint16_t* __restrict__ q, const int* __restrict__ q_indptr,
+    const uint8_t* __restrict__ cache, const int* __restrict__ page_indptr,
+    const int* __restrict__ page_indices, int num_pages, const int* __restrict__ kv_len,
+    int window, float sm_scale, const uint16_t* __restrict__ sinks, int tiles_per_seq,
+    uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint16_t kt[kPfKeys * kKRow];
+  __shared__ __align__(16) uint16_t vt[kD * kVRow];
+  const int b = blockIdx.x / tiles_per_seq, tile = blockIdx.x % tiles_per_seq;
+  const int hk = blockIdx.y;
+  const int qb = q_indptr[b], qn = q_indptr[b + 1] - qb;
+  const int q0 = tile * kPfQ;
+  if (q0 >= qn) return;
+  const int L = kv_len[b];
+  const int P = L - qn;  // positions of the sequence's queries: P .. L - 1
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int head = hk * kGroup + wave;
+  const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
+                       num_pages};
+
+  // this wave's Q operands: [query subtile][k step] (rows past the sequence
+  // repeat its last query; their results are not stored)
+  bf16x8 qa[4][2];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int row = qb + min(q0 + qt * 16 + r, qn - 1);
+    const u32x4* src = (const u32x4*)(q + ((size_t)row * kHq + head) * kD);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) qa[qt][ks] = moe::as_bf16x8(src[ks * 4 + g]);
+  }
+  const float c2 = sm_scale * 1.4426950408889634f;  // scores in log2 units
+  f32x4 o[4][4];
+  float m[4], l[4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int qlast = min(q0 + kPfQ, qn) - 1;
+  const int kmax = P + qlast;                                  // last key any row sees
+  const int kmin = window > 0 ? max(0, P + q0 - window + 1) : 0;  // first key any row sees
+  for (int kb0 = kmin / kPfKeys * kPfKeys; kb0 <= kmax; kb0 += kPfKeys) {
+    // stage K [32][64] and V^T [64][32] of keys kb0 .. kb0 + 31 (keys past
+    // kv_len read the block's first key: finite, masked below)
+    {
+      const int t = threadIdx.x;
+      const int key = (t & 255) >> 3, part = t & 7;
+      const int pos = kb0 + key < L ? kb0 + key : kb0;
+      const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), t >> 8, hk, pos % kPage) +
+                                      part * 8);
+      if (t < 256) {
+        *(u32x4*)(kt + key * kKRow + part * 8) = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          vt[(part * 8 + 2 * j) * kVRow + key] = (uint16_t)(v[j] & 0xFFFF);
+          vt[(part * 8 + 2 * j + 1) * kVRow + key] = (uint16_t)(v[j] >> 16);
+        }
+      }
+    }
+    __syncthreads();
+    bf16x8 ka[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        ka[kb][ks] = moe::as_bf16x8(*(const u32x4*)(kt + (kb * 16 + r) * kKRow + ks * 32 + g * 8));
+    bf16x8 va[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vr = vt + (dt * 16 + r) * kVRow;
+      const uint2 lo = *(const uint2*)(vr + 4 * g);
+      const uint2 hi = *(const uint2*)(vr + 16 + 4 * g);
+      va[dt] = moe::as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+    }
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      f32x4 st[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        st[kb] = mfma_bf16(ka[kb][0], qa[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        st[kb] = mfma_bf16(ka[kb][1], qa[qt][1], st[kb]);
+      }
+      // mask: key kb0 + 16 kb + 4 g + i for the query at position qpos
+      const int qpos = P + q0 + qt * 16 + r;
+      float sv[8];
+      float bm = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb0 + kb * 16 + 4 * g + i;
+          const bool ok = key <= qpos && key < L && (window <= 0 || key >= qpos - window + 1);
+          sv[kb * 4 + i] = ok ? st[kb][i] * c2 : -INFINITY;
+          bm = fmaxf(bm, sv[kb * 4 + i]);
+        }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+      const float mn = fmaxf(m[qt], bm);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[qt] - mn);
+      m[qt] = mn;
+      // P enters the MFMA as two bf16 pieces, p = hi + lo to about 16 bits,
+      // so the products keep the fp32 probabilities' precision
+      bf16x8 ph, pl;
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = sv[j] == -INFINITY ? 0.0f : exp2f(sv[j] - mn);
+        ps += p;
+        ph[j] = (__bf16)p;
+        pl[j] = (__bf16)(p - (float)ph[j]);
+      }
+      l[qt] = l[qt] * alpha + ps;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[qt][dt][i] *= alpha;
+        o[qt][dt] = mfma_bf16(va[dt], ph, o[qt][dt]);
+        o[qt][dt] = mfma_bf16(va[dt], pl, o[qt][dt]);
+      }
+    }
+    __syncthreads();
+  }
+  // epilogue: row sums across the 4 lane groups, lse, sink factor, bf16
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    float lt = l[qt];
+    lt += __shfl_xor(lt, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    const int qi = q0 + qt * 16 + r;
+    const float lse = (m[qt] + __log2f(lt)) * 0.6931471805599453f;
+    const float sf = sink_factor(lse, sinks[head]);
+    const float inv = 1.0f / lt;
+    if (qi < qn) {
+      uint16_t* dst = out + ((size_t)(qb + qi) * kHq + head) * kD;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        uint16_t v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = f2bf(bf2f(f2bf(o[qt][dt][i] * inv)) * sf);
+        *(uint2*)(dst + dt * 16 + 4 * g) =
+            make_uint2((uint32_t)v4[0] | ((uint32_t)v4[1] << 16), (uint32_t)v4[2] | ((uint32_t)v4[3] << 16));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out = bf16(x + bf16(y + bias)): the output linear's bias (nn.Linear's second
+// op) and the residual add of attention.py:256.  Four columns per thread.
+__global__ __launch_bounds__(256) void bias_residual_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ y,
+                                                            const uint16_t* __restrict__ bias,
+                                                            int64_t total, int H,
+                                                            uint16_t* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= total) return;
+  const int c = (int)(i % H);
+  uint16_t o4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float t = bf2f(f2bf(bf2f(y[i + j]) + bf2f(bias[c + j])));
+    o4[j] = f2bf(bf2f(x[i + j]) + t);
+  }
+  *(uint2*)(out + i) = make_uint2((uint32_t)o4[0] | ((uint32_t)o4[1] << 16),
+                                  (uint32_t)o4[2] | ((uint32_t)o4[3] << 16));
+}
+
+// Embedding gather (transformer.py:101-105): out[i] = table[ids[i]]; ids
+// outside [0, vocab) give a zero row.  One workgroup per token, 16 bytes per
+// thread.
+__global__ __launch_bounds__(256) void embedding_kernel(const int* __restrict__ ids,
+                                                        const uint16_t* __restrict__ table,
+                                                        int vocab, int H,
+                                                        uint16_t* __restrict__ out) {
+  const int tok = blockIdx.x;
+  const int id = ids[tok];
+  const bool ok = id >= 0 && id < vocab;
+  for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (ok) v = *(const u32x4*)(table + (size_t)id * H + c);
+    *(u32x4*)(out + (size_t)tok * H + c) = v;
+  }
+}
+
+}  // namespace attn
+
+// ---------------------------------------------------------------------------
+// Launchers (argument checks live in the C ABI, attn_capi.hip)
+extern "C" {
+
+int attn_launch_rms_norm(const void* x, int n, int H, const void* w, float eps, void* out,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(attn::rms_norm_kernel, dim3(n), dim3(256), 0, s, (const uint16_t*)x, H,
+                     (const uint16_t*)w, eps, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int attn_launch_qkv_rope_append(const void* qkv, const void* bias, int n, const int* positions,
+                                const int* slots, const float* inv_freq, float conc, void* cache,
+                                int num_pages, void* q_out, hipStream_t s) {
+  hipLaunchKernelGGL(attn::qkv_rope_append_kernel, dim3(attn::kQkvHeads / 8, n), dim3(256), 0, s,
+                     (const uint16_t*)qkv, (const uint16_t*)bias, positions, slots, inv_freq, conc,
+                     (uint8_t*)cache, num_pages, (uint16_t*)q_out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int attn_launch_decode(const void* q, int batch, const void* cache, const int* page_indptr,
+                       const int* page_indices, int num_pages, const int* kv_len, int window,
+                       float sm_scale,
+                       const void* sinks, int splits, float* part_o, float* part_ml, void* out,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(attn::decode_partial_kernel, dim3(splits, attn::kHkv, batch), dim3(256), 0, s,
+                     (const uint16_t*)q, (const uint8_t*)cache, page_indptr, page_indices,
+                     num_pages, kv_len, window, sm_scale, splits, part_o, part_ml);
+  if (hipGetLastError() != hipSuccess) return -6;
+  hipLaunchKernelGGL(attn::decode_merge_kernel, dim3(attn::kHq, batch), dim3(64), 0, s,
+                     (const float*)part_o, (const float*)part_ml, splits, kv_len, window,
+                     (const uint16_t*)sinks, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int attn_launch_prefill(const void* q, const int* q_indptr, int batch, int max_q_len,
+                        const void* cache, const int* page_indptr, const int* page_indices,
+                        int num_pages, const int* kv_len, int window, float sm_scale,
+                        const void* sinks, void* out, hipStream_t s) {
+  const int tiles = (max_q_len + attn::kPfQ - 1) / attn::kPfQ;
+  hipLaunchKernelGGL(attn::prefill_kernel, dim3(tiles * batch, attn::kHkv), dim3(512), 0, s,
+                     (const uint16_t*)q, q_indptr, (const uint8_t*)cache, page_indptr, page_indices,
+                     num_pages, kv_len, window, sm_scale, (const uint16_t*)sinks, tiles,
+                     (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int attn_launch_bias_residual(const void* x, const void* y, const void* bias, int64_t n, int H,
+                              void* out, hipStream_t s) {
+  const int64_t total = n * H;
+  const int64_t blocks = (total / 4 + 255) / 256;
+  hipLaunchKernelGGL(attn::bias_residual_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)bias, total, H,
+                     (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+int attn_launch_embedding(const int* ids, int n, const void* table, int vocab, int H, void* out,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(attn::embedding_kernel, dim3(n), dim3(256), 0, s, ids,
+                     (const uint16_t*)table, vocab, H, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+}  // extern "C"

@@ -43,6 +43,43 @@ def test_library_exports_every_header_symbol(native):
         assert name in native.EXPORTED, f"{name} has no ctypes signature in moe_native"
 
 
+ATTN_HEADER = os.path.join(REPO, "include", "attn_gfx950.h")
+
+
+def test_library_exports_every_attention_symbol(native):
+    import attn_native
+    syms = sorted(set(re.findall(r"MOE_API\s+[\w\s\*]+?\b(attn_\w+)\s*\(",
+                                 open(ATTN_HEADER).read())))
+    assert {"attn_decode", "attn_prefill", "attn_qkv_rope_append", "attn_rms_norm"} <= set(syms)
+    for name in syms:
+        assert hasattr(native.lib(), name), name
+        assert name in attn_native.EXPORTED, f"{name} has no ctypes signature in attn_native"
+    with pytest.raises(AttributeError):
+        getattr(native.lib(), "attn_launch_decode")
+
+
+def test_attention_validation(native):
+    """Bad arguments are refused on the host (no launch, no GPU needed)."""
+    lib = native.lib()
+    import attn_native  # noqa: F401  (registers the signatures)
+    p = ctypes.c_void_p(16)
+    codes = header_codes()
+    assert lib.attn_rms_norm(None, 1, 2880, p, 1e-5, p, None) == codes["MOE_ERR_NULL"]
+    assert lib.attn_rms_norm(p, 1, 2881, p, 1e-5, p, None) == codes["MOE_ERR_SHAPE"]
+    assert lib.attn_rms_norm(ctypes.c_void_p(18), 1, 2880, p, 1e-5, p, None) == codes["MOE_ERR_ALIGN"]
+    assert lib.attn_decode(p, 1, p, 0, p, p, p, 128, 0, 0.125, p, p, p, 1 << 20, None) == \
+        codes["MOE_ERR_SHAPE"]                                       # no pages
+    need = lib.attn_decode_workspace_bytes(2, 300)
+    assert need >= 2 * 64 * 3 * 66 * 4
+    assert lib.attn_decode(p, 2, p, 8, p, p, p, 300, 0, 0.125, p, p, p, need - 1, None) == \
+        codes["MOE_ERR_WORKSPACE"]
+    assert lib.attn_prefill(p, p, 1, 10, p, 8, p, p, p, 0, 0.125, None, p, None) == \
+        codes["MOE_ERR_NULL"]
+    assert lib.attn_prefill(p, p, 1, 0, p, 8, p, p, p, 0, 0.125, p, p, None) == codes["MOE_OK"]
+    assert lib.attn_embedding(p, 3, p, 0, 2880, p, None) == codes["MOE_ERR_SHAPE"]
+    assert lib.attn_bias_residual(p, p, p, 2, 2882, p, None) == codes["MOE_ERR_SHAPE"]
+
+
 def test_internal_launchers_are_hidden(native):
     with pytest.raises(AttributeError):
         getattr(native.lib(), "moe_launch_mx_gemv")

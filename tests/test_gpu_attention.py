@@ -1,0 +1,220 @@
+"""GPU parity of the attention-block kernels (include/attn_gfx950.h) against
+the oracle (oracle/attn_oracle.py), through the C ABI.
+
+Bit-exact: RMSNorm, the QKV bias + YaRN RoPE (q and the cached k) and the
+appended v, bias + residual, the embedding gather.  Within tolerance (fp32
+softmax, probabilities as two bf16 pieces on the MFMA, against the oracle's
+fp64): decode and prefill / extend attention with the sink scaling, on
+scattered page tables, ragged batches, sliding windows, and the whole
+AttentionBlock at gpt-oss-20b shape.  Attention outputs are held to a
+norm-relative max error of 1e-2 and a mean absolute error of 1e-3 relative to
+the mean magnitude (the block bar of the MoE path).
+"""
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import attn_oracle as AO  # noqa: E402
+from oracle import moe_oracle as O  # noqa: E402
+from gpu_util import bf16_dev, host_bf16, i32_dev, f32_dev  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+D, HQ, HKV, PAGE = 64, 64, 8, 16
+SCALE = 1.0 / math.sqrt(D)
+
+
+@pytest.fixture(scope="module")
+def A():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import attn_native
+    return attn_native
+
+
+def bf(x):
+    return O.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def close(got, ref, rel=1e-2, mae=1e-3):
+    m = O.compare_outputs(got, ref)
+    scale = np.abs(O.bf16_to_f32(ref)).mean()
+    assert m["max_rel"] <= rel and m["mae"] <= mae * max(scale, 1e-30), m
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+
+
+def test_rms_norm_bit_exact(A):
+    x = O.make_input(11, 7)
+    w = bf(np.random.default_rng(12).uniform(0.5, 1.5, 2880))
+    got = host_bf16(A.rms_norm(bf16_dev(x), bf16_dev(w), 1e-5))
+    np.testing.assert_array_equal(got, O.rms_norm(x, w, 1e-5))
+
+
+def test_bias_residual_and_embedding_bit_exact(A):
+    rng = np.random.default_rng(13)
+    x, y = O.make_input(14, 5), O.make_input(15, 5)
+    b = bf(rng.standard_normal(2880) * 0.1)
+    got = host_bf16(A.bias_residual(bf16_dev(x), bf16_dev(y), bf16_dev(b)))
+    want = O.f32_to_bf16(O.bf16_to_f32(x) + O.bf16_to_f32(AO.bias_add(y, b)))
+    np.testing.assert_array_equal(got, want)
+    table = bf(rng.standard_normal((100, 2880)))
+    ids = np.array([3, 99, 0, -1, 100, 3], dtype=np.int32)
+    got = host_bf16(A.embedding(i32_dev(ids), bf16_dev(table)))
+    want = np.where(((ids >= 0) & (ids < 100))[:, None], table[np.clip(ids, 0, 99)], 0)
+    np.testing.assert_array_equal(got, want.astype(np.uint16))
+
+
+def _inv_freq_dev():
+    from model.attention import yarn_rope_tables
+    from model.config import GPTOssConfig
+    inv, conc = yarn_rope_tables(GPTOssConfig())
+    np.testing.assert_array_equal(inv, AO.yarn_inv_freq())     # host table == oracle's
+    assert np.float32(conc) == AO.yarn_concentration()
+    return f32_dev(inv), conc
+
+
+def test_qkv_rope_append_bit_exact(A):
+    rng = np.random.default_rng(21)
+    n, pages = 9, 12
+    qkv = bf(rng.standard_normal((n, (HQ + 2 * HKV) * D)))
+    bias = bf(rng.standard_normal((HQ + 2 * HKV) * D) * 0.1)
+    pos = np.array([0, 1, 2, 15, 16, 4095, 4096, 70000, 131071], dtype=np.int32)
+    slots = rng.choice(pages * PAGE, n, replace=False).astype(np.int32)
+    slots[-1] = pages * PAGE + 5          # outside the pool: not written
+    cache = torch.zeros((pages, 2, HKV, PAGE, D), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((n, HQ, D), dtype=torch.bfloat16, device="cuda")
+    inv, conc = _inv_freq_dev()
+    A.qkv_rope_append(bf16_dev(qkv), bf16_dev(bias), i32_dev(pos), i32_dev(slots), inv, conc,
+                      cache, q)
+    ref = AO.bias_add(qkv, bias)
+    rq, rk, rv = AO.split_qkv(ref)
+    np.testing.assert_array_equal(host_bf16(q), AO.rope(rq, pos))
+    rk = AO.rope(rk, pos)
+    c = host_bf16(cache)
+    want = np.zeros_like(c)
+    for i in range(n - 1):
+        pg, sl = divmod(int(slots[i]), PAGE)
+        want[pg, 0, :, sl] = rk[i]
+        want[pg, 1, :, sl] = rv[i]
+    np.testing.assert_array_equal(c, want)
+
+
+class PagedSeqs:
+    """Random keys / values of a few sequences laid out in a scattered page pool."""
+
+    def __init__(self, seed, lengths, pages=None):
+        rng = np.random.default_rng(seed)
+        need = [-(-L // PAGE) for L in lengths]
+        pool = pages or sum(need) + 3
+        perm = rng.permutation(pool)
+        self.k = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
+        self.v = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
+        cache = bf(rng.standard_normal((pool, 2, HKV, PAGE, D)))   # unused slots: garbage
+        indptr, ids, off = [0], [], 0
+        for L, k, v, npg in zip(lengths, self.k, self.v, need):
+            mine = perm[off:off + npg]
+            off += npg
+            for p in range(L):
+                cache[mine[p // PAGE], 0, :, p % PAGE] = k[p]
+                cache[mine[p // PAGE], 1, :, p % PAGE] = v[p]
+            ids.extend(mine.tolist())
+            indptr.append(len(ids))
+        self.cache = bf16_dev(cache)
+        self.page_indptr = i32_dev(np.array(indptr))
+        self.page_indices = i32_dev(np.array(ids))
+        self.kv_len = i32_dev(np.array(lengths))
+        self.lengths = lengths
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_decode_attention(A, window):
+    lengths = [1, 130, 1000, 4100]
+    seqs = PagedSeqs(31, lengths)
+    rng = np.random.default_rng(32)
+    q = bf(rng.standard_normal((len(lengths), HQ, D)))
+    sinks = bf(rng.standard_normal(HQ))
+    span = max(min(L, window) if window else L for L in lengths)
+    ws = torch.empty(A.decode_workspace_bytes(len(lengths), span), dtype=torch.uint8, device="cuda")
+    out = torch.empty((len(lengths), HQ, D), dtype=torch.bfloat16, device="cuda")
+    A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, span,
+             window, SCALE, bf16_dev(sinks), out, ws)
+    got = host_bf16(out)
+    for b, L in enumerate(lengths):
+        o, lse = AO.attention(q[b:b + 1], seqs.k[b], seqs.v[b], np.array([L - 1]), window)
+        close(got[b:b + 1], AO.sink_scale(o, lse, sinks))
+
+
+def test_decode_span_too_small_is_nan(A):
+    seqs = PagedSeqs(33, [300])
+    q = bf(np.random.default_rng(34).standard_normal((1, HQ, D)))
+    ws = torch.empty(A.decode_workspace_bytes(1, 300), dtype=torch.uint8, device="cuda")
+    out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device="cuda")
+    A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, 200, 0,
+             SCALE, bf16_dev(bf(np.zeros(HQ))), out, ws)
+    assert np.isnan(O.bf16_to_f32(host_bf16(out))).all()
+
+
+@pytest.mark.parametrize("window", [0, 128])
+@pytest.mark.parametrize("qlens", [[300], [1, 64, 65, 200]])
+def test_prefill_attention(A, window, qlens):
+    # the last q_len tokens of each sequence are the queries: with a cached
+    # prefix (extend) for all but the first sequence
+    prefix = [0, 5, 100, 37][:len(qlens)]
+    lengths = [p + q for p, q in zip(prefix, qlens)]
+    seqs = PagedSeqs(41 + len(qlens), lengths)
+    rng = np.random.default_rng(42)
+    n = sum(qlens)
+    q = bf(rng.standard_normal((n, HQ, D)))
+    sinks = bf(rng.standard_normal(HQ))
+    q_indptr = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    out = torch.empty((n, HQ, D), dtype=torch.bfloat16, device="cuda")
+    A.prefill(bf16_dev(q), i32_dev(q_indptr), max(qlens), seqs.cache, seqs.page_indptr,
+              seqs.page_indices, seqs.kv_len, window, SCALE, bf16_dev(sinks), out)
+    got = host_bf16(out)
+    for b, (L, ql) in enumerate(zip(lengths, qlens)):
+        rows = slice(q_indptr[b], q_indptr[b + 1])
+        o, lse = AO.attention(q[rows], seqs.k[b], seqs.v[b], np.arange(L - ql, L), window)
+        close(got[rows], AO.sink_scale(o, lse, sinks))
+
+
+def _block(A, p, layer_idx):
+    from model.attention import AttentionBlock
+    from model.config import GPTOssConfig
+    blk = AttentionBlock(GPTOssConfig(), layer_idx=layer_idx, device="cuda")
+    with torch.no_grad():
+        blk.sinks.copy_(bf16_dev(p.sinks))
+        blk.norm.weight.copy_(bf16_dev(p.norm_w))
+        blk.qkv.weight.copy_(bf16_dev(p.qkv_w))
+        blk.qkv.bias.copy_(bf16_dev(p.qkv_b))
+        blk.out.weight.copy_(bf16_dev(p.out_w))
+        blk.out.bias.copy_(bf16_dev(p.out_b))
+    return blk
+
+
+@pytest.mark.parametrize("layer_idx", [0, 1])  # sliding window 128, full attention
+def test_attention_block_prefill_then_decode(A, layer_idx):
+    """AttentionBlock at 20B shape: a 150-token prefill then three decode
+    steps through the paged cache, each against the oracle's block."""
+    from model.kv_cache import PagedKVCache
+    p = AO.make_attn_params(51 + layer_idx)
+    blk = _block(A, p, layer_idx)
+    cache = PagedKVCache(num_layers=2, num_pages=64, max_batch=2, max_tokens=256)
+    cache.add_sequence(0)
+    cache.enable_sliding_window(0, 128)
+    window = 128 if layer_idx % 2 == 0 else 0
+    n0 = 150
+    x = O.make_input(52, n0 + 3)
+    kc = np.zeros((0, HKV, D), dtype=np.uint16)
+    vc = kc.copy()
+    steps = [(0, n0), (n0, n0 + 1), (n0 + 1, n0 + 2), (n0 + 2, n0 + 3)]
+    for a, b in steps:
+        cache.begin_forward([0], [b - a])
+        got = host_bf16(blk(bf16_dev(x[a:b]).view(1, b - a, 2880), cache).view(b - a, 2880))
+        cache.end_forward()
+        ref, k_new, v_new = AO.attn_block_forward(x[a:b], p, kc, vc, window)
+        kc, vc = np.concatenate([kc, k_new]), np.concatenate([vc, v_new])
+        m = O.compare_outputs(got, ref)
+        assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, (a, b, m)
+    assert cache.seq_len(0) == n0 + 3
