@@ -31,6 +31,8 @@ _SIGS = {
     "attn_prefill": ([_P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I32, _F, _P, _P, _P], _INT),
     "attn_bias_residual": ([_P, _P, _P, _I64, _I64, _P, _P], _INT),
     "attn_embedding": ([_P, _I64, _P, _I64, _I64, _P, _P], _INT),
+    "attn_sample_workspace_bytes": ([_I64], _SZ),
+    "attn_sample_top_p": ([_P, _I64, _I64, _F, _F, _F, _P, _P, _SZ, _P], _INT),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -155,4 +157,27 @@ def embedding(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None =
     _expect(out, "out", torch.bfloat16, (n, H))
     _check(_lib.attn_embedding(_ptr(ids), n, _ptr(table), vocab, H, _ptr(out), _stream()),
            "attn_embedding")
+    return out
+
+
+def sample_workspace(batch: int, device="cuda") -> torch.Tensor:
+    """A zeroed sampling workspace (each call leaves it zeroed)."""
+    return torch.zeros(int(_lib.attn_sample_workspace_bytes(batch)), dtype=torch.uint8,
+                       device=device)
+
+
+def sample_top_p(logits: torch.Tensor, temperature: float, top_p: float, uniform: float,
+                 workspace: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 logits [batch, vocab] -> token ids [batch] int32 (TVM's top-p sampler)."""
+    _expect(logits, "logits", torch.bfloat16)
+    if logits.dim() == 1:
+        logits = logits.view(1, -1)
+    batch, vocab = logits.shape
+    if out is None:
+        out = torch.empty(batch, dtype=torch.int32, device=logits.device)
+    _expect(out, "out", torch.int32, (batch,))
+    _expect(workspace, "workspace", torch.uint8)
+    _check(_lib.attn_sample_top_p(_ptr(logits), batch, vocab, temperature, top_p, uniform,
+                                  _ptr(out), _ptr(workspace), workspace.numel(), _stream()),
+           "attn_sample_top_p")
     return out

@@ -25,6 +25,9 @@ int attn_launch_bias_residual(const void* x, const void* y, const void* bias, in
                               void* out, hipStream_t s);
 int attn_launch_embedding(const int* ids, int n, const void* table, int vocab, int H, void* out,
                           hipStream_t s);
+size_t attn_sample_state_bytes();
+int attn_launch_sample(const void* logits, int batch, int V, float temperature, float top_p,
+                       float uniform, int* out, void* state, hipStream_t s);
 }
 
 namespace {
@@ -138,6 +141,23 @@ int attn_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int64_t
   if (!a4(ids) || !a16(table) || !a16(out)) return MOE_ERR_ALIGN;
   return status(attn_launch_embedding(ids, (int)n, table, (int)vocab, (int)H, out,
                                       as_stream(stream)));
+}
+
+size_t attn_sample_workspace_bytes(int64_t batch) {
+  return batch > 0 ? (size_t)batch * attn_sample_state_bytes() : 0;
+}
+
+int attn_sample_top_p(const uint16_t* logits, int64_t batch, int64_t vocab, float temperature,
+                      float top_p, float uniform, int32_t* out_ids, void* workspace,
+                      size_t workspace_bytes, moe_stream_t stream) {
+  if (batch < 0 || batch > 65535 || vocab <= 0 || vocab >= ((int64_t)1 << 30)) return MOE_ERR_SHAPE;
+  if (batch == 0) return MOE_OK;
+  if (!(temperature >= 0.0f) || !(top_p > 0.0f) || !(uniform >= 0.0f)) return MOE_ERR_UNSUPPORTED;
+  if (!logits || !out_ids || !workspace) return MOE_ERR_NULL;
+  if (!a16(logits) || !a4(out_ids) || !a16(workspace)) return MOE_ERR_ALIGN;
+  if (workspace_bytes < attn_sample_workspace_bytes(batch)) return MOE_ERR_WORKSPACE;
+  return status(attn_launch_sample(logits, (int)batch, (int)vocab, temperature, top_p, uniform,
+                                   out_ids, workspace, as_stream(stream)));
 }
 
 }  // extern "C"

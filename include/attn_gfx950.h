@@ -93,6 +93,25 @@ MOE_API int attn_bias_residual(const uint16_t* x, const uint16_t* y, const uint1
 MOE_API int attn_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int64_t vocab,
                            int64_t H, uint16_t* out, moe_stream_t stream);
 
+/* Workspace of attn_sample_top_p: 256 KB per sequence.  It must be zero
+ * before the first call (e.g. hipMemset once after allocation); every call
+ * leaves it zero again. */
+MOE_API size_t attn_sample_workspace_bytes(int64_t batch);
+
+/* Top-p sampling of one token per sequence from bf16 logits [batch, vocab]
+ * (the unembedding's bf16 output, model/transformer.py:95-100), replacing
+ * TVM's vm.builtin.sample_top_p_from_logits (engine.py:39-40,165-167):
+ * argmax if temperature < 1e-6; else e = exp((l - max) / temperature), the
+ * top-p mass is the cumulative mass in descending-logit order up to and
+ * including the element at which it reaches top_p, and the first element whose
+ * cumulative mass exceeds uniform x that mass is chosen (equal logits in index
+ * order; past the mass: the first maximum).  exp is rounded once to fp32 and
+ * the masses are summed exactly (fp64) where TVM adds fp32 values serially.
+ * out_ids [batch] int32. */
+MOE_API int attn_sample_top_p(const uint16_t* logits, int64_t batch, int64_t vocab,
+                              float temperature, float top_p, float uniform, int32_t* out_ids,
+                              void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,8 +31,9 @@ where they leave the order open):
              softmax and lse (natural log) in fp64; o rounded to bf16.
 * Sinks      s = bf16(sigmoid(lse - sink)), o' = bf16(o * s)
              (``attention.py:235-245``; sigmoid in fp64 rounded to fp32).
-* Sampling   TVM's algorithm on fp32 values; sort descending by logit, equal
-             logits in index order (the C++ std::sort leaves their order open).
+* Sampling   TVM's algorithm with exact (fp64) masses and exp rounded once to
+             fp32; sort descending by logit, equal logits in index order (the
+             C++ std::sort leaves their order open).
 """
 from __future__ import annotations
 
@@ -258,30 +259,88 @@ def make_attn_params(seed: int, hidden: int = 2880, hq: int = N_Q_HEADS, hkv: in
 def sample_top_p_from_logits(logits: np.ndarray, temperature: float, top_p: float,
                              uniform_sample: float) -> int:
     """TVM's SampleTopPFromLogits, restated: sort descending by logit; argmax
-    if temperature < 1e-6; else e = expf((l - max) / T) summed in sorted order,
-    probabilities e / sum accumulated in sorted order, top_p_sum = the mass of
-    the prefix up to and including the element at which the running sum
-    reaches top_p, and the first element whose cumulative probability over
-    top_p_sum exceeds uniform_sample is returned (the last one otherwise).
-    fp32 throughout, serial; equal logits in index order."""
+    if temperature < 1e-6; else e = exp((l - max) * (1 / T)), probabilities
+    e / sum(e) accumulated in sorted order, the top-p mass = the running sum up
+    to and including the element before which it was still below top_p, and
+    the first element whose cumulative probability over the top-p mass
+    exceeds uniform_sample is returned (the first maximum otherwise).
+
+    Canonical numerics: the exponent's argument in fp32 as written, exp
+    rounded once to fp32 (through fp64), and the sums exact (fp64).  TVM adds
+    the fp32 values serially, in an order not observable here, which over the
+    201088-entry vocabulary carries a relative error near 1e-3 -- enough to
+    move the chosen element by a rank or so; the exact sums are this build's
+    definition.  Equal logits are taken in index order."""
     l = np.asarray(logits, dtype=np.float32).reshape(-1)
     order = np.argsort(-l, kind="stable")
     ls = l[order]
     if temperature < 1e-6:
         return int(order[0])
     scale = np.float32(1.0 / temperature)
-    e = np.exp(((ls - ls[0]) * scale).astype(np.float32)).astype(np.float32)
-    # np.add.accumulate adds serially in the output dtype: the running fp32
-    # sums of the serial loops
-    total = np.cumsum(e, dtype=np.float32)[-1]
-    prob = (e / total).astype(np.float32)
-    cums = np.cumsum(prob, dtype=np.float32)
-    # top_p_sum adds the same probabilities in the same order as the running
-    # sum, up to and including the first one at which the sum before it is
-    # not below top_p
-    before = np.concatenate([[np.float32(0.0)], cums[:-1]]).astype(np.float32)
-    inside = np.nonzero(before < np.float32(top_p))[0]
-    top = cums[inside[-1]]
-    u = np.float32(uniform_sample)
-    hit = np.nonzero(u < (cums / top).astype(np.float32))[0]
+    arg = ((ls - ls[0]) * scale).astype(np.float32)
+    e = np.exp(arg.astype(np.float64)).astype(np.float32).astype(np.float64)
+    total = e.sum()
+    cums = np.cumsum(e) / total
+    before = np.concatenate([[0.0], cums[:-1]])
+    top = cums[np.nonzero(before < float(np.float32(top_p)))[0][-1]]
+    hit = np.nonzero(float(np.float32(uniform_sample)) < cums / top)[0]
     return int(order[hit[0]] if hit.size else order[0])
+
+
+# ---------------------------------------------------------------------------
+# The decode loop's model (model/transformer.py:13-133)
+# ---------------------------------------------------------------------------
+
+@dataclasses.dataclass
+class ModelParams:
+    """GPTOssForCausalLM parameters (bf16 bits / MXFP4 bytes)."""
+    embedding: np.ndarray     # [V, H]
+    layers: list              # [(AttnParams, moe_oracle.BlockParams)]
+    norm_w: np.ndarray        # [H]
+    unembedding: np.ndarray   # [V, H]
+
+
+def make_model_params(seed: int, layers: int, vocab: int, hidden: int = 2880,
+                      experts: int = 32, inter: int = 2880) -> ModelParams:
+    """Per-layer seeds seed + 100 i (attention) and seed + 100 i + 1 (MoE);
+    embedding and unembedding N(0, 1) and N(0, 0.02) from seed - 1."""
+    from oracle.moe_oracle import make_params
+    rng = np.random.Generator(np.random.PCG64(seed - 1))
+    emb = _bf16_normal(rng, (vocab, hidden), 1.0)
+    unemb = _bf16_normal(rng, (vocab, hidden), 0.02)
+    lay = [(make_attn_params(seed + 100 * i, hidden=hidden),
+            make_params(seed + 100 * i + 1, num_experts=experts, hidden=hidden, inter=inter))
+           for i in range(layers)]
+    return ModelParams(emb, lay, f32_to_bf16(np.ones(hidden, dtype=np.float32)), unemb)
+
+
+class OracleModel:
+    """Teacher-forced forward of one sequence: ``forward(ids)`` appends the
+    tokens to this object's per-layer caches and returns the fp32 logits
+    (bf16 values) of every appended token.  Even layers use the sliding
+    window (model/attention.py:87; the engine enables it for each sequence,
+    engine.py:116-125)."""
+
+    def __init__(self, p: ModelParams, window: int = SLIDING_WINDOW, k: int = 4,
+                 eps: float = 1e-5):
+        self.p, self.window, self.k, self.eps = p, window, k, eps
+        empty = np.zeros((0, N_KV_HEADS, HEAD_DIM), dtype=np.uint16)
+        self.kc = [empty.copy() for _ in p.layers]
+        self.vc = [empty.copy() for _ in p.layers]
+
+    def forward(self, ids) -> np.ndarray:
+        from oracle.moe_oracle import block_forward
+        x = self.p.embedding[np.asarray(ids, dtype=np.int64)]
+        for i, (ap, mp) in enumerate(self.p.layers):
+            w = self.window if i % 2 == 0 else 0
+            x, k, v = attn_block_forward(x, ap, self.kc[i], self.vc[i], w, self.eps)
+            self.kc[i] = np.concatenate([self.kc[i], k])
+            self.vc[i] = np.concatenate([self.vc[i], v])
+            x = block_forward(x, mp, self.k, self.eps).out
+        h = rms_norm(x, self.p.norm_w, self.eps)
+        self.hidden = h  # final hidden state (bf16 bits) of the appended tokens
+        return self.logits(h)
+
+    def logits(self, h_bf16: np.ndarray) -> np.ndarray:
+        """fp32 logits (bf16 values) of final hidden states (model/transformer.py:95-100)."""
+        return bf16_to_f32(linear(h_bf16, self.p.unembedding, None))

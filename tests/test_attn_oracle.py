@@ -138,27 +138,24 @@ def test_sink_equals_extra_softmax_logit():
 
 
 def _serial_sampler(logits, temperature, top_p, u):
-    """Literal serial loop of the TVM sampler on np.float32 scalars."""
+    """Literal loop of the sampler in Python floats (fp64), the argument of
+    exp in fp32 as written and exp rounded to fp32."""
     idx = sorted(range(len(logits)), key=lambda i: (-float(logits[i]), i))
     if temperature < 1e-6:
         return idx[0]
     mx = np.float32(logits[idx[0]])
     scale = np.float32(1.0 / temperature)
-    ex = [np.float32(np.exp(np.float32((np.float32(logits[i]) - mx) * scale))) for i in idx]
-    total = np.float32(0)
+    ex = [float(np.float32(math.exp(float(np.float32((np.float32(logits[i]) - mx) * scale)))))
+          for i in idx]
+    total = math.fsum(ex)
+    cum, top, cums = 0.0, 0.0, []
     for v in ex:
-        total = np.float32(total + v)
-    cum = np.float32(0)
-    top = np.float32(0)
-    cums = []
-    for v in ex:
-        p = np.float32(v / total)
-        if cum < np.float32(top_p):
-            top = np.float32(top + p)
-        cum = np.float32(cum + p)
+        if cum < float(np.float32(top_p)):
+            top = cum + v / total
+        cum += v / total
         cums.append(cum)
     for i, c in zip(idx, cums):
-        if np.float32(u) < np.float32(c / top):
+        if float(np.float32(u)) < c / top:
             return i
     return idx[0]
 
