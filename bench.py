@@ -22,7 +22,9 @@ Besides the JSON contract fields the line carries
                 fewer steps: configs 0 (decode 1), 2 (prefill 4096, Zipf
                 routing), 3a/3b (120B decode 256 / prefill 2048) and 4 (24
                 chained layers, a mixed decode + prefill step captured in one
-                HIP graph and replayed);
+                HIP graph and replayed); the attention kernels (decode over
+                64 x 4096 cached tokens, prefill of 4096) and the whole
+                gpt-oss-20b decode loop (tokens per second);
   cpu_baseline  the serial C restatement of the reference block (the CPU
                 oracle) timed on this host's cores on a bounded sample of the
                 same tokens and weights, one thread (the reference's llvm
@@ -311,6 +313,147 @@ def run_mixed(steps: int, warmup: int, dev, layers: int = 24, n_dec: int = 32,
     return res
 
 
+def kernel_us(fn, steps: int, warmup: int = 3) -> float:
+    """Average microseconds per call from HIP events on the launch stream; a
+    spin kernel queued first lets the host run ahead of the GPU."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.4e9 * 30e-6 * steps))
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps
+
+
+def run_attention(steps: int, dev) -> dict:
+    """The attention kernels at gpt-oss shape (64 query heads, 8 KV heads,
+    head_dim 64, pages of 16): decode attention over 64 sequences of 4096
+    cached tokens (scattered pages; full layer and 128-token sliding layer),
+    HBM-bound on the K/V bytes read; prefill attention of one 4096-token
+    sequence, MFMA-bound on its causal (windowed) score and value products."""
+    import math
+
+    import torch
+
+    import attn_native as A
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    B, L = 64, 4096
+    pages = B * L // 16
+    log(f"workload attention: decode {B} x {L} cached tokens, prefill {L}")
+    cache = torch.randn((pages, 2, 8, 16, 64), generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(pages, generator=g, device=dev).to(torch.int32)
+    indptr = (torch.arange(B + 1, device=dev, dtype=torch.int32) * (L // 16)).contiguous()
+    kv_len = torch.full((B,), L, dtype=torch.int32, device=dev)
+    q = torch.randn((B, 64, 64), generator=g, device=dev).to(torch.bfloat16)
+    sinks = torch.randn(64, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(64)
+    res = {}
+    for window in (0, 128):
+        span = L if window == 0 else window
+        ws = torch.empty(A.decode_workspace_bytes(B, span), dtype=torch.uint8, device=dev)
+        us = kernel_us(lambda i: A.decode(q, cache, indptr, perm, kv_len, span, window, scale,
+                                          sinks, out, ws), steps)
+        kv_bytes = B * span * 8 * 64 * 2 * 2
+        gbs = kv_bytes / us / 1e3
+        res[f"decode_b{B}_ctx{L}_window{window}"] = {
+            "us": round(us, 2), "kv_bytes": kv_bytes, "achieved_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "attn decode_partial + decode_merge (split over 128-key chunks)"}
+    del cache, perm
+    n = L
+    cache = torch.randn((n // 16, 2, 8, 16, 64), generator=g, device=dev).to(torch.bfloat16)
+    pages1 = torch.arange(n // 16, dtype=torch.int32, device=dev)
+    ind1 = torch.tensor([0, n // 16], dtype=torch.int32, device=dev)
+    qi = torch.tensor([0, n], dtype=torch.int32, device=dev)
+    kl = torch.tensor([n], dtype=torch.int32, device=dev)
+    qp = torch.randn((n, 64, 64), generator=g, device=dev).to(torch.bfloat16)
+    op = torch.empty_like(qp)
+    for window in (0, 128):
+        us = kernel_us(lambda i: A.prefill(qp, qi, n, cache, ind1, pages1, kl, window, scale,
+                                           sinks, op), max(5, steps // 10))
+        pairs = sum(min(i + 1, window) if window else i + 1 for i in range(n))
+        flops = pairs * 64 * 2 * 64 * 2          # q.k and p.v per (query, key, head)
+        tf = flops / us / 1e6
+        res[f"prefill_{n}_window{window}"] = {
+            "us": round(us, 2), "algorithmic_flops": flops, "tflops": round(tf, 2),
+            "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            "kernel": "attn prefill_kernel (bf16 MFMA 16x16x32, probabilities as two bf16 pieces)"}
+    for k, v in res.items():
+        log(f"attention {k}: {v['us']} us")
+    return res
+
+
+def _random_model(model, seed: int):
+    """Random weights of the reference's distributions into a GPTOssForCausalLM:
+    MXFP4 bytes uniform, E8M0 scales in 118..122, biases N(0, 0.01), dense
+    weights N(0, 0.02), embedding and sinks N(0, 1), norm weights 1."""
+    import torch
+    g = torch.Generator(device=next(model.parameters()).device)
+    g.manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dtype == torch.uint8:
+                lo, hi = (118, 123) if name.endswith("scales") else (0, 256)
+                p.copy_(torch.randint(lo, hi, p.shape, generator=g, device=p.device,
+                                      dtype=torch.int32).to(torch.uint8))
+            elif name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                std = (1.0 if ("embedding.weight" in name and "unembedding" not in name)
+                       or name.endswith("sinks") else 0.01 if "bias" in name else 0.02)
+                p.copy_((torch.randn(p.shape, generator=g, device=p.device) * std).to(p.dtype))
+
+
+def run_decode_loop(dev, prompt_len: int = 128, steps: int = 32) -> dict:
+    """The decode loop of the whole gpt-oss-20b model (24 layers, vocab
+    201088, random weights): a prompt prefill, then `steps` decode steps, each
+    the next-token forward and the GPU top-p sample, the sampled token fed
+    back on the device (eager, one host table update per step)."""
+    import torch
+
+    from engine import Engine
+    from model.config import gpt_oss_20b
+    cfg = gpt_oss_20b()
+    cfg.context_window_size = 4096
+    cfg.prefill_chunk_size = 4096
+    log(f"workload decode_loop20b: {cfg.num_hidden_layers} layers, prompt {prompt_len}, {steps} steps")
+    eng = Engine(config=cfg, max_total_seq_len=prompt_len + steps + 64)
+    _random_model(eng.model, 11)
+    g = torch.Generator()
+    g.manual_seed(12)
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=g, dtype=torch.int32)
+    seq = eng.begin_sequence()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = eng.sample_device(eng.prefill(prompt, seq))
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    for _ in range(3):
+        tok = eng.sample_device(eng.decode(tok, seq))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = eng.sample_device(eng.decode(tok, seq))
+    torch.cuda.synchronize()
+    t_dec = (time.perf_counter() - t0) / steps
+    weight_bytes = sum(p.numel() * p.element_size() for p in eng.model.parameters())
+    res = {"workload": "gpt-oss-20b decode loop (24 layers, vocab 201088, random weights), batch 1",
+           "prompt_tokens": prompt_len, "decode_steps": steps,
+           "prefill_ms": round(t_pre * 1e3, 2), "prefill_tok_s": round(prompt_len / t_pre, 1),
+           "ms_per_token": round(t_dec * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
+           "model_bytes": weight_bytes, "last_token": int(tok.item())}
+    log(f"decode_loop20b: prefill {res['prefill_ms']} ms, decode {res['ms_per_token']} ms/token")
+    del eng
+    return res
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -381,7 +524,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="time only the primary workload")
-    ap.add_argument("--secondary", default="decode1,prefill4096,decode256_120b,prefill2048_120b,mixed24",
+    ap.add_argument("--secondary",
+                    default="decode1,prefill4096,decode256_120b,prefill2048_120b,mixed24,"
+                            "attention,decode_loop20b",
                     help="comma-separated secondary workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 512 MiB (the known-size kernel that "
@@ -438,6 +583,10 @@ def main() -> int:
         for name in [s for s in args.secondary.split(",") if s and s != args.config]:
             if name == MIXED[0]:
                 sec[name] = run_mixed(10, 2, dev)
+            elif name == "attention":
+                sec[name] = run_attention(50, dev)
+            elif name == "decode_loop20b":
+                sec[name] = run_decode_loop(dev)
             else:
                 st = 30 if CONFIGS[name][1] >= 2048 else 100
                 res, b, x = run_block_config(name, st, 5, args.weight_sets, dev)

@@ -127,17 +127,24 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
 // takes keys [lo + 128 s, lo + 128 (s + 1)) of the sequence's attended range
 // [lo, kv_len) for the 8 query heads of hk, and writes the partial softmax
 // state of each head: m (max score), l (sum of exp(score - m)) and
-// o[64] = sum exp(score - m) v.  Scores in fp32 (q.k * sm_scale).
+// o[64] = sum exp(score - m) v.  Scores in fp32 (q.k * sm_scale).  The
+// chunk's K and V rows are staged in LDS first (the chunk's page ids read
+// once, then 256 threads x 8 16-byte loads, all in flight), so the HBM
+// traffic is coalesced and no load waits behind another.
 constexpr int kDecChunk = 128;
+constexpr int kDecKRow = kD + 8;  // padded K row (bf16)
 
 __global__ __launch_bounds__(256) void decode_partial_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ cache,
     const int* __restrict__ page_indptr, const int* __restrict__ page_indices, int num_pages,
     const int* __restrict__ kv_len, int window, float sm_scale, int splits,
     float* __restrict__ part_o, float* __restrict__ part_ml) {
+  __shared__ __align__(16) uint16_t ks[kDecChunk * kDecKRow];
+  __shared__ __align__(16) uint16_t vs[kDecChunk * kD];
   __shared__ float qs[kGroup][kD];
   __shared__ float sc[kGroup][kDecChunk];
   __shared__ float red[kGroup][2];
+  __shared__ int pid[kDecChunk / kPage + 1];
   const int s = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x;
   const int L = kv_len[b];
@@ -152,29 +159,52 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     }
     return;
   }
+  const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
+                       num_pages};
+  // the chunk spans at most 9 pages (it need not start on a page boundary)
+  const int pg0 = k0 / kPage;
+  if (t <= kDecChunk / kPage) pid[t] = pages.page_of(min((pg0 + t) * kPage, L - 1));
   for (int i = t; i < kGroup * kD; i += 256)
     qs[i / kD][i % kD] = bf2f(q[((size_t)b * kHq + hk * kGroup) * kD + i]);
   __syncthreads();
-  const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
-                       num_pages};
+  {
+    // 16-byte unit u: K units 0..1023 (key u / 8, part u % 8), V units 1024..2047;
+    // keys past the chunk repeat its last key (finite, not used)
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int u = t + 256 * j;
+      const int key = min((u & 1023) >> 3, nk - 1), part = u & 7;
+      const int pos = k0 + key;
+      v[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], u >> 10, hk, pos % kPage) +
+                             part * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int u = t + 256 * j;
+      const int key = (u & 1023) >> 3, part = u & 7;
+      if (u < 1024)
+        *(u32x4*)(ks + key * kDecKRow + part * 8) = v[j];
+      else
+        *(u32x4*)(vs + key * kD + part * 8) = v[j];
+    }
+  }
+  __syncthreads();
   {
     // scores: thread -> key t % 128, heads 4 (t / 128) .. + 3
     const int kk = t & (kDecChunk - 1);
     const int h0 = (t >> 7) * 4;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (kk < nk) {
-      const int pos = k0 + kk;
-      const u32x4* kr = (const u32x4*)kv_row(cache, pages.page_of(pos), 0, hk, pos % kPage);
+    const u32x4* kr = (const u32x4*)(ks + kk * kDecKRow);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const u32x4 v = kr[c];
+    for (int c = 0; c < 8; ++c) {
+      const u32x4 v = kr[c];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e0 = __uint_as_float(v[j] << 16), e1 = __uint_as_float(v[j] & 0xFFFF0000u);
+      for (int j = 0; j < 4; ++j) {
+        const float e0 = __uint_as_float(v[j] << 16), e1 = __uint_as_float(v[j] & 0xFFFF0000u);
 #pragma unroll
-          for (int h = 0; h < 4; ++h)
-            acc[h] = fmaf(e1, qs[h0 + h][c * 8 + 2 * j + 1], fmaf(e0, qs[h0 + h][c * 8 + 2 * j], acc[h]));
-        }
+        for (int h = 0; h < 4; ++h)
+          acc[h] = fmaf(e1, qs[h0 + h][c * 8 + 2 * j + 1], fmaf(e0, qs[h0 + h][c * 8 + 2 * j], acc[h]));
       }
     }
 #pragma unroll
@@ -207,9 +237,9 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     // o[h][d]: thread -> dim t % 64, heads t / 64 and t / 64 + 4
     const int d = t & 63, h0 = t >> 6;
     float o0 = 0.f, o1 = 0.f;
+#pragma unroll 8
     for (int kk = 0; kk < nk; ++kk) {
-      const int pos = k0 + kk;
-      const float v = bf2f(kv_row(cache, pages.page_of(pos), 1, hk, pos % kPage)[d]);
+      const float v = bf2f(vs[kk * kD + d]);
       o0 = fmaf(sc[h0][kk], v, o0);
       o1 = fmaf(sc[h0 + 4][kk], v, o1);
     }
@@ -268,7 +298,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
 //
 // Workgroup = (query tile of 64 rows of one sequence, kv head hk): 8 waves,
 // wave w = query head 8 hk + w, so the 8 heads of a GQA group share each
-// key/value block staged in LDS.  Keys in blocks of 32 (two pages).
+// key/value block staged in LDS.  Keys in blocks of 64 (four pages), double
+// buffered: the next block's global loads are in flight while the current
+// block's MFMAs run, one barrier per block.
 //
 // The products are arranged so that only two facts of the MFMA's lane layout
 // matter: operand row (A) / column (B) = lane % 16, and result element i of
@@ -276,17 +308,16 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
 // operand slots carries is the same for A and B, so pairing slot j of A with
 // slot j of B always multiplies matching k.
 //  * S^T = K Q^T (A = 16 keys x 32 dims, B = 32 dims x 16 queries): lane l of
-//    key subblock kb holds S[query l % 16][key 16 kb + 4 (l / 16) + i].
-//  * O^T += V^T P^T (A = 16 dims x 32 keys, B = 32 keys x 16 queries, P as
-//    two bf16 pieces): P's
-//    operand slot j of lane l carries key kj(l, j) = 4 (l / 16) + j (j < 4) or
-//    16 + 4 (l / 16) + j - 4 (j >= 4) -- exactly the scores lane l holds --
-//    and V^T's slot j of lane l carries the same key, read from a transposed
-//    LDS tile.
-constexpr int kPfQ = 64;      // query rows per wave
-constexpr int kPfKeys = 32;   // keys per block
+//    key subblock kk holds S[query l % 16][key 16 kk + 4 (l / 16) + i].
+//  * O^T += V^T P^T per 32 keys (A = 16 dims x 32 keys, B = 32 keys x 16
+//    queries, P as two bf16 pieces): P's operand slot j of lane l carries key
+//    4 (l / 16) + j (j < 4) or 16 + 4 (l / 16) + j - 4 (j >= 4) -- exactly the
+//    scores lane l holds -- and V^T's slot j of lane l carries the same key,
+//    read from a transposed LDS tile.
+constexpr int kPfQ = 64;              // query rows per wave
+constexpr int kPfKeys = 64;           // keys per block
 constexpr int kKRow = kD + 8;         // K tile row (bf16), padded
-constexpr int kVRow = kPfKeys + 4;    // V^T tile row (bf16), padded
+constexpr int kVRow = kPfKeys + 8;    // V^T tile row (bf16), padded
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -298,8 +329,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const int* __restrict__ page_indices, int num_pages, const int* __restrict__ kv_len,
     int window, float sm_scale, const uint16_t* __restrict__ sinks, int tiles_per_seq,
     uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint16_t kt[kPfKeys * kKRow];
-  __shared__ __align__(16) uint16_t vt[kD * kVRow];
+  __shared__ __align__(16) uint16_t kt[2][kPfKeys * kKRow];
+  __shared__ __align__(16) uint16_t vt[2][kD * kVRow];
   const int b = blockIdx.x / tiles_per_seq, tile = blockIdx.x % tiles_per_seq;
   const int hk = blockIdx.y;
   const int qb = q_indptr[b], qn = q_indptr[b + 1] - qb;
@@ -307,7 +338,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   if (q0 >= qn) return;
   const int L = kv_len[b];
   const int P = L - qn;  // positions of the sequence's queries: P .. L - 1
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = threadIdx.x;
+  const int wave = t >> 6, lane = t & 63;
   const int r = lane & 15, g = lane >> 4;
   const int head = hk * kGroup + wave;
   const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
@@ -334,89 +366,139 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     for (int dt = 0; dt < 4; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const int qlast = min(q0 + kPfQ, qn) - 1;
-  const int kmax = P + qlast;                                  // last key any row sees
+  const int kmax = P + qlast;                                     // last key any row sees
   const int kmin = window > 0 ? max(0, P + q0 - window + 1) : 0;  // first key any row sees
-  for (int kb0 = kmin / kPfKeys * kPfKeys; kb0 <= kmax; kb0 += kPfKeys) {
-    // stage K [32][64] and V^T [64][32] of keys kb0 .. kb0 + 31 (keys past
-    // kv_len read the block's first key: finite, masked below)
-    {
-      const int t = threadIdx.x;
-      const int key = (t & 255) >> 3, part = t & 7;
-      const int pos = kb0 + key < L ? kb0 + key : kb0;
-      const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), t >> 8, hk, pos % kPage) +
-                                      part * 8);
-      if (t < 256) {
-        *(u32x4*)(kt + key * kKRow + part * 8) = v;
-      } else {
+  const int kfirst = kmin / kPfKeys * kPfKeys;
+
+  // Staging: threads 0..255 hold K units (u = t, t + 256 of the block's 512:
+  // key u / 8, 16-byte part u % 8); threads 256..511 hold V parts of keys 2m
+  // and 2m + 1 (m = (t - 256) / 8), written transposed as key pairs.  Keys
+  // past kv_len read the block's first key (finite, masked).
+  u32x4 sr0, sr1;
+  auto load = [&](int kb0) {
+    if (t < 256) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          vt[(part * 8 + 2 * j) * kVRow + key] = (uint16_t)(v[j] & 0xFFFF);
-          vt[(part * 8 + 2 * j + 1) * kVRow + key] = (uint16_t)(v[j] >> 16);
-        }
+      for (int j = 0; j < 2; ++j) {
+        const int u = t + 256 * j, key = u >> 3, part = u & 7;
+        const int pos = kb0 + key < L ? kb0 + key : kb0;
+        const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), 0, hk, pos % kPage) +
+                                        part * 8);
+        if (j == 0) sr0 = v; else sr1 = v;
+      }
+    } else {
+      const int tv = t - 256, m2 = tv >> 3, part = tv & 7;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int key = 2 * m2 + j;
+        const int pos = kb0 + key < L ? kb0 + key : kb0;
+        const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), 1, hk, pos % kPage) +
+                                        part * 8);
+        if (j == 0) sr0 = v; else sr1 = v;
       }
     }
-    __syncthreads();
-    bf16x8 ka[2][2];
+  };
+  auto store = [&](int buf) {
+    if (t < 256) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int j = 0; j < 2; ++j) {
+        const int u = t + 256 * j, key = u >> 3, part = u & 7;
+        *(u32x4*)(kt[buf] + key * kKRow + part * 8) = j == 0 ? sr0 : sr1;
+      }
+    } else {
+      const int tv = t - 256, m2 = tv >> 3, part = tv & 7;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t a0 = (sr0[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        const uint32_t a1 = (sr1[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        *(uint32_t*)(vt[buf] + (part * 8 + e) * kVRow + 2 * m2) = a0 | (a1 << 16);
+      }
+    }
+  };
+
+  if (kfirst <= kmax) {
+    load(kfirst);
+    store(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int kb0 = kfirst; kb0 <= kmax; kb0 += kPfKeys) {
+    const bool more = kb0 + kPfKeys <= kmax;
+    if (more) load(kb0 + kPfKeys);  // in flight during this block's MFMAs
+    bf16x8 ka[4][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        ka[kb][ks] = moe::as_bf16x8(*(const u32x4*)(kt + (kb * 16 + r) * kKRow + ks * 32 + g * 8));
-    bf16x8 va[4];
+        ka[kk][ks] =
+            moe::as_bf16x8(*(const u32x4*)(kt[buf] + (kk * 16 + r) * kKRow + ks * 32 + g * 8));
+    bf16x8 va[2][4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vr = vt + (dt * 16 + r) * kVRow;
-      const uint2 lo = *(const uint2*)(vr + 4 * g);
-      const uint2 hi = *(const uint2*)(vr + 16 + 4 * g);
-      va[dt] = moe::as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-    }
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* vr = vt[buf] + (dt * 16 + r) * kVRow + s2 * 32;
+        const uint2 lo = *(const uint2*)(vr + 4 * g);
+        const uint2 hi = *(const uint2*)(vr + 16 + 4 * g);
+        va[s2][dt] = moe::as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+      }
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
-      f32x4 st[2];
+      const int qpos0 = P + q0 + qt * 16;  // this subtile's positions: qpos0 .. qpos0 + 15
+      // every key of the block masked for all 16 queries: nothing to add
+      if (qpos0 + 15 < kb0 || (window > 0 && qpos0 - window + 1 > kb0 + kPfKeys - 1)) continue;
+      f32x4 st[4];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        st[kb] = mfma_bf16(ka[kb][0], qa[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
-        st[kb] = mfma_bf16(ka[kb][1], qa[qt][1], st[kb]);
+      for (int kk = 0; kk < 4; ++kk) {
+        st[kk] = mfma_bf16(ka[kk][0], qa[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        st[kk] = mfma_bf16(ka[kk][1], qa[qt][1], st[kk]);
       }
-      // mask: key kb0 + 16 kb + 4 g + i for the query at position qpos
-      const int qpos = P + q0 + qt * 16 + r;
-      float sv[8];
+      // mask: key kb0 + 16 kk + 4 g + i for the query at position qpos
+      const int qpos = qpos0 + r;
+      float sv[16];
       float bm = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kb0 + kb * 16 + 4 * g + i;
+          const int key = kb0 + kk * 16 + 4 * g + i;
           const bool ok = key <= qpos && key < L && (window <= 0 || key >= qpos - window + 1);
-          sv[kb * 4 + i] = ok ? st[kb][i] * c2 : -INFINITY;
-          bm = fmaxf(bm, sv[kb * 4 + i]);
+          sv[kk * 4 + i] = ok ? st[kk][i] * c2 : -INFINITY;
+          bm = fmaxf(bm, sv[kk * 4 + i]);
         }
       bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
       bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
       const float mn = fmaxf(m[qt], bm);
       const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[qt] - mn);
       m[qt] = mn;
-      // P enters the MFMA as two bf16 pieces, p = hi + lo to about 16 bits,
-      // so the products keep the fp32 probabilities' precision
-      bf16x8 ph, pl;
       float ps = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = sv[j] == -INFINITY ? 0.0f : exp2f(sv[j] - mn);
-        ps += p;
-        ph[j] = (__bf16)p;
-        pl[j] = (__bf16)(p - (float)ph[j]);
-      }
-      l[qt] = l[qt] * alpha + ps;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[qt][dt][i] *= alpha;
-        o[qt][dt] = mfma_bf16(va[dt], ph, o[qt][dt]);
-        o[qt][dt] = mfma_bf16(va[dt], pl, o[qt][dt]);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        // P enters the MFMA as two bf16 pieces, p = hi + lo to about 16 bits,
+        // so the products keep the fp32 probabilities' precision
+        bf16x8 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float sj = sv[s2 * 8 + j];
+          const float p = sj == -INFINITY ? 0.0f : exp2f(sj - mn);
+          ps += p;
+          ph[j] = (__bf16)p;
+          pl[j] = (__bf16)(p - (float)ph[j]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          o[qt][dt] = mfma_bf16(va[s2][dt], ph, o[qt][dt]);
+          o[qt][dt] = mfma_bf16(va[s2][dt], pl, o[qt][dt]);
+        }
       }
+      l[qt] = l[qt] * alpha + ps;
     }
+    if (more) store(buf ^ 1);
     __syncthreads();
+    buf ^= 1;
   }
   // epilogue: row sums across the 4 lane groups, lse, sink factor, bf16
 #pragma unroll
