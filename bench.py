@@ -415,7 +415,8 @@ def run_decode_loop(dev, prompt_len: int = 128, steps: int = 32) -> dict:
     """The decode loop of the whole gpt-oss-20b model (24 layers, vocab
     201088, random weights): a prompt prefill, then `steps` decode steps, each
     the next-token forward and the GPU top-p sample, the sampled token fed
-    back on the device (eager, one host table update per step)."""
+    back on the device (eager, one host table update per step), then the same
+    step captured in one HIP graph and replayed."""
     import torch
 
     from engine import Engine
@@ -443,13 +444,26 @@ def run_decode_loop(dev, prompt_len: int = 128, steps: int = 32) -> dict:
         tok = eng.sample_device(eng.decode(tok, seq))
     torch.cuda.synchronize()
     t_dec = (time.perf_counter() - t0) / steps
+    # the same steps replayed from one captured HIP graph
+    eng.capture_decode(seq)
+    for _ in range(3):
+        eng.decode_sample(seq)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = eng.decode_sample(seq)
+    torch.cuda.synchronize()
+    t_graph = (time.perf_counter() - t0) / steps
     weight_bytes = sum(p.numel() * p.element_size() for p in eng.model.parameters())
     res = {"workload": "gpt-oss-20b decode loop (24 layers, vocab 201088, random weights), batch 1",
            "prompt_tokens": prompt_len, "decode_steps": steps,
            "prefill_ms": round(t_pre * 1e3, 2), "prefill_tok_s": round(prompt_len / t_pre, 1),
            "ms_per_token": round(t_dec * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
+           "graph_ms_per_token": round(t_graph * 1e3, 3),
+           "graph_decode_tok_s": round(1.0 / t_graph, 1),
            "model_bytes": weight_bytes, "last_token": int(tok.item())}
-    log(f"decode_loop20b: prefill {res['prefill_ms']} ms, decode {res['ms_per_token']} ms/token")
+    log(f"decode_loop20b: prefill {res['prefill_ms']} ms, decode {res['ms_per_token']} ms/token "
+        f"eager, {res['graph_ms_per_token']} ms/token from one HIP graph")
     del eng
     return res
 

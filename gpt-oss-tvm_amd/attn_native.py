@@ -31,6 +31,10 @@ _SIGS = {
     "attn_prefill": ([_P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I32, _F, _P, _P, _P], _INT),
     "attn_bias_residual": ([_P, _P, _P, _I64, _I64, _P, _P], _INT),
     "attn_embedding": ([_P, _I64, _P, _I64, _I64, _P, _P], _INT),
+    "attn_gemv": ([_P, _I64, _I64, _P, _I64, _P, _F, _P, _P], _INT),
+    "attn_gemv_bias_residual": ([_P, _I64, _I64, _P, _I64, _P, _P, _P, _P], _INT),
+    "attn_qkv_gemv_rope_append": ([_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _F, _P, _I64, _P,
+                                   _P], _INT),
     "attn_sample_workspace_bytes": ([_I64], _SZ),
     "attn_sample_top_p": ([_P, _I64, _I64, _F, _F, _F, _P, _P, _SZ, _P], _INT),
 }
@@ -181,3 +185,71 @@ def sample_top_p(logits: torch.Tensor, temperature: float, top_p: float, uniform
                                   _ptr(out), _ptr(workspace), workspace.numel(), _stream()),
            "attn_sample_top_p")
     return out
+
+
+GEMV_MAX_TOKENS = 8
+
+
+def gemv(x: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = None,
+         norm_w: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """bf16(t @ W^T) for at most 8 token rows (decode-sized nn.Linear matmul),
+    t = x or RMSNorm(x) with weight norm_w."""
+    _expect(x, "x", torch.bfloat16)
+    _expect(W, "W", torch.bfloat16)
+    N, K = W.shape
+    M = x.numel() // K
+    if norm_w is not None:
+        _expect(norm_w, "norm_w", torch.bfloat16, (K,))
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _expect(out, "out", torch.bfloat16, (M, N))
+    _check(_lib.attn_gemv(_ptr(x), M, K, _ptr(W), N, _ptr(norm_w), eps, _ptr(out), _stream()),
+           "attn_gemv")
+    return out
+
+
+def gemv_bias_residual(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor,
+                       residual: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(residual + bf16(bf16(x @ W^T) + bias)) for at most 8 token rows."""
+    _expect(x, "x", torch.bfloat16)
+    _expect(W, "W", torch.bfloat16)
+    N, K = W.shape
+    M = x.numel() // K
+    _expect(bias, "bias", torch.bfloat16, (N,))
+    _expect(residual, "residual", torch.bfloat16)
+    if residual.numel() != M * N:
+        raise ValueError(f"residual: expected {M * N} elements, got {residual.numel()}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _expect(out, "out", torch.bfloat16)
+    _check(_lib.attn_gemv_bias_residual(_ptr(x), M, K, _ptr(W), N, _ptr(bias), _ptr(residual),
+                                        _ptr(out), _stream()), "attn_gemv_bias_residual")
+    return out
+
+
+def qkv_gemv_rope_append(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor,
+                         positions: torch.Tensor, slots: torch.Tensor, inv_freq: torch.Tensor,
+                         concentration: float, kv_cache: torch.Tensor, q_out: torch.Tensor,
+                         norm_w: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """The decode QKV projection with bias, RoPE and the cache append fused
+    (and the block's pre-norm when norm_w is given)."""
+    _expect(x, "x", torch.bfloat16)
+    _expect(W, "W", torch.bfloat16)
+    N, K = W.shape
+    if N != QKV_DIM:
+        raise ValueError(f"W: expected {QKV_DIM} rows, got {N}")
+    M = x.numel() // K
+    _expect(bias, "bias", torch.bfloat16, (QKV_DIM,))
+    _expect(positions, "positions", torch.int32, (M,))
+    _expect(slots, "slots", torch.int32, (M,))
+    _expect(inv_freq, "inv_freq", torch.float32, (HEAD_DIM // 2,))
+    _expect(kv_cache, "kv_cache", torch.bfloat16)
+    _expect(q_out, "q_out", torch.bfloat16, (M, Q_HEADS, HEAD_DIM))
+    if norm_w is not None:
+        _expect(norm_w, "norm_w", torch.bfloat16, (K,))
+    _check(_lib.attn_qkv_gemv_rope_append(_ptr(x), M, K, _ptr(W), _ptr(norm_w), eps, _ptr(bias),
+                                          _ptr(positions),
+                                          _ptr(slots), _ptr(inv_freq), concentration,
+                                          _ptr(kv_cache), kv_cache.shape[0], _ptr(q_out),
+                                          _stream()), "attn_qkv_gemv_rope_append")
+    return q_out

@@ -26,6 +26,13 @@ int attn_launch_bias_residual(const void* x, const void* y, const void* bias, in
 int attn_launch_embedding(const int* ids, int n, const void* table, int vocab, int H, void* out,
                           hipStream_t s);
 size_t attn_sample_state_bytes();
+int attn_launch_gemv(const void* x, int M, int K, const void* W, int N, void* out,
+                     const void* norm_w, float eps, const void* bias, const void* res,
+                     hipStream_t s);
+int attn_launch_qkv_gemv(const void* x, int M, int K, const void* W, const void* norm_w,
+                         float eps, const void* bias, const int* positions, const int* slots,
+                         const float* inv_freq, float conc, void* cache, int num_pages,
+                         void* q_out, hipStream_t s);
 int attn_launch_sample(const void* logits, int batch, int V, float temperature, float top_p,
                        float uniform, int* out, void* state, hipStream_t s);
 }
@@ -158,6 +165,53 @@ int attn_sample_top_p(const uint16_t* logits, int64_t batch, int64_t vocab, floa
   if (workspace_bytes < attn_sample_workspace_bytes(batch)) return MOE_ERR_WORKSPACE;
   return status(attn_launch_sample(logits, (int)batch, (int)vocab, temperature, top_p, uniform,
                                    out_ids, workspace, as_stream(stream)));
+}
+
+namespace {
+int check_gemv(const void* x, int64_t M, int64_t K, const void* W, int64_t N, const void* out) {
+  if (M < 1 || M > 8 || K <= 0 || K % 8 || K > 4096 || N <= 0 || N >= ((int64_t)1 << 31))
+    return MOE_ERR_SHAPE;
+  if (!x || !W || !out) return MOE_ERR_NULL;
+  if (!a16(x) || !a16(W) || ((uintptr_t)out & 1u)) return MOE_ERR_ALIGN;
+  return MOE_OK;
+}
+}  // namespace
+
+int attn_gemv(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W, int64_t N,
+              const uint16_t* norm_w, float eps, uint16_t* out, moe_stream_t stream) {
+  int rc = check_gemv(x, M, K, W, N, out);
+  if (rc) return rc;
+  if (norm_w && ((uintptr_t)norm_w & 1u)) return MOE_ERR_ALIGN;
+  return status(attn_launch_gemv(x, (int)M, (int)K, W, (int)N, out, norm_w, eps, nullptr,
+                                 nullptr, as_stream(stream)));
+}
+
+int attn_gemv_bias_residual(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W, int64_t N,
+                            const uint16_t* bias, const uint16_t* residual, uint16_t* out,
+                            moe_stream_t stream) {
+  int rc = check_gemv(x, M, K, W, N, out);
+  if (rc) return rc;
+  if (!bias || !residual) return MOE_ERR_NULL;
+  if (((uintptr_t)bias & 1u) || ((uintptr_t)residual & 1u)) return MOE_ERR_ALIGN;
+  return status(attn_launch_gemv(x, (int)M, (int)K, W, (int)N, out, nullptr, 0.0f, bias,
+                                 residual, as_stream(stream)));
+}
+
+int attn_qkv_gemv_rope_append(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W,
+                              const uint16_t* norm_w, float eps, const uint16_t* qkv_bias,
+                              const int32_t* positions, const int32_t* slots,
+                              const float* inv_freq, float concentration, void* kv_cache,
+                              int64_t num_pages, uint16_t* q_out, moe_stream_t stream) {
+  int rc = check_gemv(x, M, K, W, kHeadDim * (kQHeads + 2 * kKvHeads), q_out);
+  if (rc) return rc;
+  if (num_pages <= 0 || num_pages > kMaxPages) return MOE_ERR_SHAPE;
+  if (!qkv_bias || !positions || !slots || !inv_freq || !kv_cache) return MOE_ERR_NULL;
+  if (!a16(kv_cache) || !a4(positions) || !a4(slots) || !a4(inv_freq) ||
+      ((uintptr_t)qkv_bias & 1u) || (norm_w && ((uintptr_t)norm_w & 1u)))
+    return MOE_ERR_ALIGN;
+  return status(attn_launch_qkv_gemv(x, (int)M, (int)K, W, norm_w, eps, qkv_bias, positions,
+                                     slots, inv_freq, concentration, kv_cache, (int)num_pages,
+                                     q_out, as_stream(stream)));
 }
 
 }  // extern "C"

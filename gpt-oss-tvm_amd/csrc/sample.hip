@@ -17,7 +17,8 @@
 //      top-p mass) are found at element granularity inside their bins, in
 //      fp64; the result is a value v* and a rank j* among the elements of that
 //      value (equal logits are taken in index order);
-//   3. one workgroup finds the j*-th element of value v* in index order.
+//   3. the j*-th element of value v* in index order: matches counted per
+//      index range by 64 workgroups, then the owning range searched by one.
 // The histogram is left zeroed after each call (it must be zero before the
 // first): nothing is cleared with a memset, so the calls can be captured.
 //
@@ -57,6 +58,7 @@ struct State {  // per sequence, after the histogram
   uint32_t pick_key;  // value of the chosen element
   uint32_t pick_rank; // 1-based rank among the elements of that value
   uint32_t pad;
+  uint32_t part_count[64];  // matches of the chosen value per index range
 };
 
 // 1. histogram and maximum.  Grid (ceil(V / 2048), batch), 256 threads x 8.
@@ -218,38 +220,83 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(State* __restrict__
   if (t == 0) s.max_key = 0u;
 }
 
-// 3. the pick_rank-th element of value pick_key, in index order.  One
-// 1024-thread workgroup per sequence over contiguous chunks.
-__global__ __launch_bounds__(kSelThreads) void find_kernel(const uint16_t* __restrict__ logits,
-                                                           int V, const State* __restrict__ st,
-                                                           int* __restrict__ out) {
-  __shared__ int wsum[kSelThreads / 64];
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+// 3. the pick_rank-th element of value pick_key, in index order, in two
+// launches: count_kernel counts the matches of each of kFindParts contiguous
+// ranges (16-byte loads), locate_kernel finds the range holding the wanted
+// rank and the element inside it (a block-wide prefix over that range).
+constexpr int kFindParts = 64;
+constexpr int kFindThreads = 256;
+
+__device__ __forceinline__ int part_begin(int V, int p) {
+  // ranges of whole 8-element groups (the last one takes the remainder)
+  const int groups = (V + 7) / 8;
+  return min(V, (int)(((int64_t)groups * p / kFindParts) * 8));
+}
+
+__global__ __launch_bounds__(kFindThreads) void count_kernel(const uint16_t* __restrict__ logits,
+                                                             int V, State* __restrict__ st) {
+  __shared__ int wsum[kFindThreads / 64];
+  const int b = blockIdx.y, p = blockIdx.x, t = threadIdx.x;
   const uint16_t* l = logits + (size_t)b * V;
   const uint32_t want = st[b].pick_key;
-  const int rank = (int)st[b].pick_rank;
-  const int chunk = (V + kSelThreads - 1) / kSelThreads;
-  const int i0 = t * chunk, i1 = min(V, i0 + chunk);
-  if (t == 0) out[b] = -1;  // replaced below (always, for a consistent histogram)
+  const int i0 = part_begin(V, p), i1 = part_begin(V, p + 1);
   int c = 0;
-  for (int i = i0; i < i1; ++i) c += key16(l[i]) == want;
-  int incl = c;
+  for (int i = i0 + t * 8; i < i1; i += kFindThreads * 8) {
+    if (i + 8 <= i1 && (V & 7) == 0) {
+      const u32x4 v = *(const u32x4*)(l + i);
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
+      for (int j = 0; j < 4; ++j)
+        c += (key16(v[j] & 0xFFFFu) == want) + (key16(v[j] >> 16) == want);
+    } else {
+      for (int k = i; k < min(i + 8, i1); ++k) c += key16(l[k]) == want;
+    }
   }
-  if (lane == 63) wsum[w] = incl;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off, 64);
+  if ((t & 63) == 0) wsum[t >> 6] = c;
   __syncthreads();
-  int before = incl - c;
-  for (int i = 0; i < w; ++i) before += wsum[i];
-  if (before < rank && before + c >= rank) {
-    int r = before;
-    for (int i = i0; i < i1; ++i)
-      if (key16(l[i]) == want && ++r == rank) {
-        out[b] = i;
-        break;
-      }
+  if (t == 0) st[b].part_count[p] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+}
+
+__global__ __launch_bounds__(kFindThreads) void locate_kernel(const uint16_t* __restrict__ logits,
+                                                              int V, const State* __restrict__ st,
+                                                              int* __restrict__ out) {
+  __shared__ int base_s, part_s;
+  __shared__ int wsum[kFindThreads / 64];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint16_t* l = logits + (size_t)b * V;
+  const State& s = st[b];
+  const uint32_t want = s.pick_key;
+  const int rank = (int)s.pick_rank;
+  if (t == 0) {
+    int acc = 0, p = 0;
+    for (; p < kFindParts - 1 && acc + (int)s.part_count[p] < rank; ++p) acc += s.part_count[p];
+    base_s = acc;
+    part_s = p;
+    out[b] = -1;  // replaced below
+  }
+  __syncthreads();
+  const int i0 = part_begin(V, part_s), i1 = part_begin(V, part_s + 1);
+  // chunks of kFindThreads elements in index order; a running count across them
+  int before_chunk = base_s;
+  for (int c0 = i0; c0 < i1; c0 += kFindThreads) {
+    const int i = c0 + t;
+    const int hit = i < i1 && key16(l[i]) == want;
+    int incl = hit;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    int pre = 0;
+    for (int k = 0; k < w; ++k) pre += wsum[k];
+    const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (hit && before_chunk + pre + incl == rank) out[b] = i;
+    before_chunk += total;
+    __syncthreads();
+    if (before_chunk >= rank) break;  // uniform: every thread has the same count
   }
 }
 
@@ -268,7 +315,10 @@ int attn_launch_sample(const void* logits, int batch, int V, float temperature, 
   hipLaunchKernelGGL(smp::select_kernel, dim3(batch), dim3(smp::kSelThreads), 0, s, st,
                      temperature, top_p, uniform);
   if (hipGetLastError() != hipSuccess) return -6;
-  hipLaunchKernelGGL(smp::find_kernel, dim3(batch), dim3(smp::kSelThreads), 0, s,
+  hipLaunchKernelGGL(smp::count_kernel, dim3(smp::kFindParts, batch), dim3(smp::kFindThreads), 0,
+                     s, (const uint16_t*)logits, V, st);
+  if (hipGetLastError() != hipSuccess) return -6;
+  hipLaunchKernelGGL(smp::locate_kernel, dim3(batch), dim3(smp::kFindThreads), 0, s,
                      (const uint16_t*)logits, V, (const smp::State*)st, out);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

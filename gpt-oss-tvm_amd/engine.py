@@ -93,6 +93,60 @@ class Engine:
     def extend(self, input_tokens, sequence_id: int = 0) -> torch.Tensor:
         return self._run(self.model.extend, input_tokens, sequence_id)
 
+    # -- the decode step in one HIP graph ---------------------------------------------
+    def _step_body(self) -> None:
+        embed = self.model.embed(self._token)
+        logits = self.model.decode(embed, self.paged_kv_cache)
+        self.graph_logits = logits
+        self.sample_device(logits)
+
+    @torch.no_grad()
+    def capture_decode(self, sequence_id: int) -> None:
+        """Capture one decode step of ``sequence_id`` -- embedding of the last
+        sampled token, every layer, final norm, unembedding, sampling into the
+        same token buffer -- in a HIP graph (``decode_sample`` replays it).
+
+        Nothing is allocated inside the step: the KV cache's forward tables
+        are fixed device buffers refreshed by ``begin_forward`` before each
+        replay, every MoE block's workspace is reserved for one token, and the
+        decode attention's split count is fixed at the pool's capacity
+        (``static_span``).  The warm-up and capture steps are rolled back."""
+        c = self.paged_kv_cache
+        c.static_span = c.num_pages * 16
+        c.reserve_decode(1, c.static_span)
+        for blk in self.model.model.block:
+            blk.mlp.reserve(1)
+        token = self._token.clone()  # the warm-up step samples over it
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            c.begin_forward([sequence_id], [1])
+            self._step_body()
+            c.end_forward()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        c.popn(sequence_id, 1)
+        self._token.copy_(token)
+        c.begin_forward([sequence_id], [1])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._step_body()
+        c.end_forward()
+        c.popn(sequence_id, 1)
+        self._graph, self._graph_seq = graph, sequence_id
+
+    def decode_sample(self, sequence_id: int) -> torch.Tensor:
+        """One captured decode step fed with the last sampled token
+        (``sample_device`` / ``sample`` wrote it): the next token, as the
+        1-element device tensor the following step reads; its logits are in
+        ``graph_logits``."""
+        if getattr(self, "_graph", None) is None or self._graph_seq != sequence_id:
+            raise RuntimeError(f"capture_decode({sequence_id}) first")
+        self.paged_kv_cache.begin_forward([sequence_id], [1])
+        self._graph.replay()
+        self.paged_kv_cache.end_forward()
+        return self._token
+
     def sample_device(self, logits: torch.Tensor) -> torch.Tensor:
         """The sampled token id as a 1-element int32 device tensor (no host sync).
 

@@ -7,10 +7,12 @@ the same parameter names and shapes (``sinks`` [64], ``norm.weight`` [H],
 KV append, attention over the paged cache, sink scaling, output projection,
 residual) and the alternating sliding window (even layers, attention.py:87).
 
-The dense projections are plain bf16 GEMMs (``torch.nn.functional.linear``
-without bias: hipBLASLt, fp32 accumulation, one bf16 rounding, as the
-reference's matmul); the biases are added by the HIP epilogues as separate
-bf16 ops (``nn.Linear``'s second op).  Everything else runs in the HIP
+The dense projections round once to bf16 after fp32 accumulation, as the
+reference's matmul, and add their biases as separate bf16 ops (``nn.Linear``'s
+second op): for up to 8 tokens (decode) in hand-written GEMV kernels with the
+bias, RoPE and cache append (QKV) or the bias and residual (output) fused; for
+prefill-sized inputs as library GEMMs (``torch.nn.functional.linear`` without
+bias, hipBLASLt) followed by the HIP epilogue kernels.  Everything else runs in the HIP
 kernels of libmoe_gfx950 (attn_native): there is no other path.
 """
 from __future__ import annotations
@@ -120,21 +122,31 @@ class AttentionBlock(torch.nn.Module):
         n = x2.shape[0]
         if n != tables.num_tokens:
             raise ValueError(f"{n} tokens in x, {tables.num_tokens} in the forward's tables")
-        t = A.rms_norm(x2, self.norm.weight, self.eps)
-        qkv = F.linear(t, self.qkv.weight)
         q = torch.empty((n, A.Q_HEADS, A.HEAD_DIM), dtype=x.dtype, device=x.device)
         layer = cache.layer(self.layer_idx)
-        A.qkv_rope_append(qkv, self.qkv.bias, tables.positions, tables.slots, self.inv_freq,
-                          self.concentration, layer, q)
+        small = n <= A.GEMV_MAX_TOKENS  # decode-sized: GEMV kernels with fused norm / epilogues
+        if small:
+            A.qkv_gemv_rope_append(x2, self.qkv.weight, self.qkv.bias, tables.positions,
+                                   tables.slots, self.inv_freq, self.concentration, layer, q,
+                                   norm_w=self.norm.weight, eps=self.eps)
+        else:
+            t = A.rms_norm(x2, self.norm.weight, self.eps)
+            qkv = F.linear(t, self.qkv.weight)
+            A.qkv_rope_append(qkv, self.qkv.bias, tables.positions, tables.slots, self.inv_freq,
+                              self.concentration, layer, q)
         o = torch.empty_like(q)
         window = self._window(tables)
         if tables.is_decode:
-            span = min(tables.max_kv_len, window) if window > 0 else tables.max_kv_len
+            span = cache.static_span or tables.max_kv_len
+            span = min(span, window) if window > 0 else span
             ws = cache.decode_workspace(tables.batch, span)
             A.decode(q, layer, tables.page_indptr, tables.page_indices, tables.kv_len, span,
                      window, self.sm_scale, self.sinks, o, ws)
         else:
             A.prefill(q, tables.q_indptr, tables.max_q_len, layer, tables.page_indptr,
                       tables.page_indices, tables.kv_len, window, self.sm_scale, self.sinks, o)
-        y = F.linear(o.view(n, A.Q_HEADS * A.HEAD_DIM), self.out.weight)
+        o2 = o.view(n, A.Q_HEADS * A.HEAD_DIM)
+        if small:
+            return A.gemv_bias_residual(o2, self.out.weight, self.out.bias, x2).view(x.shape)
+        y = F.linear(o2, self.out.weight)
         return A.bias_residual(x2, y, self.out.bias).view(x.shape)

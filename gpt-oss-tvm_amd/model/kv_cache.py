@@ -13,7 +13,9 @@ list, its length after the append, the positions and cache slots of the
 appended tokens -- and copies them into device buffers allocated once at
 construction, so the forward itself allocates nothing and can be captured in
 a HIP graph (the tables are inputs of the graph: refresh them with
-``begin_forward`` before each replay).
+``begin_forward`` before each replay; ``static_span`` fixes the decode
+attention's split count at the pool's capacity for a captured forward, whose
+empty splits return at once and merge to the same result).
 
 Sliding window: the reference's cache keeps only the window's pages for its
 "mha_sliding" layers; this cache keeps every token and the kernels attend to
@@ -79,6 +81,8 @@ class PagedKVCache:
                                    dtype=torch.int32, pin_memory=torch.cuda.is_available())
         self.tables: ForwardTables | None = None
         self._decode_ws: torch.Tensor | None = None
+        # decode attention's key bound for a captured forward (0: per forward)
+        self.static_span = 0
 
     def decode_workspace(self, batch: int, span: int) -> torch.Tensor:
         """The decode attention's split buffers for `batch` sequences attending

@@ -10,8 +10,9 @@ Parameter names follow the reference's modules, so a gpt-oss checkpoint
 loads through ``weights.TorchCheckpoint.load_into`` (embedding.weight,
 block.N.attn.*, block.N.mlp.*, norm.scale, unembedding.weight).
 
-Every operator is a HIP kernel of libmoe_gfx950 except the dense bf16
-projections (QKV, attention output, unembedding), which are library GEMMs.
+Every operator is a HIP kernel of libmoe_gfx950; the dense bf16 projections
+(QKV, attention output, unembedding) are HIP GEMVs for up to 8 tokens and
+library GEMMs for more.
 """
 from __future__ import annotations
 
@@ -57,9 +58,13 @@ class Transformer(torch.nn.Module):
             [TransformerBlock(config, i, device) for i in range(config.num_hidden_layers)])
         self.norm = _Weight((config.hidden_size,), device, torch.bfloat16, fill=1.0)
 
-    def forward(self, x: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
+    def layers(self, x: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
         for blk in self.block:
             x = blk(x, cache)
+        return x
+
+    def forward(self, x: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
+        x = self.layers(x, cache)
         H = x.shape[-1]
         return A.rms_norm(x.reshape(-1, H), self.norm.weight, self.eps).view(x.shape)
 
@@ -77,7 +82,10 @@ class GPTOssForCausalLM(torch.nn.Module):
         self.sw_pattern = config.sliding_window_pattern
 
     def _logits_bf16(self, h: torch.Tensor) -> torch.Tensor:
-        return F.linear(h.reshape(-1, self.hidden_size), self.unembedding.weight)
+        h2 = h.reshape(-1, self.hidden_size)
+        if h2.shape[0] <= A.GEMV_MAX_TOKENS:  # decode-sized: the GEMV kernel
+            return A.gemv(h2.contiguous(), self.unembedding.weight)
+        return F.linear(h2, self.unembedding.weight)
 
     def _get_logits(self, h: torch.Tensor) -> torch.Tensor:
         """bf16 logits of the unembedding, as fp32 (model/transformer.py:95-100)."""
@@ -94,9 +102,16 @@ class GPTOssForCausalLM(torch.nn.Module):
         return self._get_logits(h[:, -1:, :]).view(1, 1, -1)
 
     def decode(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
-        """Logits [1, b, vocab] of one new token per sequence (model/transformer.py:121-126)."""
-        h = self.model(input_embed, cache)
-        return self._get_logits(h).view(1, -1, self.config.vocab_size)
+        """Logits [1, b, vocab] of one new token per sequence (model/transformer.py:121-126).
+
+        Up to 8 sequences: the final norm runs inside the unembedding GEMV."""
+        if input_embed.numel() // self.hidden_size > A.GEMV_MAX_TOKENS:
+            h = self.model(input_embed, cache)
+            return self._get_logits(h).view(1, -1, self.config.vocab_size)
+        x = self.model.layers(input_embed, cache)
+        lg = A.gemv(x.reshape(-1, self.hidden_size), self.unembedding.weight,
+                    norm_w=self.model.norm.weight, eps=self.model.eps)
+        return lg.float().view(1, -1, self.config.vocab_size)
 
     def extend(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
         """Prefill of new tokens over a cached prefix (model/transformer.py:128-140)."""

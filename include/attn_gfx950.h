@@ -6,8 +6,9 @@
  * (model/attention.py:182-256): RMSNorm, a fused QKV nn.Linear, YaRN RoPE on
  * q and k, append_mha_kv, self_attention (prefill) / cross_attention (decode)
  * / both merged (extend), the sink scaling, the output nn.Linear and the
- * residual add.  The plain dense projections (QKV, output, unembedding) are
- * library GEMMs on the host side; these entry points are everything else.
+ * residual add.  The dense projections (QKV, output, unembedding) are
+ * library GEMMs on the host side for prefill-sized inputs and the GEMV entry
+ * points below (with their epilogues fused) for decode-sized ones.
  * The conventions of moe_gfx950.h hold: caller-owned device buffers, nothing
  * allocated, no host synchronisation, the stream last, MOE_OK or a negative
  * MOE_ERR_* code (no launch on error).
@@ -92,6 +93,33 @@ MOE_API int attn_bias_residual(const uint16_t* x, const uint16_t* y, const uint1
  * H % 8 == 0. */
 MOE_API int attn_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int64_t vocab,
                            int64_t H, uint16_t* out, moe_stream_t stream);
+
+/* Decode-sized dense projection (nn.Linear's matmul for M <= 8 tokens):
+ * out[m][n] = bf16(sum_k t[m][k] W[n][k]), fp32 accumulation, one bf16
+ * rounding, where t = x, or t = RMSNorm(x) with weight norm_w and eps when
+ * norm_w is not NULL (the same arithmetic as attn_rms_norm).  x [M, K], W [N,
+ * K], out [M, N] bf16; K % 8 == 0, K <= 4096.  Replaces the final norm and
+ * the unembedding nn.Linear at decode (model/transformer.py:63,95-100). */
+MOE_API int attn_gemv(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W, int64_t N,
+                      const uint16_t* norm_w, float eps, uint16_t* out, moe_stream_t stream);
+
+/* The attention output nn.Linear at decode with its bias and the residual
+ * (model/attention.py:254-256): out = bf16(residual + bf16(bf16(x W^T) +
+ * bias)); residual, out [M, N]. */
+MOE_API int attn_gemv_bias_residual(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W,
+                                    int64_t N, const uint16_t* bias, const uint16_t* residual,
+                                    uint16_t* out, moe_stream_t stream);
+
+/* The block's pre-norm (when norm_w is not NULL), the fused QKV nn.Linear at
+ * decode (model/attention.py:80,204) and attn_qkv_rope_append in one kernel:
+ * W [5120, K], then the bias, YaRN RoPE, q_out and the cache append exactly
+ * as attn_qkv_rope_append does. */
+MOE_API int attn_qkv_gemv_rope_append(const uint16_t* x, int64_t M, int64_t K, const uint16_t* W,
+                                      const uint16_t* norm_w, float eps,
+                                      const uint16_t* qkv_bias, const int32_t* positions,
+                                      const int32_t* slots, const float* inv_freq,
+                                      float concentration, void* kv_cache, int64_t num_pages,
+                                      uint16_t* q_out, moe_stream_t stream);
 
 /* Workspace of attn_sample_top_p: 256 KB per sequence.  It must be zero
  * before the first call (e.g. hipMemset once after allocation); every call

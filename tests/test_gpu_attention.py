@@ -218,3 +218,59 @@ def test_attention_block_prefill_then_decode(A, layer_idx):
         m = O.compare_outputs(got, ref)
         assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, (a, b, m)
     assert cache.seq_len(0) == n0 + 3
+
+
+def _ulp_close(got, ref, what, frac=0.01):
+    """Equal but for fp32 summation order: at most `frac` of the elements
+    differ, each by one bf16 ulp of its value, or -- for results near zero
+    after cancellation -- by at most 2^-16 of the largest magnitude (far above
+    fp32 accumulation error, far below one bf16 ulp of typical values)."""
+    g, r = O.bf16_to_f32(got).astype(np.float64), O.bf16_to_f32(ref).astype(np.float64)
+    ulp = np.spacing(np.abs(r).astype(np.float32)).astype(np.float64) * 2 ** 16
+    floor = np.abs(r).max() * 2.0 ** -16
+    diff = np.abs(g - r)
+    assert (diff > 0).mean() <= frac and np.all(diff <= np.maximum(ulp, floor)), \
+        (what, (diff > 0).mean(), (diff / np.maximum(ulp, floor)).max())
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_gemv_kernels(A, M):
+    """The decode-sized projections: unembedding-shaped GEMV, the output
+    projection with bias + residual, and the QKV projection with bias, RoPE
+    and the cache append, against the oracle's nn.Linear and RoPE."""
+    rng = np.random.default_rng(60 + M)
+    K, N = 2880, 4096 + 40          # N not a multiple of the row block
+    x = bf(rng.standard_normal((M, K)))
+    W = bf(rng.standard_normal((N, K)) * 0.02)
+    _ulp_close(host_bf16(A.gemv(bf16_dev(x), bf16_dev(W))), AO.linear(x, W, None), "gemv")
+    nw = bf(rng.uniform(0.5, 1.5, K))
+    xr = O.make_input(62, M)
+    got = host_bf16(A.gemv(bf16_dev(xr), bf16_dev(W), norm_w=bf16_dev(nw), eps=1e-5))
+    _ulp_close(got, AO.linear(O.rms_norm(xr, nw, 1e-5), W, None), "norm + gemv")
+    Ko, No = 4096, 2880
+    o = bf(rng.standard_normal((M, Ko)) * 0.3)
+    Wo = bf(rng.standard_normal((No, Ko)) * 0.02)
+    bo = bf(rng.standard_normal(No) * 0.01)
+    res = O.make_input(61, M)
+    got = host_bf16(A.gemv_bias_residual(bf16_dev(o), bf16_dev(Wo), bf16_dev(bo), bf16_dev(res)))
+    want = O.f32_to_bf16(O.bf16_to_f32(res) + O.bf16_to_f32(AO.linear(o, Wo, bo)))
+    _ulp_close(got, want, "out projection", frac=0.02)
+    Wq = bf(rng.standard_normal(((HQ + 2 * HKV) * D, K)) * 0.02)
+    bq = bf(rng.standard_normal((HQ + 2 * HKV) * D) * 0.01)
+    pos = np.arange(100, 100 + M, dtype=np.int32) * 37
+    pages = 4
+    slots = rng.choice(pages * PAGE, M, replace=False).astype(np.int32)
+    cache = torch.zeros((pages, 2, HKV, PAGE, D), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((M, HQ, D), dtype=torch.bfloat16, device="cuda")
+    inv, conc = _inv_freq_dev()
+    xq = O.make_input(63, M)
+    A.qkv_gemv_rope_append(bf16_dev(xq), bf16_dev(Wq), bf16_dev(bq), i32_dev(pos), i32_dev(slots),
+                           inv, conc, cache, q, norm_w=bf16_dev(nw), eps=1e-5)
+    rq, rk, rv = AO.split_qkv(AO.linear(O.rms_norm(xq, nw, 1e-5), Wq, bq))
+    _ulp_close(host_bf16(q), AO.rope(rq, pos), "q", frac=0.03)
+    c = host_bf16(cache)
+    rk = AO.rope(rk, pos)
+    for i in range(M):
+        pg, sl = divmod(int(slots[i]), PAGE)
+        _ulp_close(c[pg, 0, :, sl], rk[i], "k", frac=0.03)
+        _ulp_close(c[pg, 1, :, sl], rv[i], "v", frac=0.03)
