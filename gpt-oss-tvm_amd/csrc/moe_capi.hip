@@ -4,6 +4,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "../../include/moe_gfx950.h"
@@ -27,7 +28,7 @@ int moe_launch_router_logits(const void* x, const void* norm_w, const void* gate
 int moe_select_chunks(int n);
 int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out, void* w_out,
                             void* counts, void* indptr, void* sorted_pairs, void* token_indices,
-                            void* expert_ids, void* pair_pos, hipStream_t stream);
+                            void* expert_ids, void* pair_pos, int zero_ints, hipStream_t stream);
 size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
 size_t moe_pieces_total_bytes(int64_t rows, int64_t K, int pieces);
 int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, void* packed,
@@ -51,7 +52,8 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* scales1, const void* bias1, const void* blocks2,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
-                         void* status, hipStream_t stream);
+                         void* status, const void* w, const void* x, void* out, void* arrive,
+                         hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
                       hipStream_t stream);
 }
@@ -80,6 +82,12 @@ inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // kGemmMinTokens or more tokens (each weight tile then serves many tokens),
 // the grouped GEMV below that or when N is not a multiple of its tile.
 constexpr int64_t kGemmMinTokens = 48;
+
+// The decode launch combines a token's k mlp2 rows itself (the last of its k
+// tiles to arrive sums them) up to this many tokens; above it a separate
+// gating kernel is faster: the combine's device-scope round trips (arrival
+// count, then the y rows) sit at the launch's tail.
+constexpr int64_t kFusedCombineMaxTokens = 32;
 
 int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indptr,
                   const int32_t* sorted_pairs, int k_top, int arow_mode, int orow_mode,
@@ -127,8 +135,10 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
       nk * (size_t)H * 4,     // y        fp32 [n*k, H]
       (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
-      // counts int32 [chunks of 16 tokens, E] (the large-n grouping)
-      (size_t)moe_select_chunks((int)n) * E * 4,
+      // counts int32: [chunks of 16 tokens, E] (the grouping above 128
+      // tokens), or [n, H / 16] (the decode launch's arrival counts)
+      std::max((size_t)moe_select_chunks((int)n) * E,
+               n <= kFusedCombineMaxTokens ? (size_t)n * (H / 16) : 0) * 4,
       // sync int32 [E + 1]: the decode launch's per-expert mlp1 completion
       // counts and its status word (zeroed by the logits kernel)
       (size_t)(E + 1) * 4,
@@ -370,7 +380,7 @@ int moe_mlp_decode(const void* t_pieces, const int32_t* indptr, const int32_t* s
   return moe_launch_mx_decode(t_pieces, (int)n, indptr, sorted_pairs, (int)k, mlp1_blocks,
                               mlp1_scales, mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E,
                               (int)H, (int)I, (int)(n * k), alpha, limit, act_pieces, y, done,
-                              done + E, as_stream(stream));
+                              done + E, nullptr, nullptr, nullptr, nullptr, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -455,17 +465,24 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
                                      logits, t_pk, t_qs, sync, s)))
     return rc;
+  // the decode launch's arrival counts (fused combine) zeroed by the selection
+  // kernel
+  const bool fuse = !gemm && n <= kFusedCombineMaxTokens;
+  const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
-                                    ei, pp, s)))
+                                    ei, pp, zero_ints, s)))
     return rc;
   // Decode (at most 128 tokens, the shape and device fit): mlp1, the encoding
   // of act and mlp2 in one launch.
   if (!gemm && n <= 128) {
+    // up to kFusedCombineMaxTokens with the gated combine: the last of a
+    // token's k mlp2 tiles to arrive writes its 16 columns of out (NaN if a
+    // wait gave up); above, the gating kernel (NaN rows after a give-up)
     rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
                               mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
-                              (int)I, nk, alpha, limit, act_pk, y, sync, sync + E, s);
-    // a nonzero status (a wait gave up) makes the gating write NaN rows
-    if (rc == MOE_OK)
+                              (int)I, nk, alpha, limit, act_pk, y, sync, sync + E,
+                              fuse ? w : nullptr, x, fuse ? out : nullptr, counts, s);
+    if (rc == MOE_OK && !fuse)
       return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s);
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }

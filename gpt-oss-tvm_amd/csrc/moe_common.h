@@ -193,7 +193,10 @@ __device__ __forceinline__ float key_value(uint32_t key) {
 }
 
 // Cache-policy operand of the global_load_lds builtin: sc1 = device scope.
-constexpr int kCpolSc1 = 16;
+constexpr int kCpolSc1 = 16;  // also the aux operand of the buffer-load builtins
+// Word 3 of a raw buffer resource (32-bit data format; byte offsets, no
+// swizzle): loads past num_records return zero.
+constexpr int kBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");

@@ -685,7 +685,14 @@ __device__ __forceinline__ void mx_pass(
               if ((h == 0 || g == 0) && tt < nb) {
                 const int j = start + b0 + tt;
                 const int orow = orow_mode == 0 ? rowmap[tt] : j;
-                out[(size_t)orow * out_ld + r0 + r] = h == 0 ? y0 : y1;
+                float* dst = out + (size_t)orow * out_ld + r0 + r;
+                // the decode launch's mlp2: device scope (sc1), read by the
+                // gated combine of other workgroups
+                if constexpr (kWait)
+                  __hip_atomic_store(dst, h == 0 ? y0 : y1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+                else
+                  *dst = h == 0 ? y0 : y1;
               }
             }
           } else {
@@ -812,6 +819,52 @@ __device__ __forceinline__ void store_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 constexpr int kDecodeSpinMax = 1 << 20;  // about a second of polling
+
+// The gated combine of one token's 4 columns c0 .. c0 + 3 (model/mlp.py:
+// 346-362 and the residual of :402), as moe_gating_kernel computes it: fp32
+// sum over slots r = 0..k-1 in order of y[token, r] * w[token, r], multiply and
+// add rounded separately, bf16, then bf16(x + moe).  y rows are read with
+// device scope (sc1: other workgroups wrote them with sc1 stores), 16 bytes a
+// lane, so four lanes read one 64-byte row segment; every load of up to 4
+// slots is issued before the first use.  A nonzero status (a wait gave up)
+// makes the columns NaN.
+__device__ __forceinline__ void combine4(__amdgpu_buffer_rsrc_t yr, const uint16_t* w,
+                                         const uint16_t* x, uint16_t* out, const int* status,
+                                         int tok, int k, int H, int c0) {
+#pragma clang fp contract(off)
+  const int st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint2 xv = *(const uint2*)(x + (size_t)tok * H + c0);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int r0 = 0; r0 < k; r0 += 4) {
+    u32x4 v[4];
+    float wr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (r0 + q < k) {
+        const int pr = tok * k + r0 + q;
+        wr[q] = bf2f(w[pr]);
+        v[q] = __builtin_amdgcn_raw_buffer_load_b128(yr, (pr * H + c0) * 4, 0, kCpolSc1);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (r0 + q < k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = acc[i] + __uint_as_float(v[q][i]) * wr[q];
+      }
+    }
+  }
+  uint32_t o[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t xw = j == 0 ? xv.x : xv.y;
+    const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xFFFF0000u);
+    const uint32_t a = f2bf(__fadd_rn(x0, bf2f(f2bf(acc[2 * j]))));
+    const uint32_t b = f2bf(__fadd_rn(x1, bf2f(f2bf(acc[2 * j + 1]))));
+    o[j] = st != 0 ? 0x7FC07FC0u : a | (b << 16);
+  }
+  *(uint2*)(out + (size_t)tok * H + c0) = make_uint2(o[0], o[1]);
+}
 __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
@@ -819,7 +872,8 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint16_t* __restrict__ bias1, const uint8_t* __restrict__ blocks2,
     const uint8_t* __restrict__ scales2, const uint16_t* __restrict__ bias2, int H, int E,
     int gcap2, float alpha, float limit, uint8_t* aq, uint8_t* aqs, float* __restrict__ y,
-    int* done, int* status, int spin_max, int prepoll, int xcds) {
+    int* done, int* status, int spin_max, int prepoll, int xcds, const uint16_t* __restrict__ gw,
+    const uint16_t* __restrict__ resid, uint16_t* __restrict__ out, int* arrive) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kGroupBytes = mx_group_bytes(23);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -841,6 +895,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   L2.pre = L1.tile_ctr + 16;
   const int* const ipl = (const int*)(lds + L1.ipl);
   constexpr int tpb2 = kMxMaxGroups * 5;  // (gcap2 == kMxMaxGroups)
+  if (threadIdx.x == 0) *(int*)(lds + L1.tile_ctr + 8) = 0;  // the combine's job count
   if (wave == 0)
     mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
   else if (wave == 1)
@@ -950,6 +1005,38 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
       lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
       kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2);
+
+  // The gated combine (with the residual), done by whichever workgroup writes
+  // a token's last y tile: every workgroup holds one mlp2 segment (a batch's
+  // tiles t0 .. t0 + len - 1), so after its stores complete it counts each
+  // (token, 16-column tile) it produced; the count that reaches k_top makes
+  // that tile a combine job of this workgroup, and four lanes take each job.
+  // No workgroup waits here.
+  if (out != nullptr && s2.e >= 0) {
+    wait_vmcnt<0>();  // this wave's y stores are complete (visible to every XCD)
+    __syncthreads();  // and every wave's; the pass no longer reads the LDS
+    const int start = ipl[s2.e];
+    const int nb = min(tpb2, ipl[s2.e + 1] - start - s2.b0);
+    const int* rowmap = (const int*)(lds + L2.rowmap);  // the batch's sorted_pairs entries
+    int* jobs = (int*)lds;                               // at most 15 x 180 ints
+    int* njobs = (int*)(lds + L2.tile_ctr + 8);          // zero since the start
+    for (int id = threadIdx.x; id < nb * s2.len; id += blockDim.x) {
+      const int tt = id / s2.len, tile = s2.t0 + id - tt * s2.len;
+      const int job = rowmap[tt] / k_top * ntiles2 + tile;
+      const int prev = __hip_atomic_fetch_add(arrive + job, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == k_top - 1) jobs[atomicAdd(njobs, 1)] = job;
+    }
+    __syncthreads();
+    const int nj = *njobs;
+    const __amdgpu_buffer_rsrc_t yr =
+        __builtin_amdgcn_make_buffer_rsrc(y, (short)0, ipl[E] * H * 4, kBufferWord3);
+    for (int q = threadIdx.x; q < nj * 4; q += blockDim.x) {
+      const int job = jobs[q >> 2];
+      const int tok = job / ntiles2;
+      combine4(yr, gw, resid, out, status, tok, k_top, H, (job - tok * ntiles2) * 16 + (q & 3) * 4);
+    }
+  }
 }
 
 template <int P, int kEpi>
@@ -1196,15 +1283,19 @@ int moe_mx_decode_check(int E, int H, int I, int nk) {
 // n) -> act pieces (3, rows nk, written) -> y (fp32 [nk][H], rows by pair).
 // done: E ints and status: one int, all zero at launch; status counts the
 // workgroups whose bounded wait gave up (their y rows are wrong).
+// With out (and w, x, arrive: n * H / 16 ints, zero at launch) the launch also
+// writes out = bf16(x + bf16(sum_r y[t, r] w[t, r])) (the gated combine).
 int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* sorted_pairs, int k_top, const void* blocks1,
                          const void* scales1, const void* bias1, const void* blocks2,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
-                         void* status, hipStream_t stream) {
+                         void* status, const void* w, const void* x, void* out, void* arrive,
+                         hipStream_t stream) {
   using namespace moe;
   if (nk <= 0) return kOk;
   if (!done || !status) return kErrUnsupported;
+  if (out && (!w || !x || !arrive || (H & 15))) return kErrUnsupported;
   const int rc = moe_mx_decode_check(E, H, I, nk);
   if (rc != kOk) return rc;
   const int grid = kNumCUs;
@@ -1220,7 +1311,8 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                      (const uint8_t*)scales2, (const uint16_t*)bias2, H, E, gcap2, alpha, limit,
                      aq, aq + moe_pieces_q_bytes(nk, I, 3), (float*)y, (int*)done,
                      (int*)status, g_decode_spin_max.load(std::memory_order_relaxed),
-                     nk <= kDecodePrepollMaxPairs ? 1 : 0, grid % kNumXcds == 0 ? kNumXcds : 1);
+                     nk <= kDecodePrepollMaxPairs ? 1 : 0, grid % kNumXcds == 0 ? kNumXcds : 1,
+                     (const uint16_t*)w, (const uint16_t*)x, (uint16_t*)out, (int*)arrive);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -656,7 +656,11 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
     const float* __restrict__ logits, int n, int E, int k, int32_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out, int32_t* __restrict__ indptr,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ token_indices,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos) {
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ pair_pos,
+    int32_t* __restrict__ zero, int zero_ints) {
+  // the decode launch's arrival counts start at zero (a kernel, not a memset:
+  // the call may be captured in a graph)
+  for (int i = threadIdx.x; i < zero_ints; i += blockDim.x) zero[i] = 0;
   __shared__ __align__(16) uint32_t keys[kSelLds];
   __shared__ int topi[kSelTok * 8];
   __shared__ float topv[kSelTok * 8];
@@ -872,10 +876,13 @@ extern "C" int moe_select_chunks(int n) { return (n + moe::kSelChunk - 1) / moe:
 // Top-k + softmax of the logits, then the grouping of the pairs: one
 // workgroup for n <= 128, otherwise a select/count pass over chunks of
 // kSelChunk tokens (counts[chunks][E]) and a placement pass.
+// zero_ints (n <= 128 only): ints of `counts` to zero on the way (the decode
+// launch's arrival counts).
 extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out,
                                        void* w_out, void* counts, void* indptr,
                                        void* sorted_pairs, void* token_indices,
-                                       void* expert_ids, void* pair_pos, hipStream_t stream) {
+                                       void* expert_ids, void* pair_pos, int zero_ints,
+                                       hipStream_t stream) {
   if (E > 256 || k > 8 || k < 1) return moe::kErrUnsupported;
   int32_t* pi = (int32_t*)idx_out;
   uint16_t* pw = (uint16_t*)w_out;
@@ -883,7 +890,7 @@ extern "C" int moe_launch_select_group(const float* logits, int n, int E, int k,
           *ei = (int32_t*)expert_ids, *pp = (int32_t*)pair_pos;
   if (n <= 128) {
     hipLaunchKernelGGL(moe::moe_select_permute_kernel, dim3(1), dim3(1024), 0, stream, logits, n,
-                       E, k, pi, pw, ip, sp, ti, ei, pp);
+                       E, k, pi, pw, ip, sp, ti, ei, pp, (int32_t*)counts, zero_ints);
   } else {
     const int nch = moe_select_chunks(n);
     int32_t* cnt = (int32_t*)counts;

@@ -19,8 +19,11 @@
  *     decode launch (moe_mlp_decode, and moe_block_forward for n <= 128)
  *     waits for other workgroups of its own launch, and if that bounded wait
  *     gives up it reports so in a device status word; the block then writes
- *     NaN to every output element and moe_block_status() returns
- *     MOE_ERR_INCOMPLETE.
+ *     NaN to the output (every element above 32 tokens; up to 32 tokens, where
+ *     the launch combines each token's rows itself as they complete, every
+ *     element combined after the give-up, which includes every element that
+ *     the given-up work fed) and moe_block_status() returns
+ *     MOE_ERR_INCOMPLETE: treat the whole output as invalid.
  *
  * Tensor conventions: bf16 tensors are uint16_t bit patterns, row-major,
  * 16-byte aligned.  MXFP4 weights stay in the checkpoint layout of
@@ -252,9 +255,10 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
 /* Byte offsets of the intermediates inside the block workspace, in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
  * t_pieces, act, act_pieces, y, logits (fp32 [n, E], bf16 values), counts
- * (int32 [ceil(n / 16), E], expert histogram per 16-token chunk, n > 128),
- * sync (int32 [E + 1]: the decode launch's per-expert counts, then its status
- * word). */
+ * (int32 [ceil(n / 16), E], expert histogram per 16-token chunk, n > 128; or
+ * int32 [n, H / 16], the decode launch's arrivals per token and 16-column
+ * tile of y, n <= 32), sync (int32 [E + 1]: the decode launch's per-expert
+ * counts, then its status word). */
 MOE_API int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
                                  size_t offsets[15]);
 
@@ -280,7 +284,8 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
  * threads) race and give wrong results; calls in order on one stream are
  * safe.  The array keeps the last call's contents, and nothing in it needs to
  * start at zero.  moe_block_status does not apply (the status word lives in
- * the static array; the outputs are NaN if the decode launch gave up).
+ * the static array; the outputs are NaN, as for moe_block_forward, if the
+ * decode launch gave up).
  */
 MOE_API int moe_block_forward_noalloc(const uint16_t* x, int64_t n, int64_t E, int64_t k,
                                       int64_t H, int64_t I, const uint16_t* norm_w,

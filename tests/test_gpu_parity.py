@@ -328,10 +328,13 @@ def block20b():
     return p, make_block(p)
 
 
-@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (5, 12), (520, 16)])
+@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (5, 12), (32, 13), (33, 14), (520, 16)])
 def test_block_20b_shape(native, block20b, n, seed):
     """BASELINE configs 0 (n = 1) and 1 (n = 64) at full 20B shape, a ragged n,
-    and 520 tokens (the tiled GEMM path)."""
+    both sides of the decode launch's fused-combine limit (32 tokens: the
+    launch sums the k rows itself; 33: the gating kernel does; the staged
+    check compares the block with the gating kernel bit for bit), and 520
+    tokens (the tiled GEMM path)."""
     p, blk = block20b
     x = O.make_input(seed, n)
     tr = O.block_forward(x, p)
@@ -419,7 +422,7 @@ def test_mlp_decode_unsupported(native, block20b):
                           blk.mlp2_weight_scales, blk.mlp2_bias, 1.702, blk.swiglu_limit)
 
 
-@pytest.mark.parametrize("n,mode", [(64, "four"), (128, "four"), (100, "zipf")])
+@pytest.mark.parametrize("n,mode", [(32, "four"), (64, "four"), (128, "four"), (100, "zipf")])
 def test_block_decode_skewed_routing(native, n, mode):
     """The one-launch decode chain with heavy experts: every token on experts
     0..3 (64 or 128 tokens each: several mlp1 batches of 16 and mlp2 batches of
@@ -462,14 +465,16 @@ def test_block_deterministic_and_empty(native, block20b):
 # the decode launch's bounded wait: a give-up is reported, never silent
 # ---------------------------------------------------------------------------
 
-def test_decode_wait_give_up_is_reported(native, block20b):
+@pytest.mark.parametrize("n", [16, 64])
+def test_decode_wait_give_up_is_reported(native, block20b, n):
     """With the wait bound set to 0 polls from the host, every phase-2
     workgroup of the decode launch gives up at once (all kernels still run to
     their end): moe_block_status reports MOE_ERR_INCOMPLETE, every output is
-    NaN, and the standalone launch's status word counts the give-ups.  With
-    the default bound restored the same calls are correct again."""
+    NaN (16 tokens: the launch's own combine; 64: the gating kernel), and the
+    standalone launch's status word counts the give-ups.  With the default
+    bound restored the same calls are correct again."""
     p, blk = block20b
-    n, H = 64, 2880
+    H = 2880
     x = O.make_input(28, n)
     xd = bf16_dev(x).view(1, n, H)
     prev = native.set_decode_spin_limit(0)
