@@ -118,9 +118,15 @@ constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exac
 constexpr int kPiecesAct = 3;
 constexpr int kPiecesF32 = 4;
 
+// The fp32 act rows have a region of their own only where mlp2 reads them
+// while writing y (at most two pairs per expert: the GEMV encodes act while
+// staging it).  Otherwise act, when a path writes it at all, is last read by
+// the pieces kernel before mlp2 starts, and shares y's bytes (y holds
+// max(H, I) columns' worth).
 void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kNumRegions],
             size_t* total) {
   const size_t nk = (size_t)n * (size_t)k;
+  const bool own_act = (int64_t)nk <= 2 * E;
   const size_t sizes[kNumRegions] = {
       (size_t)n * H * 2,      // t        bf16 [n, H]
       nk * 4,                 // idx      int32 [n, k]
@@ -131,9 +137,9 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       nk * 4,                 // expert_ids
       nk * 4,                 // pair_pos
       moe_pieces_total_bytes(n, H, kPiecesT),          // t_pieces
-      nk * (size_t)I * 4,                              // act      fp32 [n*k, I]
+      own_act ? nk * (size_t)I * 4 : 0,                // act      fp32 [n*k, I]
       moe_pieces_total_bytes((int64_t)nk, I, kPiecesAct),  // act_pieces
-      nk * (size_t)H * 4,     // y        fp32 [n*k, H]
+      nk * (size_t)std::max(H, I) * 4,                 // y        fp32 [n*k, H]
       (size_t)n * E * 4,      // logits   fp32 [n, E] (bf16 values)
       // counts int32: [chunks of 16 tokens, E] (the grouping above 128
       // tokens), or [n, H / 16] (the decode launch's arrival counts)
@@ -148,6 +154,7 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
     off[i] = o;
     o = round_up(o + sizes[i], 256);
   }
+  if (!own_act) off[9] = off[11];
   *total = o;
 }
 

@@ -254,7 +254,9 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
 
 /* Byte offsets of the intermediates inside the block workspace, in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
- * t_pieces, act, act_pieces, y, logits (fp32 [n, E], bf16 values), counts
+ * t_pieces, act (fp32 [n*k, I]; where n*k > 2E it shares y's offset: its
+ * last reader runs before y is written), act_pieces, y (fp32 [n*k, H], in a
+ * region of n*k*max(H, I) floats), logits (fp32 [n, E], bf16 values), counts
  * (int32 [ceil(n / 16), E], expert histogram per 16-token chunk, n > 128; or
  * int32 [n, H / 16], the decode launch's arrivals per token and 16-column
  * tile of y, n <= 32), sync (int32 [E + 1]: the decode launch's per-expert
@@ -277,8 +279,8 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
  * allocates every intermediate itself.  The workspace is a static device
  * array of 48 MiB held by each GPU the library runs on until the process
  * ends; nothing is allocated (no hipMalloc/hipFree) by this call.  Limit:
- * moe_workspace_bytes(n, E, k, H, I) <= 48 MiB (n <= 357 tokens at
- * gpt-oss-20b's shape, n <= 356 at 120b's), else MOE_ERR_TOO_LARGE with no
+ * moe_workspace_bytes(n, E, k, H, I) <= 48 MiB (n <= 530 tokens at
+ * gpt-oss-20b's shape, n <= 528 at 120b's), else MOE_ERR_TOO_LARGE with no
  * launch.  Same results as moe_block_forward.  Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (other streams or host
  * threads) race and give wrong results; calls in order on one stream are

@@ -147,14 +147,33 @@ def test_validation_rejects_bad_arguments(native):
 
 
 def test_workspace_layout(native):
-    n, E, k, H, I = 64, 32, 4, 2880, 2880
-    total = native.workspace_bytes(n, E, k, H, I)
-    offs = native.workspace_layout(n, E, k, H, I)
-    assert len(offs) == 15 and offs == sorted(offs) and all(o % 256 == 0 for o in offs)
-    assert offs[11] + n * k * H * 4 <= offs[12]             # y before logits
-    assert offs[13] + (n + 15) // 16 * E * 4 <= offs[14]    # counts, then sync
-    assert offs[14] + (E + 1) * 4 <= total                  # sync last: E counts + status
-    assert native.workspace_bytes(n, E, k, H + 1, I) == 0
+    E, k, H, I = 32, 4, 2880, 2880
+    for n in (64, 16, 8, 1):
+        total = native.workspace_bytes(n, E, k, H, I)
+        offs = native.workspace_layout(n, E, k, H, I)
+        nk = n * k
+        assert len(offs) == 15 and all(o % 256 == 0 for o in offs)
+        if nk > 2 * E:   # act shares y's bytes (read by the pieces kernel before mlp2)
+            assert offs[9] == offs[11]
+            rest = offs[:9] + offs[10:]
+        else:            # mlp2's GEMV reads act while writing y: a region of its own
+            assert offs[9] + nk * I * 4 <= offs[10]
+            rest = offs
+        assert rest == sorted(rest)
+        assert offs[11] + nk * max(H, I) * 4 <= offs[12]     # y before logits
+        counts = max((n + 15) // 16 * E, n * (H // 16) if n <= 32 else 0)
+        assert offs[13] + counts * 4 <= offs[14]            # counts, then sync
+        assert offs[14] + (E + 1) * 4 <= total              # sync last: E counts + status
+    assert native.workspace_bytes(64, E, k, H + 1, I) == 0
+
+
+def test_noalloc_limits_documented(native):
+    """The header's token limits of moe_block_forward_noalloc (48 MiB of
+    static scratch): 530 tokens at gpt-oss-20b's shape, 528 at 120b's."""
+    lim = 48 << 20
+    for E, n_max in ((32, 530), (128, 528)):
+        assert native.workspace_bytes(n_max, E, 4, 2880, 2880) <= lim
+        assert native.workspace_bytes(n_max + 1, E, 4, 2880, 2880) > lim
 
 
 def test_decode_spin_limit_hook(native):

@@ -39,7 +39,7 @@ def test_noalloc_matches_workspace_entry_point():
         m = O.compare_outputs(got, O.block_forward(x, p).out)
         assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, m
     # beyond the 48 MiB scratch: refused with MOE_ERR_TOO_LARGE, nothing launched
-    n = 358
+    n = 531
     x = torch.zeros((n, H), dtype=torch.bfloat16, device="cuda")
     out = torch.zeros((n, H), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError, match=r"\(-8\)"):
