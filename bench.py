@@ -357,7 +357,7 @@ def run_attention(steps: int, dev) -> dict:
     res = {}
     for window in (0, 128):
         span = L if window == 0 else window
-        ws = torch.empty(A.decode_workspace_bytes(B, span), dtype=torch.uint8, device=dev)
+        ws = A.decode_workspace(B, span, dev)
         us = kernel_us(lambda i: A.decode(q, cache, indptr, perm, kv_len, span, window, scale,
                                           sinks, out, ws), steps)
         kv_bytes = B * span * 8 * 64 * 2 * 2

@@ -90,6 +90,13 @@ def decode_workspace_bytes(batch: int, max_span: int) -> int:
     return int(_lib.attn_decode_workspace_bytes(batch, max_span))
 
 
+def decode_workspace(batch: int, max_span: int, device="cuda") -> torch.Tensor:
+    """A zeroed attn_decode workspace (its arrival counts must be zero before
+    the first call; every call leaves them zero)."""
+    return torch.zeros(max(decode_workspace_bytes(batch, max_span), 256), dtype=torch.uint8,
+                       device=device)
+
+
 def _tables(kv_cache, page_indptr, page_indices, kv_len, batch):
     _expect(kv_cache, "kv_cache", torch.bfloat16)
     _expect(page_indptr, "page_indptr", torch.int32, (batch + 1,))
@@ -101,7 +108,8 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, page_indptr: torch.Tensor,
            page_indices: torch.Tensor, kv_len: torch.Tensor, max_span: int, window: int,
            sm_scale: float, sinks: torch.Tensor, out: torch.Tensor,
            workspace: torch.Tensor) -> torch.Tensor:
-    """One query token per sequence over its cached keys (cross_attention)."""
+    """One query token per sequence over its cached keys (cross_attention);
+    ``workspace`` from ``decode_workspace`` (reused across calls)."""
     _expect(q, "q", torch.bfloat16)
     batch = q.shape[0]
     _expect(q, "q", torch.bfloat16, (batch, Q_HEADS, HEAD_DIM))

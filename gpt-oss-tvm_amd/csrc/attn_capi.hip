@@ -16,7 +16,7 @@ int attn_launch_qkv_rope_append(const void* qkv, const void* bias, int n, const 
 int attn_launch_decode(const void* q, int batch, const void* cache, const int* page_indptr,
                        const int* page_indices, int num_pages, const int* kv_len, int window,
                        float sm_scale, const void* sinks, int splits, float* part_o,
-                       float* part_ml, void* out, hipStream_t s);
+                       float* part_ml, int* arrive, void* out, hipStream_t s);
 int attn_launch_prefill(const void* q, const int* q_indptr, int batch, int max_q_len,
                         const void* cache, const int* page_indptr, const int* page_indices,
                         int num_pages, const int* kv_len, int window, float sm_scale,
@@ -80,10 +80,17 @@ int attn_qkv_rope_append(const uint16_t* qkv, const uint16_t* qkv_bias, int64_t 
                                             as_stream(stream)));
 }
 
+// Workspace of attn_decode: the arrival counts [batch][8] (int32, padded to
+// 256 bytes; zero before the first call, left zero by every call), then the
+// split partials o [batch][64][splits][64] and (m, l) [batch][64][splits][2].
+static size_t decode_counts_bytes(int64_t batch) {
+  return ((size_t)batch * kKvHeads * 4 + 255) & ~(size_t)255;
+}
+
 size_t attn_decode_workspace_bytes(int64_t batch, int64_t max_span) {
   if (batch <= 0 || max_span <= 0) return 0;
   const size_t parts = (size_t)batch * kQHeads * (size_t)decode_splits(max_span);
-  return parts * (kHeadDim + 2) * sizeof(float) + 256;
+  return decode_counts_bytes(batch) + parts * (kHeadDim + 2) * sizeof(float) + 256;
 }
 
 int attn_decode(const uint16_t* q, int64_t batch, const void* kv_cache, int64_t num_pages,
@@ -101,11 +108,12 @@ int attn_decode(const uint16_t* q, int64_t batch, const void* kv_cache, int64_t 
   if (workspace_bytes < attn_decode_workspace_bytes(batch, max_span)) return MOE_ERR_WORKSPACE;
   const int64_t splits = decode_splits(max_span);
   if (splits > 65535) return MOE_ERR_SHAPE;
-  float* part_o = (float*)workspace;
+  int* arrive = (int*)workspace;
+  float* part_o = (float*)((char*)workspace + decode_counts_bytes(batch));
   float* part_ml = part_o + (size_t)batch * kQHeads * splits * kHeadDim;
   return status(attn_launch_decode(q, (int)batch, kv_cache, page_indptr, page_indices,
                                    (int)num_pages, kv_len, window, sm_scale, sinks, (int)splits,
-                                   part_o, part_ml, out, as_stream(stream)));
+                                   part_o, part_ml, arrive, out, as_stream(stream)));
 }
 
 int attn_prefill(const uint16_t* q, const int32_t* q_indptr, int64_t batch, int64_t max_q_len,

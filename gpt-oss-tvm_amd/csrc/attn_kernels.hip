@@ -19,6 +19,8 @@ using moe::bf2f;
 using moe::f2bf;
 using moe::f32x4;
 using moe::kWave;
+using moe::load_dev;
+using moe::store_dev;
 using moe::u32x4;
 
 constexpr int kD = 64;          // head_dim
@@ -134,11 +136,16 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
 constexpr int kDecChunk = 128;
 constexpr int kDecKRow = kD + 8;  // padded K row (bf16)
 
+__device__ void decode_merge_group(const float* part_o, const float* part_ml, int splits,
+                                   int used, bool bad, int b, int hk, const uint16_t* sinks,
+                                   uint16_t* out);
+
 __global__ __launch_bounds__(256) void decode_partial_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ cache,
     const int* __restrict__ page_indptr, const int* __restrict__ page_indices, int num_pages,
     const int* __restrict__ kv_len, int window, float sm_scale, int splits,
-    float* __restrict__ part_o, float* __restrict__ part_ml) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ arrive,
+    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t ks[kDecChunk * kDecKRow];
   __shared__ __align__(16) uint16_t vs[kDecChunk * kD];
   __shared__ float qs[kGroup][kD];
@@ -152,11 +159,14 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   const int k0 = lo + s * kDecChunk;
   const int nk = max(0, min(kDecChunk, L - k0));
   const size_t pidx = ((size_t)b * kHq + hk * kGroup) * splits + s;  // head h: + h * splits
+  // the splits holding keys: the first ceil(span / kDecChunk) (at most splits)
+  const int span = L - lo;
+  const int used = min((span + kDecChunk - 1) / kDecChunk, splits);
+  // a split past the attended range holds no keys and writes nothing (the
+  // merge reads only the used splits); an empty range gives NaN outputs
   if (nk == 0) {
-    if (t < kGroup) {
-      part_ml[(pidx + (size_t)t * splits) * 2 + 0] = -INFINITY;
-      part_ml[(pidx + (size_t)t * splits) * 2 + 1] = 0.0f;
-    }
+    if (span <= 0 && s == 0)
+      decode_merge_group(part_o, part_ml, splits, 0, true, b, hk, sinks, out);
     return;
   }
   const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
@@ -243,13 +253,31 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
       o0 = fmaf(sc[h0][kk], v, o0);
       o1 = fmaf(sc[h0 + 4][kk], v, o1);
     }
-    part_o[(pidx + (size_t)h0 * splits) * kD + d] = o0;
-    part_o[(pidx + (size_t)(h0 + 4) * splits) * kD + d] = o1;
+    // device scope (sc1): the merge may run in a workgroup on another XCD
+    store_dev(part_o + (pidx + (size_t)h0 * splits) * kD + d, o0);
+    store_dev(part_o + (pidx + (size_t)(h0 + 4) * splits) * kD + d, o1);
     if (t < kGroup) {
-      part_ml[(pidx + (size_t)t * splits) * 2 + 0] = red[t][0];
-      part_ml[(pidx + (size_t)t * splits) * 2 + 1] = red[t][1];
+      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 0, red[t][0]);
+      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 1, red[t][1]);
     }
   }
+  // The last of the group's used splits to finish merges them: each wave's
+  // stores complete (vmcnt), the workgroup meets, one thread counts the
+  // arrival (agent-scope atomic) and the one that completes the count resets
+  // it to zero for the next call.
+  __shared__ int is_last;
+  moe::wait_vmcnt<0>();
+  __syncthreads();
+  if (t == 0) {
+    int* cnt = arrive + b * kHkv + hk;
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == used - 1;
+    if (is_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (is_last)
+    decode_merge_group(part_o, part_ml, splits, used, span > splits * kDecChunk, b, hk, sinks,
+                       out);
 }
 
 // Sink scaling of attention.py:235-245: lse (natural log) -> s =
@@ -259,38 +287,39 @@ __device__ __forceinline__ float sink_factor(float lse, uint16_t sink) {
   return bf2f(f2bf((float)(1.0 / (1.0 + exp(-(double)z)))));
 }
 
-// Decode attention, phase 2: one wave per (sequence, query head) merges the
-// splits (max, rescaled sums in split order), then lse, the sink factor and
-// the bf16 output.  Lane = dim.  A sequence whose attended range is longer
-// than the splits cover (the caller's bound was too small) gets NaN outputs.
-__global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restrict__ part_o,
-                                                          const float* __restrict__ part_ml,
-                                                          int splits,
-                                                          const int* __restrict__ kv_len,
-                                                          int window,
-                                                          const uint16_t* __restrict__ sinks,
-                                                          uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int L = kv_len[b];
-  const int span = window > 0 ? min(L, window) : L;
-  if (span > splits * kDecChunk || span <= 0) {
-    out[((size_t)b * kHq + h) * kD + d] = 0x7FC0;
-    return;
+// Decode attention, merge: the group's 8 query heads of sequence b (thread
+// -> dim t % 64, heads t / 64 and t / 64 + 4) over the used splits (max,
+// rescaled sums in split order), then lse, the sink factor and the bf16
+// output.  The partials are read with device scope (written by other
+// workgroups).  `bad` (the attended range is empty or longer than the splits
+// cover: the caller's bound was too small) gives NaN outputs.
+__device__ void decode_merge_group(const float* part_o, const float* part_ml, int splits,
+                                   int used, bool bad, int b, int hk, const uint16_t* sinks,
+                                   uint16_t* out) {
+  const int d = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int h = hk * kGroup + (threadIdx.x >> 6) + 4 * j;
+    uint16_t* o_out = out + ((size_t)b * kHq + h) * kD + d;
+    if (bad) {
+      *o_out = 0x7FC0;
+      continue;
+    }
+    const size_t base = ((size_t)b * kHq + h) * splits;
+    float m = -INFINITY;
+    for (int s = 0; s < used; ++s) m = fmaxf(m, load_dev(part_ml + (base + s) * 2));
+    float l = 0.f, o = 0.f;
+    for (int s = 0; s < used; ++s) {
+      const float ms = load_dev(part_ml + (base + s) * 2);
+      if (ms == -INFINITY) continue;
+      const float f = __expf(ms - m);
+      l = fmaf(load_dev(part_ml + (base + s) * 2 + 1), f, l);
+      o = fmaf(load_dev(part_o + (base + s) * kD + d), f, o);
+    }
+    const float lse = m + __logf(l);
+    const float ob = bf2f(f2bf(o / l));
+    *o_out = f2bf(ob * sink_factor(lse, sinks[h]));
   }
-  const size_t base = ((size_t)b * kHq + h) * splits;
-  float m = -INFINITY;
-  for (int s = 0; s < splits; ++s) m = fmaxf(m, part_ml[(base + s) * 2]);
-  float l = 0.f, o = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float ms = part_ml[(base + s) * 2];
-    if (ms == -INFINITY) continue;
-    const float f = __expf(ms - m);
-    l = fmaf(part_ml[(base + s) * 2 + 1], f, l);
-    o = fmaf(part_o[(base + s) * kD + d], f, o);
-  }
-  const float lse = m + __logf(l);
-  const float ob = bf2f(f2bf(o / l));
-  out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
 }
 
 // ---------------------------------------------------------------------------
@@ -587,14 +616,11 @@ int attn_launch_qkv_rope_append(const void* qkv, const void* bias, int n, const 
 int attn_launch_decode(const void* q, int batch, const void* cache, const int* page_indptr,
                        const int* page_indices, int num_pages, const int* kv_len, int window,
                        float sm_scale,
-                       const void* sinks, int splits, float* part_o, float* part_ml, void* out,
-                       hipStream_t s) {
+                       const void* sinks, int splits, float* part_o, float* part_ml, int* arrive,
+                       void* out, hipStream_t s) {
   hipLaunchKernelGGL(attn::decode_partial_kernel, dim3(splits, attn::kHkv, batch), dim3(256), 0, s,
                      (const uint16_t*)q, (const uint8_t*)cache, page_indptr, page_indices,
-                     num_pages, kv_len, window, sm_scale, splits, part_o, part_ml);
-  if (hipGetLastError() != hipSuccess) return -6;
-  hipLaunchKernelGGL(attn::decode_merge_kernel, dim3(attn::kHq, batch), dim3(64), 0, s,
-                     (const float*)part_o, (const float*)part_ml, splits, kv_len, window,
+                     num_pages, kv_len, window, sm_scale, splits, part_o, part_ml, arrive,
                      (const uint16_t*)sinks, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

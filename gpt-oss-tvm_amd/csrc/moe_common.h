@@ -202,6 +202,19 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Device-scope (agent) relaxed stores and loads: on gfx950 the stores write
+// through (sc1) and the loads bypass the non-coherent caches, so data passes
+// between workgroups on different XCDs (each XCD has its own L2) within one
+// launch.  The writer waits for its stores (vmcnt) before the release count.
+template <class T>
+__device__ __forceinline__ void store_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T load_dev(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // s_waitcnt with only the vector-memory count: vmcnt(n), n < 64
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -814,10 +814,6 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
 // polls): a workgroup that gives up adds 1 to *status and goes on, so the
 // launch always ends; its y rows are then wrong and the status says so.
 constexpr int kDecodeGroups1 = 2;  // mlp1 batch: 2 groups of 8 tokens
-template <class T>
-__device__ __forceinline__ void store_dev(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 constexpr int kDecodeSpinMax = 1 << 20;  // about a second of polling
 
 // The gated combine of one token's 4 columns c0 .. c0 + 3 (model/mlp.py:

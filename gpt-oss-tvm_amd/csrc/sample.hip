@@ -11,13 +11,17 @@
 // fp32, model/transformer.py:95-100), so a sequence has at most 65536 distinct
 // logit values.  Instead of a sort:
 //   1. count the elements of each value in a 65536-bin histogram (integer
-//      atomics: deterministic) and take the maximum;
-//   2. one workgroup walks the bins in descending value order: mass of a bin =
-//      count x exp((v - max) / T); the two crossings (top_p, then u times the
-//      top-p mass) are found at element granularity inside their bins, in
-//      fp64; the result is a value v* and a rank j* among the elements of that
-//      value (equal logits are taken in index order);
-//   3. the j*-th element of value v* in index order: matches counted per
+//      atomics: deterministic) and take the maximum; each workgroup counts
+//      its 16384 elements in LDS first and adds one global atomic per value
+//      it saw;
+//   2. the masses of 64 segments of 1024 bins (descending values): mass of a
+//      bin = count x exp((v - max) / T), summed per segment in a fixed order;
+//   3. one workgroup finds the two crossings (top_p, then u times the top-p
+//      mass): the segment from the 64 segment masses, the bin from a scan of
+//      that segment's 1024 masses, the element inside the bin in fp64; the
+//      result is a value v* and a rank j* among the elements of that value
+//      (equal logits are taken in index order);
+//   4. the j*-th element of value v* in index order: matches counted per
 //      index range by 64 workgroups, then the owning range searched by one.
 // The histogram is left zeroed after each call (it must be zero before the
 // first): nothing is cleared with a memset, so the calls can be captured.
@@ -35,6 +39,8 @@ using moe::bf2f;
 using moe::u32x4;
 
 constexpr int kBins = 65536;
+constexpr int kSegBins = 1024;           // bins per mass segment (one thread each)
+constexpr int kSegs = kBins / kSegBins;  // 64
 
 // exp((v - max) * scale): the argument in fp32 as written, exp rounded once
 // to fp32 (through fp64), carried as fp64 for the exact sums
@@ -59,42 +65,60 @@ struct State {  // per sequence, after the histogram
   uint32_t pick_rank; // 1-based rank among the elements of that value
   uint32_t pad;
   uint32_t part_count[64];  // matches of the chosen value per index range
+  double seg_mass[kSegs];   // mass of bins 65535 - 1024 p - [0, 1024) per segment p
 };
 
-// 1. histogram and maximum.  Grid (ceil(V / 2048), batch), 256 threads x 8.
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ logits, int V,
-                                                   State* __restrict__ st) {
-  const int b = blockIdx.y;
+// 1. histogram and maximum.  Grid (ceil(V / 16384), batch), 1024 threads x 16
+// elements.  The workgroup's counts go to LDS first as 16-bit counters, two
+// per word (a workgroup sees at most 16384 elements, so a count never carries
+// into its neighbour), then one global atomic per nonzero bin.
+constexpr int kHistThreads = 1024;
+constexpr int kHistElems = kHistThreads * 16;
+constexpr size_t kHistLds = kBins * 2;  // 128 KB
+
+__global__ __launch_bounds__(kHistThreads) void hist_kernel(const uint16_t* __restrict__ logits,
+                                                            int V, State* __restrict__ st) {
+  extern __shared__ __align__(16) uint32_t h[];  // kBins / 2 words
+  const int b = blockIdx.y, t = threadIdx.x;
   const uint16_t* l = logits + (size_t)b * V;
   State& s = st[b];
-  const int i0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  for (int i = t; i < kBins / 8; i += kHistThreads) ((u32x4*)h)[i] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
   uint32_t mk = 0;
-  if (i0 + 8 <= V && (V & 7) == 0) {
-    const u32x4 v = *(const u32x4*)(l + i0);
+  auto add = [&](uint32_t k) {
+    atomicAdd(&h[k >> 1], 1u << ((k & 1u) << 4));
+    mk = max(mk, k);
+  };
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t k0 = key16(v[j] & 0xFFFFu), k1 = key16(v[j] >> 16);
-      atomicAdd(&s.counts[k0], 1u);
-      atomicAdd(&s.counts[k1], 1u);
-      mk = max(mk, max(k0, k1));
+  for (int j = 0; j < 2; ++j) {
+    const int i0 = blockIdx.x * kHistElems + (j * kHistThreads + t) * 8;
+    if (i0 + 8 <= V && (V & 7) == 0) {
+      const u32x4 v = *(const u32x4*)(l + i0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        add(key16(v[q] & 0xFFFFu));
+        add(key16(v[q] >> 16));
+      }
+    } else {
+      for (int i = i0; i < min(i0 + 8, V); ++i) add(key16(l[i]));
     }
-  } else {
-    for (int i = i0; i < min(i0 + 8, V); ++i) {
-      const uint32_t k = key16(l[i]);
-      atomicAdd(&s.counts[k], 1u);
-      mk = max(mk, k);
+  }
+  __syncthreads();
+  for (int i = t; i < kBins / 8; i += kHistThreads) {
+    const u32x4 v = ((const u32x4*)h)[i];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (v[q] & 0xFFFFu) atomicAdd(&s.counts[8 * i + 2 * q], v[q] & 0xFFFFu);
+      if (v[q] >> 16) atomicAdd(&s.counts[8 * i + 2 * q + 1], v[q] >> 16);
     }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, off, 64));
-  if ((threadIdx.x & 63) == 0 && mk) atomicMax(&s.max_key, mk);
+  if ((t & 63) == 0 && mk) atomicMax(&s.max_key, mk);
 }
 
-// 2. the two crossings.  One 1024-thread workgroup per sequence; thread t owns
-// the 64 bins of keys [65535 - 64 t - 63, 65535 - 64 t] (descending values).
-constexpr int kSelThreads = 1024;
-constexpr int kPerThread = kBins / kSelThreads;
-
+// Fixed-order sums over a 1024-thread workgroup: exclusive prefix of v in
+// thread order (lane scan, then the 16 wave totals in order) and the total.
 __device__ double block_exclusive_scan(double v, double* tmp, double* total) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   double incl = v;
@@ -107,7 +131,7 @@ __device__ double block_exclusive_scan(double v, double* tmp, double* total) {
   __syncthreads();
   if (t == 0) {
     double acc = 0.0;
-    for (int i = 0; i < kSelThreads / 64; ++i) {
+    for (int i = 0; i < kSegBins / 64; ++i) {
       const double x = tmp[i];
       tmp[i] = acc;
       acc += x;
@@ -120,21 +144,39 @@ __device__ double block_exclusive_scan(double v, double* tmp, double* total) {
   return r;
 }
 
-__global__ __launch_bounds__(kSelThreads) void select_kernel(State* __restrict__ st,
-                                                             float temperature, float top_p,
-                                                             float uniform) {
-  __shared__ double tmp[kSelThreads / 64];
+// The mass of bin key k (0 for an empty bin).
+__device__ __forceinline__ double bin_mass(uint32_t c, uint32_t k, float m, float scale) {
+  return c ? (double)c * weight(value_of(k), m, scale) : 0.0;
+}
+
+// 2. segment masses.  Grid (64, batch), 1024 threads: thread t of segment p
+// holds bin 65535 - 1024 p - t.
+__global__ __launch_bounds__(kSegBins) void mass_kernel(State* __restrict__ st,
+                                                        float temperature) {
+  __shared__ double tmp[kSegBins / 64];
+  __shared__ double tot;
+  if (temperature < 1e-6f) return;  // argmax: no masses
+  State& s = st[blockIdx.y];
+  const int p = blockIdx.x;
+  const uint32_t k = 65535u - kSegBins * p - threadIdx.x;
+  const double v = bin_mass(s.counts[k], k, value_of(s.max_key), 1.0f / temperature);
+  block_exclusive_scan(v, tmp, &tot);
+  if (threadIdx.x == 0) s.seg_mass[p] = tot;
+}
+
+// 3. the two crossings.  One 1024-thread workgroup per sequence.
+__global__ __launch_bounds__(kSegBins) void select_kernel(State* __restrict__ st,
+                                                          float temperature, float top_p,
+                                                          float uniform) {
+  __shared__ double tmp[kSegBins / 64];
+  __shared__ double segm[kSegs];
+  __shared__ double segpre[kSegs + 1];  // exclusive prefix of the segment masses
   __shared__ double tot_s, crossing_s;
-  __shared__ int found, owner1, owner2;
+  __shared__ int seg_s, owner, last_nz;
   State& s = st[blockIdx.x];
   const int t = threadIdx.x;
   const uint32_t mk = s.max_key;
   const float m = value_of(mk);
-  const int top_bin = 65535 - kPerThread * t;  // this thread's bins: top_bin down to top_bin - 63
-  if (t == 0) {
-    found = 0;
-    owner1 = owner2 = kSelThreads;
-  }
   if (temperature < 1e-6f) {
     // argmax: the first element of the largest value
     if (t == 0) {
@@ -143,89 +185,99 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(State* __restrict__
     }
   } else {
     const float scale = 1.0f / temperature;
-    double mass = 0.0;
-    for (int i = 0; i < kPerThread; ++i) {
-      const int k = top_bin - i;
-      const uint32_t c = s.counts[k];
-      if (c) mass += (double)c * weight(value_of(k), m, scale);
-    }
-    const double before = block_exclusive_scan(mass, tmp, &tot_s);
-    const double total = tot_s;
-    // crossing 1: the element at which the running sum reaches top_p; the
-    // top-p mass runs up to and including it
-    const double tp = (double)top_p * total;
-    // the first segment holding a crossing does the element-level search
-    // (rounding of the scan could let two neighbours both claim it)
-    if (before < tp && before + mass >= tp) atomicMin(&owner1, t);
+    if (t < kSegs) segm[t] = s.seg_mass[t];
     __syncthreads();
-    if (t == owner1) {
-      double run = before;
-      int i = 0;
-      for (; i < kPerThread; ++i) {
-        const int k = top_bin - i;
-        const uint32_t c = s.counts[k];
-        if (!c) continue;
-        const double p = weight(value_of(k), m, scale);
-        if (run + c * p >= tp) {
-          const double j = ceil((tp - run) / p);          // elements with sum before < tp
-          run += fmin(fmax(j, 1.0), (double)c) * p;
-          break;
-        }
-        run += c * p;
+    if (t == 0) {
+      double acc = 0.0;
+      for (int p = 0; p < kSegs; ++p) {
+        segpre[p] = acc;
+        acc += segm[p];
       }
-      crossing_s = run;  // (the segment's end if rounding put the crossing past it)
-      found = 1;
+      segpre[kSegs] = acc;
     }
     __syncthreads();
-    if (t == 0 && !found) crossing_s = total;  // top_p >= 1: everything
+    // The segment whose range [segpre[p], segpre[p + 1]) holds a crossing
+    // (strict: the first with segpre[p] <= x < segpre[p + 1], else the first
+    // with segpre[p] < x <= segpre[p + 1]), then the bin: the segment's 1024
+    // masses scanned in bin order from segpre[p]; owner = the first bin whose
+    // range holds x.  A rounding difference between the segment's own sum and
+    // its scan leaves the owner at kSegBins (none).
+    auto locate = [&](double x, bool strict, uint32_t& c, uint32_t& k, double& before,
+                      double& mass) -> int {
+      if (t == 0) {
+        seg_s = -1;
+        owner = kSegBins;
+        last_nz = -1;
+        for (int p = 0; p < kSegs; ++p) {
+          const bool in = strict ? (segpre[p] <= x && x < segpre[p + 1])
+                                 : (segpre[p] < x && x <= segpre[p + 1]);
+          if (in) {
+            seg_s = p;
+            break;
+          }
+        }
+      }
+      __syncthreads();
+      const int p = seg_s;
+      if (p < 0) return -1;  // uniform
+      k = 65535u - kSegBins * p - t;
+      c = s.counts[k];
+      mass = bin_mass(c, k, m, scale);
+      before = segpre[p] + block_exclusive_scan(mass, tmp, &tot_s);
+      const bool in = strict ? (before <= x && x < before + mass)
+                             : (before < x && x <= before + mass);
+      if (in) atomicMin(&owner, t);
+      if (c) atomicMax(&last_nz, t);
+      __syncthreads();
+      return p;
+    };
+    uint32_t c = 0, k = 0;
+    double before = 0.0, mass = 0.0;
+    // crossing 1: the element at which the running sum reaches top_p x total;
+    // the top-p mass runs up to and including it
+    const double tp = (double)top_p * segpre[kSegs];
+    const int p1 = locate(tp, false, c, k, before, mass);
+    if (t == 0) crossing_s = p1 < 0 ? segpre[kSegs] : segpre[p1 + 1];  // none: everything
+    __syncthreads();
+    if (p1 >= 0 && t == owner) {
+      const double w = mass / c;
+      const double j = ceil((tp - before) / w);  // elements with sum before < tp
+      crossing_s = before + fmin(fmax(j, 1.0), (double)c) * w;
+    }
     __syncthreads();
     // crossing 2: the first element whose cumulative mass exceeds u x top-p mass
     const double x = (double)uniform * crossing_s;
-    if (t == 0) found = 0;
-    if (before <= x && before + mass > x) atomicMin(&owner2, t);
-    __syncthreads();
-    if (t == owner2) {
-      double run = before;
-      int last = -1;
-      for (int i = 0; i < kPerThread; ++i) {
-        const int k = top_bin - i;
-        const uint32_t c = s.counts[k];
-        if (!c) continue;
-        last = k;
-        const double p = weight(value_of(k), m, scale);
-        if (run + c * p > x) {
-          const double j = floor((x - run) / p) + 1.0;
-          s.pick_key = (uint32_t)k;
-          s.pick_rank = (uint32_t)fmin(fmax(j, 1.0), (double)c);
-          last = -2;
-          break;
-        }
-        run += c * p;
+    const int p2 = locate(x, true, c, k, before, mass);
+    if (p2 < 0) {
+      // past the top-p mass: the first element of the largest value
+      if (t == 0) {
+        s.pick_key = mk;
+        s.pick_rank = 1;
       }
-      if (last >= 0) {  // rounding put the crossing past the segment: its last element
-        s.pick_key = (uint32_t)last;
-        s.pick_rank = s.counts[last];
+    } else if (owner < kSegBins) {
+      if (t == owner) {
+        const double w = mass / c;
+        const double j = floor((x - before) / w) + 1.0;
+        s.pick_key = k;
+        s.pick_rank = (uint32_t)fmin(fmax(j, 1.0), (double)c);
       }
-      found = 1;
-    }
-    __syncthreads();
-    if (t == 0 && !found) {  // past the top-p mass: the first element of the largest value
-      s.pick_key = mk;
-      s.pick_rank = 1;
+    } else if (t == last_nz) {  // rounding put the crossing past the bins: the last element
+      s.pick_key = k;
+      s.pick_rank = c;
     }
   }
-  __syncthreads();
-  // leave the histogram zeroed for the next call
-  for (int i = t; i < kBins; i += kSelThreads) s.counts[i] = 0u;
-  if (t == 0) s.max_key = 0u;
 }
 
-// 3. the pick_rank-th element of value pick_key, in index order, in two
+// 4. the pick_rank-th element of value pick_key, in index order, in two
 // launches: count_kernel counts the matches of each of kFindParts contiguous
-// ranges (16-byte loads), locate_kernel finds the range holding the wanted
-// rank and the element inside it (a block-wide prefix over that range).
+// ranges (16-byte loads) and leaves the histogram zeroed for the next call
+// (part p clears bins [1024 p, 1024 p + 1024)), locate_kernel finds the range
+// holding the wanted rank and the element inside it (a block-wide prefix over
+// that range).
 constexpr int kFindParts = 64;
 constexpr int kFindThreads = 256;
+constexpr int kLocThreads = 1024;
+static_assert(kBins == kFindParts * kFindThreads * 4, "one 16-byte clear per thread");
 
 __device__ __forceinline__ int part_begin(int V, int p) {
   // ranges of whole 8-element groups (the last one takes the remainder)
@@ -239,6 +291,8 @@ __global__ __launch_bounds__(kFindThreads) void count_kernel(const uint16_t* __r
   const int b = blockIdx.y, p = blockIdx.x, t = threadIdx.x;
   const uint16_t* l = logits + (size_t)b * V;
   const uint32_t want = st[b].pick_key;
+  ((u32x4*)st[b].counts)[p * kFindThreads + t] = u32x4{0u, 0u, 0u, 0u};
+  if (p == 0 && t == 0) st[b].max_key = 0u;
   const int i0 = part_begin(V, p), i1 = part_begin(V, p + 1);
   int c = 0;
   for (int i = i0 + t * 8; i < i1; i += kFindThreads * 8) {
@@ -258,11 +312,11 @@ __global__ __launch_bounds__(kFindThreads) void count_kernel(const uint16_t* __r
   if (t == 0) st[b].part_count[p] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
 }
 
-__global__ __launch_bounds__(kFindThreads) void locate_kernel(const uint16_t* __restrict__ logits,
-                                                              int V, const State* __restrict__ st,
-                                                              int* __restrict__ out) {
+__global__ __launch_bounds__(kLocThreads) void locate_kernel(const uint16_t* __restrict__ logits,
+                                                             int V, const State* __restrict__ st,
+                                                             int* __restrict__ out) {
   __shared__ int base_s, part_s;
-  __shared__ int wsum[kFindThreads / 64];
+  __shared__ int wsum[kLocThreads / 64];
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const uint16_t* l = logits + (size_t)b * V;
   const State& s = st[b];
@@ -277,9 +331,9 @@ __global__ __launch_bounds__(kFindThreads) void locate_kernel(const uint16_t* __
   }
   __syncthreads();
   const int i0 = part_begin(V, part_s), i1 = part_begin(V, part_s + 1);
-  // chunks of kFindThreads elements in index order; a running count across them
+  // chunks of kLocThreads elements in index order; a running count across them
   int before_chunk = base_s;
-  for (int c0 = i0; c0 < i1; c0 += kFindThreads) {
+  for (int c0 = i0; c0 < i1; c0 += kLocThreads) {
     const int i = c0 + t;
     const int hit = i < i1 && key16(l[i]) == want;
     int incl = hit;
@@ -290,9 +344,11 @@ __global__ __launch_bounds__(kFindThreads) void locate_kernel(const uint16_t* __
     }
     if (lane == 63) wsum[w] = incl;
     __syncthreads();
-    int pre = 0;
-    for (int k = 0; k < w; ++k) pre += wsum[k];
-    const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    int pre = 0, total = 0;
+    for (int k = 0; k < kLocThreads / 64; ++k) {
+      pre += k < w ? wsum[k] : 0;
+      total += wsum[k];
+    }
     if (hit && before_chunk + pre + incl == rank) out[b] = i;
     before_chunk += total;
     __syncthreads();
@@ -309,16 +365,24 @@ size_t attn_sample_state_bytes() { return sizeof(smp::State); }
 int attn_launch_sample(const void* logits, int batch, int V, float temperature, float top_p,
                        float uniform, int* out, void* state, hipStream_t s) {
   smp::State* st = (smp::State*)state;
-  hipLaunchKernelGGL(smp::hist_kernel, dim3((V + 2047) / 2048, batch), dim3(256), 0, s,
-                     (const uint16_t*)logits, V, st);
+  static const bool lds_ok =  // more than 64 KB of dynamic LDS, once
+      hipFuncSetAttribute((const void*)smp::hist_kernel,
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)smp::kHistLds) == hipSuccess;
+  if (!lds_ok) return -6;
+  hipLaunchKernelGGL(smp::hist_kernel, dim3((V + smp::kHistElems - 1) / smp::kHistElems, batch),
+                     dim3(smp::kHistThreads), smp::kHistLds, s, (const uint16_t*)logits, V, st);
   if (hipGetLastError() != hipSuccess) return -6;
-  hipLaunchKernelGGL(smp::select_kernel, dim3(batch), dim3(smp::kSelThreads), 0, s, st,
+  hipLaunchKernelGGL(smp::mass_kernel, dim3(smp::kSegs, batch), dim3(smp::kSegBins), 0, s, st,
+                     temperature);
+  if (hipGetLastError() != hipSuccess) return -6;
+  hipLaunchKernelGGL(smp::select_kernel, dim3(batch), dim3(smp::kSegBins), 0, s, st,
                      temperature, top_p, uniform);
   if (hipGetLastError() != hipSuccess) return -6;
   hipLaunchKernelGGL(smp::count_kernel, dim3(smp::kFindParts, batch), dim3(smp::kFindThreads), 0,
                      s, (const uint16_t*)logits, V, st);
   if (hipGetLastError() != hipSuccess) return -6;
-  hipLaunchKernelGGL(smp::locate_kernel, dim3(batch), dim3(smp::kFindThreads), 0, s,
+  hipLaunchKernelGGL(smp::locate_kernel, dim3(batch), dim3(smp::kLocThreads), 0, s,
                      (const uint16_t*)logits, V, (const smp::State*)st, out);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

@@ -96,9 +96,17 @@ class Engine:
     # -- the decode step in one HIP graph ---------------------------------------------
     def _step_body(self) -> None:
         embed = self.model.embed(self._token)
-        logits = self.model.decode(embed, self.paged_kv_cache)
-        self.graph_logits = logits
-        self.sample_device(logits)
+        lb = self.model.decode_logits_bf16(embed, self.paged_kv_cache)
+        self._graph_logits_bf16 = lb
+        p = self.sample_parameters
+        A.sample_top_p(lb[-1:], p["temperature"], p["top_p"], p["random_seed"], self._sample_ws,
+                       self._token)
+
+    @property
+    def graph_logits(self) -> torch.Tensor:
+        """fp32 logits [1, 1, vocab] of the last captured decode step (its bf16
+        logits, converted on request)."""
+        return self._graph_logits_bf16.float().view(1, -1, self.config.vocab_size)
 
     @torch.no_grad()
     def capture_decode(self, sequence_id: int) -> None:

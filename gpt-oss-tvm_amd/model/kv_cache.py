@@ -70,15 +70,26 @@ class PagedKVCache:
                                 dtype=dtype, device=device)
         self.free = list(range(num_pages - 1, -1, -1))  # pop() hands out page 0 first
         self.seqs: dict[int, _Seq] = {}
-        i32 = dict(dtype=torch.int32, device=device)
-        self._q_indptr = torch.zeros(max_batch + 1, **i32)
-        self._positions = torch.zeros(max_tokens, **i32)
-        self._slots = torch.zeros(max_tokens, **i32)
-        self._page_indptr = torch.zeros(max_batch + 1, **i32)
-        self._page_indices = torch.zeros(num_pages, **i32)
-        self._kv_len = torch.zeros(max_batch, **i32)
-        self._pinned = torch.zeros(2 * (max_batch + 1) + 2 * max_tokens + num_pages + max_batch,
-                                   dtype=torch.int32, pin_memory=torch.cuda.is_available())
+        # The forward tables live in one device buffer at fixed offsets (kernels
+        # captured in a graph keep their addresses), uploaded from a pinned
+        # staging buffer of the same layout in three small copies: the
+        # per-sequence tables with the positions, the slots, the page indices
+        # (each copy spans only what the forward uses).
+        sizes = (max_batch + 1, max_batch + 1, max_batch, max_tokens, max_tokens, num_pages)
+        self._tables_dev = torch.zeros(sum(sizes), dtype=torch.int32, device=device)
+        # two staging buffers used in turn: a forward waits only for the copy
+        # made from its buffer two forwards ago (an event), not for the stream
+        self._pinned = [torch.zeros(sum(sizes), dtype=torch.int32,
+                                    pin_memory=torch.cuda.is_available()) for _ in range(2)]
+        self._stage_events: list = [None, None]
+        self._stage = 0
+        self._table_offsets, views, off = [], [], 0
+        for k in sizes:
+            self._table_offsets.append(off)
+            views.append(self._tables_dev[off:off + k])
+            off += k
+        (self._q_indptr, self._page_indptr, self._kv_len, self._positions, self._slots,
+         self._page_indices) = views
         self.tables: ForwardTables | None = None
         self._decode_ws: torch.Tensor | None = None
         # decode attention's key bound for a captured forward (0: per forward)
@@ -91,7 +102,7 @@ class PagedKVCache:
         import attn_native
         need = attn_native.decode_workspace_bytes(batch, span)
         if self._decode_ws is None or self._decode_ws.numel() < need:
-            self._decode_ws = torch.empty(need, dtype=torch.uint8, device=self.data.device)
+            self._decode_ws = attn_native.decode_workspace(batch, span, self.data.device)
         return self._decode_ws
 
     def reserve_decode(self, batch: int, span: int) -> None:
@@ -162,20 +173,21 @@ class PagedKVCache:
             page_indices.extend(s.pages)
             page_indptr.append(len(page_indices))
             kv_len.append(s.length)
-        host = self._pinned
-        parts = [q_indptr, positions, slots, page_indptr, page_indices, kv_len]
-        dsts = [self._q_indptr, self._positions, self._slots, self._page_indptr,
-                self._page_indices, self._kv_len]
-        off = 0
-        for vals, dst in zip(parts, dsts):
-            k = len(vals)
-            if k:
-                host[off:off + k] = torch.tensor(vals, dtype=torch.int32)
-                dst[:k].copy_(host[off:off + k], non_blocking=True)
-            off += k
+        j = self._stage
+        if self._stage_events[j] is not None:
+            self._stage_events[j].synchronize()  # this buffer's previous copy is done
+        host, offs = self._pinned[j], self._table_offsets
+        parts = [q_indptr, page_indptr, kv_len, positions, slots, page_indices]
+        for vals, off in zip(parts, offs):
+            host[off:off + len(vals)] = torch.tensor(vals, dtype=torch.int32)
+        for a, b in ((0, offs[3] + n), (offs[4], offs[4] + n),
+                     (offs[5], offs[5] + len(page_indices))):
+            self._tables_dev[a:b].copy_(host[a:b], non_blocking=True)
         if self.data.is_cuda:
-            # the pinned staging is reused by the next forward: wait for these copies
-            torch.cuda.current_stream().synchronize()
+            ev = torch.cuda.Event()
+            ev.record()
+            self._stage_events[j] = ev
+            self._stage = j ^ 1
         self.tables = ForwardTables(
             batch=batch, num_tokens=n, max_q_len=max(append_lengths),
             max_kv_len=max(kv_len), q_indptr=self._q_indptr[:batch + 1],

@@ -101,17 +101,21 @@ class GPTOssForCausalLM(torch.nn.Module):
         h = self.model(input_embed, cache)
         return self._get_logits(h[:, -1:, :]).view(1, 1, -1)
 
-    def decode(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
-        """Logits [1, b, vocab] of one new token per sequence (model/transformer.py:121-126).
-
-        Up to 8 sequences: the final norm runs inside the unembedding GEMV."""
+    def decode_logits_bf16(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
+        """The unembedding's bf16 logits [b, vocab] of one new token per
+        sequence (``decode`` returns them as fp32).  Up to 8 sequences the
+        final norm runs inside the unembedding GEMV."""
         if input_embed.numel() // self.hidden_size > A.GEMV_MAX_TOKENS:
             h = self.model(input_embed, cache)
-            return self._get_logits(h).view(1, -1, self.config.vocab_size)
+            return self._logits_bf16(h)
         x = self.model.layers(input_embed, cache)
-        lg = A.gemv(x.reshape(-1, self.hidden_size), self.unembedding.weight,
-                    norm_w=self.model.norm.weight, eps=self.model.eps)
-        return lg.float().view(1, -1, self.config.vocab_size)
+        return A.gemv(x.reshape(-1, self.hidden_size), self.unembedding.weight,
+                      norm_w=self.model.norm.weight, eps=self.model.eps)
+
+    def decode(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
+        """Logits [1, b, vocab] of one new token per sequence (model/transformer.py:121-126)."""
+        return self.decode_logits_bf16(input_embed, cache).float().view(1, -1,
+                                                                        self.config.vocab_size)
 
     def extend(self, input_embed: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
         """Prefill of new tokens over a cached prefix (model/transformer.py:128-140)."""

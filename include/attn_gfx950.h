@@ -52,7 +52,10 @@ MOE_API int attn_qkv_rope_append(const uint16_t* qkv, const uint16_t* qkv_bias, 
                                  int64_t num_pages, uint16_t* q_out, moe_stream_t stream);
 
 /* Workspace of attn_decode for `batch` sequences attending to at most
- * max_span keys each (min(kv_len, window) for sliding layers). */
+ * max_span keys each (min(kv_len, window) for sliding layers).  Its first
+ * 32 x batch bytes are arrival counts that must be zero before the first call
+ * on the workspace; every call leaves them zero (zero the whole workspace
+ * once when it is allocated). */
 MOE_API size_t attn_decode_workspace_bytes(int64_t batch, int64_t max_span);
 
 /* Decode attention: one query token per sequence, q [batch, 64, 64] bf16 at

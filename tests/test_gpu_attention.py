@@ -136,7 +136,7 @@ def test_decode_attention(A, window):
     q = bf(rng.standard_normal((len(lengths), HQ, D)))
     sinks = bf(rng.standard_normal(HQ))
     span = max(min(L, window) if window else L for L in lengths)
-    ws = torch.empty(A.decode_workspace_bytes(len(lengths), span), dtype=torch.uint8, device="cuda")
+    ws = A.decode_workspace(len(lengths), span)
     out = torch.empty((len(lengths), HQ, D), dtype=torch.bfloat16, device="cuda")
     A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, span,
              window, SCALE, bf16_dev(sinks), out, ws)
@@ -146,10 +146,34 @@ def test_decode_attention(A, window):
         close(got[b:b + 1], AO.sink_scale(o, lse, sinks))
 
 
+def test_decode_attention_reused_workspace_and_large_bound(A):
+    """The last split of each (sequence, kv head) to finish merges the
+    group; its arrival counts live in the workspace and are left zero, so
+    calls in a row on one workspace agree bit for bit, also with a span bound
+    far above the lengths (the split count a captured graph fixes: splits past
+    a sequence's keys do nothing)."""
+    lengths = [1, 130, 1000, 4100]
+    seqs = PagedSeqs(35, lengths)
+    rng = np.random.default_rng(36)
+    q = bf16_dev(bf(rng.standard_normal((len(lengths), HQ, D))))
+    sinks = bf16_dev(bf(rng.standard_normal(HQ)))
+    outs = []
+    ws = A.decode_workspace(len(lengths), 40960)
+    for span in (4100, 40960, 4100):
+        for _ in range(2):
+            out = torch.empty((len(lengths), HQ, D), dtype=torch.bfloat16, device="cuda")
+            A.decode(q, seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, span, 0,
+                     SCALE, sinks, out, ws)
+            outs.append(host_bf16(out))
+        assert int(ws[:32 * len(lengths)].count_nonzero()) == 0   # arrival counts left zero
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
 def test_decode_span_too_small_is_nan(A):
     seqs = PagedSeqs(33, [300])
     q = bf(np.random.default_rng(34).standard_normal((1, HQ, D)))
-    ws = torch.empty(A.decode_workspace_bytes(1, 300), dtype=torch.uint8, device="cuda")
+    ws = A.decode_workspace(1, 300)
     out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device="cuda")
     A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, 200, 0,
              SCALE, bf16_dev(bf(np.zeros(HQ))), out, ws)

@@ -204,7 +204,8 @@ def test_many_tokens_per_expert(native):
                                           (32, 2880, 2880, 1, 37), (32, 2880, 2880, 64, 38),
                                           (32, 2880, 2880, 128, 39), (32, 2880, 64, 4096, 40),
                                           (128, 2880, 64, 1100, 41), (128, 256, 64, 4100, 42),
-                                          (40, 192, 64, 1500, 43)])
+                                          (40, 192, 64, 1500, 43), (32, 2880, 2880, 2, 44),
+                                          (128, 2880, 64, 2, 45), (128, 256, 64, 1, 46)])
 def test_block_internal_routing(native, E, H, I, n, seed):
     """The block's own router and grouping (logits kernel — VALU fp64 dots up
     to 1024 tokens, fp64 MFMA dots above — then one workgroup of top-k +
@@ -328,9 +329,11 @@ def block20b():
     return p, make_block(p)
 
 
-@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (5, 12), (32, 13), (33, 14), (520, 16)])
+@pytest.mark.parametrize("n,seed", [(1, 10), (64, 11), (2, 9), (3, 8), (5, 12), (32, 13), (33, 14),
+                                    (520, 16)])
 def test_block_20b_shape(native, block20b, n, seed):
-    """BASELINE configs 0 (n = 1) and 1 (n = 64) at full 20B shape, a ragged n,
+    """BASELINE configs 0 (n = 1) and 1 (n = 64) at full 20B shape, small
+    decode batches (2, 3 tokens), a ragged n,
     both sides of the decode launch's fused-combine limit (32 tokens: the
     launch sums the k rows itself; 33: the gating kernel does; the staged
     check compares the block with the gating kernel bit for bit), and 520
