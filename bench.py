@@ -150,11 +150,13 @@ def timed_steps(fn, steps: int, warmup: int) -> float:
 def staged_pass(blocks, xs, steps: int, stages, fused: bool, pieces_epilogue: bool) -> dict:
     """Per-stage HIP events on the launch stream.  A spin kernel is queued first
     so the host runs ahead of the GPU and the events time the kernels, not
-    gaps left by Python between launches."""
+    gaps left by Python between launches (a staged call costs the host about
+    a millisecond: seven C calls, their output tensors and fourteen events,
+    more than a one-token block takes on the GPU)."""
     import torch
     recs = []
     nw = len(blocks)
-    torch.cuda._sleep(int(2.4e9 * 0.4e-3 * steps))
+    torch.cuda._sleep(int(2.4e9 * 1.5e-3 * steps))
     for i in range(steps):
         ev = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for s in stages}

@@ -287,38 +287,91 @@ __device__ __forceinline__ float sink_factor(float lse, uint16_t sink) {
   return bf2f(f2bf((float)(1.0 / (1.0 + exp(-(double)z)))));
 }
 
-// Decode attention, merge: the group's 8 query heads of sequence b (thread
-// -> dim t % 64, heads t / 64 and t / 64 + 4) over the used splits (max,
-// rescaled sums in split order), then lse, the sink factor and the bf16
-// output.  The partials are read with device scope (written by other
-// workgroups).  `bad` (the attended range is empty or longer than the splits
-// cover: the caller's bound was too small) gives NaN outputs.
+// Decode attention, merge: the group's 8 query heads of sequence b over the
+// used splits (max, rescaled sums in split order), then lse, the sink factor
+// and the bf16 output.  The partials are read with device scope (written by
+// other workgroups), and every load is issued without waiting on another:
+// the maxima by 32 threads per head, then per tile of 32 splits the weights
+// exp(m_s - m) and the l_s by one thread each into LDS, and the o values by
+// the (dim, head) threads, eight loads in flight before their sums.  The
+// sums run in split order.  `bad` (the attended range is empty or longer
+// than the splits cover: the caller's bound was too small) gives NaN outputs.
+// Called by all 256 threads of the workgroup.
 __device__ void decode_merge_group(const float* part_o, const float* part_ml, int splits,
                                    int used, bool bad, int b, int hk, const uint16_t* sinks,
                                    uint16_t* out) {
-  const int d = threadIdx.x & 63;
+  constexpr int kTile = 32;
+  __shared__ float wgt[kGroup][kTile];   // exp(m_s - m) in [0, 1], or -1 for a skipped split
+  __shared__ float lval[kGroup][kTile];  // l_s
+  __shared__ float lsum[kGroup];
+  __shared__ float hmax[kGroup];
+  const int t = threadIdx.x;
+  const int d = t & 63;
+  if (bad) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      out[((size_t)b * kHq + hk * kGroup + (t >> 6) + 4 * j) * kD + d] = 0x7FC0;
+    return;
+  }
+  // maxima: thread (head t / 32, lane i = t % 32) over splits i, i + 32, ...
+  const int mh = t >> 5, mi = t & 31;
+  const size_t mbase = ((size_t)b * kHq + hk * kGroup + mh) * splits;
+  {
+    float m = -INFINITY;
+    for (int s = mi; s < used; s += kTile) m = fmaxf(m, load_dev(part_ml + (mbase + s) * 2));
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    if (mi == 0) {
+      hmax[mh] = m;
+      lsum[mh] = 0.0f;
+    }
+  }
+  float o[2] = {0.0f, 0.0f};
+  size_t obase[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    obase[j] = ((size_t)b * kHq + hk * kGroup + (t >> 6) + 4 * j) * splits;
+  for (int s0 = 0; s0 < used; s0 += kTile) {
+    const int nt = min(kTile, used - s0);
+    __syncthreads();  // hmax written; the previous tile's weights consumed
+    if (mi < nt) {
+      const float ms = load_dev(part_ml + (mbase + s0 + mi) * 2);
+      lval[mh][mi] = load_dev(part_ml + (mbase + s0 + mi) * 2 + 1);
+      wgt[mh][mi] = ms == -INFINITY ? -1.0f : __expf(ms - hmax[mh]);
+    }
+    __syncthreads();
+    if (mi == 0) {  // l in split order (one thread per head)
+      float l = lsum[mh];
+      for (int i = 0; i < nt; ++i) {
+        const float w = wgt[mh][i];
+        if (!(w < 0.0f)) l = fmaf(lval[mh][i], w, l);
+      }
+      lsum[mh] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = (t >> 6) + 4 * j;
+      for (int i0 = 0; i0 < nt; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = i0 + i < nt ? load_dev(part_o + (obase[j] + s0 + i0 + i) * kD + d) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float w = i0 + i < nt ? wgt[h][i0 + i] : -1.0f;
+          if (!(w < 0.0f)) o[j] = fmaf(v[i], w, o[j]);
+        }
+      }
+    }
+  }
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int h = hk * kGroup + (threadIdx.x >> 6) + 4 * j;
-    uint16_t* o_out = out + ((size_t)b * kHq + h) * kD + d;
-    if (bad) {
-      *o_out = 0x7FC0;
-      continue;
-    }
-    const size_t base = ((size_t)b * kHq + h) * splits;
-    float m = -INFINITY;
-    for (int s = 0; s < used; ++s) m = fmaxf(m, load_dev(part_ml + (base + s) * 2));
-    float l = 0.f, o = 0.f;
-    for (int s = 0; s < used; ++s) {
-      const float ms = load_dev(part_ml + (base + s) * 2);
-      if (ms == -INFINITY) continue;
-      const float f = __expf(ms - m);
-      l = fmaf(load_dev(part_ml + (base + s) * 2 + 1), f, l);
-      o = fmaf(load_dev(part_o + (base + s) * kD + d), f, o);
-    }
-    const float lse = m + __logf(l);
-    const float ob = bf2f(f2bf(o / l));
-    *o_out = f2bf(ob * sink_factor(lse, sinks[h]));
+    const int hl = (t >> 6) + 4 * j, h = hk * kGroup + hl;
+    const float l = lsum[hl];
+    const float lse = hmax[hl] + __logf(l);
+    const float ob = bf2f(f2bf(o[j] / l));
+    out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
   }
 }
 

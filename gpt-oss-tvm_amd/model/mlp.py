@@ -279,5 +279,5 @@ class MLPBlock(torch.nn.Module):
         rec("combine", 0)
         out = _native.gemv_gating(y.view(n, k, self.hidden_size), w, x2)
         rec("combine", 1)
-        return {"t": t, "idx": idx, "w": w, "perm": perm, "act": act, "y": y,
-                "out": out.reshape(b, seq_len, dim)}
+        return {"t": t, "idx": idx, "w": w, "perm": perm, "act": act, "act_pieces": act_pk,
+                "y": y, "out": out.reshape(b, seq_len, dim)}
