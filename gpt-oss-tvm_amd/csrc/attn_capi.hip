@@ -15,7 +15,7 @@ int attn_launch_qkv_rope_append(const void* qkv, const void* bias, int n, const 
                                 int num_pages, void* q_out, hipStream_t s);
 int attn_launch_decode(const void* q, int batch, const void* cache, const int* page_indptr,
                        const int* page_indices, int num_pages, const int* kv_len, int window,
-                       float sm_scale, const void* sinks, int splits, float* part_o,
+                       float sm_scale, const void* sinks, int splits, int cps, float* part_o,
                        float* part_ml, int* arrive, void* out, hipStream_t s);
 int attn_launch_prefill(const void* q, const int* q_indptr, int batch, int max_q_len,
                         const void* cache, const int* page_indptr, const int* page_indices,
@@ -40,7 +40,7 @@ int attn_launch_sample(const void* logits, int batch, int V, float temperature, 
 namespace {
 
 constexpr int64_t kHeadDim = 64, kQHeads = 64, kKvHeads = 8, kPage = 16;
-constexpr int64_t kDecChunk = 128;     // keys per decode workgroup
+constexpr int64_t kDecChunk = 128;     // keys per chunk of a decode workgroup
 constexpr int64_t kMaxTokens = 1 << 24;
 constexpr int64_t kMaxPages = ((int64_t)1 << 31) / kPage;
 
@@ -49,7 +49,17 @@ inline bool a4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 inline hipStream_t as_stream(moe_stream_t s) { return (hipStream_t)s; }
 inline int status(int launch_rc) { return launch_rc == 0 ? MOE_OK : MOE_ERR_LAUNCH; }
 
-int64_t decode_splits(int64_t max_span) { return (max_span + kDecChunk - 1) / kDecChunk; }
+// Chunks of 128 keys per decode workgroup: more with larger batches, where
+// there are workgroups enough (a workgroup's fixed costs, the page-table
+// reads before its first loads and the published partial after its last
+// chunk, then spread over more keys).  It depends on the batch only, so a
+// call's results do not depend on the span bound (a captured graph fixes the
+// bound at the pool's capacity).
+int64_t decode_cps(int64_t batch) { return batch >= 32 ? 8 : batch >= 8 ? 4 : batch >= 2 ? 2 : 1; }
+int64_t decode_splits(int64_t batch, int64_t max_span) {
+  const int64_t keys = kDecChunk * decode_cps(batch);
+  return (max_span + keys - 1) / keys;
+}
 
 }  // namespace
 
@@ -89,7 +99,7 @@ static size_t decode_counts_bytes(int64_t batch) {
 
 size_t attn_decode_workspace_bytes(int64_t batch, int64_t max_span) {
   if (batch <= 0 || max_span <= 0) return 0;
-  const size_t parts = (size_t)batch * kQHeads * (size_t)decode_splits(max_span);
+  const size_t parts = (size_t)batch * kQHeads * (size_t)decode_splits(batch, max_span);
   return decode_counts_bytes(batch) + parts * (kHeadDim + 2) * sizeof(float) + 256;
 }
 
@@ -106,14 +116,15 @@ int attn_decode(const uint16_t* q, int64_t batch, const void* kv_cache, int64_t 
       !a4(page_indices) || !a4(kv_len) || ((uintptr_t)sinks & 1u))
     return MOE_ERR_ALIGN;
   if (workspace_bytes < attn_decode_workspace_bytes(batch, max_span)) return MOE_ERR_WORKSPACE;
-  const int64_t splits = decode_splits(max_span);
+  const int64_t splits = decode_splits(batch, max_span);
   if (splits > 65535) return MOE_ERR_SHAPE;
   int* arrive = (int*)workspace;
   float* part_o = (float*)((char*)workspace + decode_counts_bytes(batch));
   float* part_ml = part_o + (size_t)batch * kQHeads * splits * kHeadDim;
   return status(attn_launch_decode(q, (int)batch, kv_cache, page_indptr, page_indices,
                                    (int)num_pages, kv_len, window, sm_scale, sinks, (int)splits,
-                                   part_o, part_ml, arrive, out, as_stream(stream)));
+                                   (int)decode_cps(batch), part_o, part_ml, arrive, out,
+                                   as_stream(stream)));
 }
 
 int attn_prefill(const uint16_t* q, const int32_t* q_indptr, int64_t batch, int64_t max_q_len,

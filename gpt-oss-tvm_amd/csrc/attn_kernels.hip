@@ -126,139 +126,230 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
 
 // ---------------------------------------------------------------------------
 // Decode attention, phase 1: workgroup (split s, kv head hk, sequence b)
-// takes keys [lo + 128 s, lo + 128 (s + 1)) of the sequence's attended range
-// [lo, kv_len) for the 8 query heads of hk, and writes the partial softmax
-// state of each head: m (max score), l (sum of exp(score - m)) and
-// o[64] = sum exp(score - m) v.  Scores in fp32 (q.k * sm_scale).  The
-// chunk's K and V rows are staged in LDS first (the chunk's page ids read
-// once, then 256 threads x 8 16-byte loads, all in flight), so the HBM
-// traffic is coalesced and no load waits behind another.
+// takes keys [lo + S s, lo + S (s + 1)) of the sequence's attended range
+// [lo, kv_len), S = 128 cps (cps chunks of 128 keys), for the 8 query heads of
+// hk, and writes the partial softmax state of each head: m (max score), l (sum
+// of exp(score - m)) and o[64] = sum exp(score - m) v.  The split's page ids
+// are read once; each chunk's K rows and V (transposed) are staged in LDS
+// from registers loaded while the previous chunk's products ran (256 threads
+// x 8 16-byte loads, all in flight), with an online softmax across chunks.
+// Both products run on v_mfma_f32_16x16x32_bf16, with the lane facts the
+// prefill kernel below relies on (operand row / column = lane % 16; result
+// element i of lane l = row 4 (l / 16) + i, column l % 16; A and B pair their
+// operand slots by position): wave w takes keys 32 w .. 32 w + 31 of a chunk,
+//  * S^T = K Q^T (A = 16 keys x 32 dims, B = 32 dims x 16 "queries": the 8
+//    heads, repeated): lane l holds S[head l % 16][key 32 w + 16 kk + 4 (l / 16)
+//    + i] for kk = 0, 1; scores in fp32 (times sm_scale), the chunk's maximum
+//    per head through LDS;
+//  * O^T = V^T P^T over the wave's 32 keys (P as two bf16 pieces, about 16
+//    bits, as in the prefill kernel): P's slot j of lane l carries the key
+//    lane l holds, V^T's slot j of lane l the same key from the transposed
+//    tile; at the end the four waves' partial o are summed in wave order.
 constexpr int kDecChunk = 128;
-constexpr int kDecKRow = kD + 8;  // padded K row (bf16)
+constexpr int kDecMaxCps = 8;
+constexpr int kDecKRow = kD + 8;         // padded K row (bf16)
+constexpr int kDecVRow = kDecChunk + 8;  // padded V^T row (bf16)
+
+// Sink scaling of attention.py:235-245: lse (natural log) -> s =
+// bf16(sigmoid(lse - sink)), out = bf16(bf16(o) * s).
+__device__ __forceinline__ float sink_factor(float lse, uint16_t sink) {
+  const float z = lse - bf2f(sink);
+  return bf2f(f2bf((float)(1.0 / (1.0 + exp(-(double)z)))));
+}
 
 __device__ void decode_merge_group(const float* part_o, const float* part_ml, int splits,
                                    int used, bool bad, int b, int hk, const uint16_t* sinks,
                                    uint16_t* out);
 
+__device__ __forceinline__ f32x4 dec_mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 __global__ __launch_bounds__(256) void decode_partial_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ cache,
     const int* __restrict__ page_indptr, const int* __restrict__ page_indices, int num_pages,
-    const int* __restrict__ kv_len, int window, float sm_scale, int splits,
+    const int* __restrict__ kv_len, int window, float sm_scale, int splits, int cps,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ arrive,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out) {
+  // K rows [key][dim]; after the last chunk, the waves' partial o [wave][head][dim]
   __shared__ __align__(16) uint16_t ks[kDecChunk * kDecKRow];
-  __shared__ __align__(16) uint16_t vs[kDecChunk * kD];
-  __shared__ float qs[kGroup][kD];
-  __shared__ float sc[kGroup][kDecChunk];
-  __shared__ float red[kGroup][2];
-  __shared__ int pid[kDecChunk / kPage + 1];
+  __shared__ __align__(16) uint16_t vt[kD * kDecVRow];  // V^T [dim][key]
+  __shared__ float red_m[4][16], red_l[4][16], hm[kGroup];
+  __shared__ int pid[kDecChunk * kDecMaxCps / kPage + 1];
   const int s = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x;
+  const int wave = t >> 6, lane = t & 63, r = lane & 15, g = lane >> 4;
   const int L = kv_len[b];
   const int lo = window > 0 ? max(0, L - window) : 0;
-  const int k0 = lo + s * kDecChunk;
-  const int nk = max(0, min(kDecChunk, L - k0));
+  const int skeys = kDecChunk * cps;
+  const int k0 = lo + s * skeys;
+  const int nks = max(0, min(skeys, L - k0));
   const size_t pidx = ((size_t)b * kHq + hk * kGroup) * splits + s;  // head h: + h * splits
-  // the splits holding keys: the first ceil(span / kDecChunk) (at most splits)
+  // the splits holding keys: the first ceil(span / skeys) (at most splits)
   const int span = L - lo;
-  const int used = min((span + kDecChunk - 1) / kDecChunk, splits);
+  const int used = min((span + skeys - 1) / skeys, splits);
   // a split past the attended range holds no keys and writes nothing (the
   // merge reads only the used splits); an empty range gives NaN outputs
-  if (nk == 0) {
+  if (nks == 0) {
     if (span <= 0 && s == 0)
       decode_merge_group(part_o, part_ml, splits, 0, true, b, hk, sinks, out);
     return;
   }
   const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
                        num_pages};
-  // the chunk spans at most 9 pages (it need not start on a page boundary)
-  const int pg0 = k0 / kPage;
-  if (t <= kDecChunk / kPage) pid[t] = pages.page_of(min((pg0 + t) * kPage, L - 1));
-  for (int i = t; i < kGroup * kD; i += 256)
-    qs[i / kD][i % kD] = bf2f(q[((size_t)b * kHq + hk * kGroup) * kD + i]);
-  __syncthreads();
+  // the split's pages (it need not start on a page boundary)
+  const int pg0 = k0 / kPage, npg = (k0 + nks - 1) / kPage - pg0 + 1;
+  for (int i = t; i < npg; i += 256) pid[i] = pages.page_of(min((pg0 + i) * kPage, L - 1));
+  // Q operand: head r % 8 of the group, dims 32 ks + 8 g .. + 7
+  bf16x8 qb[2];
   {
-    // 16-byte unit u: K units 0..1023 (key u / 8, part u % 8), V units 1024..2047;
-    // keys past the chunk repeat its last key (finite, not used)
-    u32x4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int u = t + 256 * j;
-      const int key = min((u & 1023) >> 3, nk - 1), part = u & 7;
-      const int pos = k0 + key;
-      v[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], u >> 10, hk, pos % kPage) +
-                             part * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int u = t + 256 * j;
-      const int key = (u & 1023) >> 3, part = u & 7;
-      if (u < 1024)
-        *(u32x4*)(ks + key * kDecKRow + part * 8) = v[j];
-      else
-        *(u32x4*)(vs + key * kD + part * 8) = v[j];
-    }
+    const u32x4* src = (const u32x4*)(q + ((size_t)b * kHq + hk * kGroup + (r & 7)) * kD);
+    qb[0] = moe::as_bf16x8(src[g]);
+    qb[1] = moe::as_bf16x8(src[4 + g]);
   }
   __syncthreads();
-  {
-    // scores: thread -> key t % 128, heads 4 (t / 128) .. + 3
-    const int kk = t & (kDecChunk - 1);
-    const int h0 = (t >> 7) * 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    const u32x4* kr = (const u32x4*)(ks + kk * kDecKRow);
+  // A chunk's loads: K 16-byte unit u = t + 256 j (key u / 8, part u % 8); V
+  // part t / 32 of keys 2 m, 2 m + 1, 64 + 2 m, 65 + 2 m (m = t % 32), written
+  // transposed as key pairs.  Keys past the chunk repeat its last key
+  // (finite; masked).
+  const int vpart = t >> 5, m2 = t & 31;
+  u32x4 kv[4], vv[4];
+  auto load_chunk = [&](int c) {
+    const int kc0 = k0 + c * kDecChunk, last = min(kDecChunk, nks - c * kDecChunk) - 1;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const u32x4 v = kr[c];
+    for (int j = 0; j < 4; ++j) {
+      const int u = t + 256 * j;
+      const int pos = kc0 + min(u >> 3, last);
+      kv[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], 0, hk, pos % kPage) +
+                              (u & 7) * 8);
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float e0 = __uint_as_float(v[j] << 16), e1 = __uint_as_float(v[j] & 0xFFFF0000u);
+    for (int j = 0; j < 4; ++j) {
+      const int pos = kc0 + min((j >> 1) * 64 + 2 * m2 + (j & 1), last);
+      vv[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], 1, hk, pos % kPage) +
+                              vpart * 8);
+    }
+  };
+  auto store_chunk = [&]() {
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
-          acc[h] = fmaf(e1, qs[h0 + h][c * 8 + 2 * j + 1], fmaf(e0, qs[h0 + h][c * 8 + 2 * j], acc[h]));
+    for (int j = 0; j < 4; ++j) {
+      const int u = t + 256 * j;
+      *(u32x4*)(ks + (u >> 3) * kDecKRow + (u & 7) * 8) = kv[j];
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t a0 = (vv[2 * h2][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        const uint32_t a1 = (vv[2 * h2 + 1][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        *(uint32_t*)(vt + (vpart * 8 + e) * kDecVRow + h2 * 64 + 2 * m2) = a0 | (a1 << 16);
+      }
+  };
+  load_chunk(0);
+  store_chunk();
+  __syncthreads();
+  const int nch = (nks + kDecChunk - 1) / kDecChunk;
+  float m_run = -INFINITY, l_run = 0.f;  // this lane's head r; l over its keys
+  f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nch; ++c) {
+    const int nkc = min(kDecChunk, nks - c * kDecChunk);
+    if (c + 1 < nch) load_chunk(c + 1);  // in flight during this chunk's products
+    // scores of the wave's 32 keys
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint16_t* kr = ks + (32 * wave + 16 * kk + r) * kDecKRow + 8 * g;
+      f32x4 st = dec_mfma(moe::as_bf16x8(*(const u32x4*)kr), qb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      st = dec_mfma(moe::as_bf16x8(*(const u32x4*)(kr + 32)), qb[1], st);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 32 * wave + 16 * kk + 4 * g + i;
+        sv[4 * kk + i] = key < nkc ? st[i] * sm_scale : -INFINITY;
+        mx = fmaxf(mx, sv[4 * kk + i]);
       }
     }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    if (g == 0) red_m[wave][r] = mx;
+    __syncthreads();
+    // the running maximum (every chunk holds a key, so mn is finite) and the
+    // rescaling of what the earlier chunks added
+    const float mn = fmaxf(m_run, fmaxf(fmaxf(red_m[0][r], red_m[1][r]),
+                                        fmaxf(red_m[2][r], red_m[3][r])));
+    const float alpha = m_run == -INFINITY ? 0.0f : __expf(m_run - mn);
+    m_run = mn;
+    l_run *= alpha;
+    bf16x8 ph, pl;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) sc[h0 + h][kk] = kk < nk ? acc[h] * sm_scale : -INFINITY;
-  }
-  __syncthreads();
-  {
-    // per head max and exp: wave w takes heads 2w, 2w + 1 (2 scores per lane)
-    const int w = t >> 6, lane = t & 63;
+    for (int j = 0; j < 8; ++j) {
+      const float p = sv[j] == -INFINITY ? 0.0f : __expf(sv[j] - mn);
+      l_run += p;
+      ph[j] = (__bf16)p;
+      pl[j] = (__bf16)(p - (float)ph[j]);
+    }
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int h = 2 * w + hh;
-      const float a = sc[h][lane], c = sc[h][lane + 64];
-      float m = fmaxf(a, c);
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vr = vt + (16 * dt + r) * kDecVRow + 32 * wave;
+      const uint2 vlo = *(const uint2*)(vr + 4 * g);
+      const uint2 vhi = *(const uint2*)(vr + 16 + 4 * g);
+      const bf16x8 va = moe::as_bf16x8(u32x4{vlo.x, vlo.y, vhi.x, vhi.y});
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-      const float pa = lane < nk ? __expf(a - m) : 0.0f;
-      const float pc = lane + 64 < nk ? __expf(c - m) : 0.0f;
-      sc[h][lane] = pa;
-      sc[h][lane + 64] = pc;
-      const float l = moe::wave_sum(pa + pc);
-      if (lane == 0) {
-        red[h][0] = m;
-        red[h][1] = l;
-      }
+      for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
+      o[dt] = dec_mfma(va, ph, o[dt]);
+      o[dt] = dec_mfma(va, pl, o[dt]);
+    }
+    __syncthreads();  // every wave is done with this chunk's tiles and maxima
+    if (c + 1 < nch) {
+      store_chunk();
+      __syncthreads();
     }
   }
+  // l over the wave's keys, then the waves' partial o in LDS (the K tile's
+  // space: every wave passed the last chunk's barrier)
+  l_run += __shfl_xor(l_run, 16, kWave);
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (g == 0) red_l[wave][r] = l_run;
+  if (wave == 0 && g == 0 && r < kGroup) hm[r] = m_run;
+  float* const obuf = (float*)ks;
+  if (r < kGroup) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) obuf[(wave * kGroup + r) * kD + 16 * dt + 4 * g + i] = o[dt][i];
+  }
   __syncthreads();
   {
-    // o[h][d]: thread -> dim t % 64, heads t / 64 and t / 64 + 4
+    // o[h][d]: thread -> dim t % 64, heads t / 64 and t / 64 + 4, waves summed in order
     const int d = t & 63, h0 = t >> 6;
     float o0 = 0.f, o1 = 0.f;
-#pragma unroll 8
-    for (int kk = 0; kk < nk; ++kk) {
-      const float v = bf2f(vs[kk * kD + d]);
-      o0 = fmaf(sc[h0][kk], v, o0);
-      o1 = fmaf(sc[h0 + 4][kk], v, o1);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      o0 += obuf[(w * kGroup + h0) * kD + d];
+      o1 += obuf[(w * kGroup + h0 + 4) * kD + d];
+    }
+    if (used == 1 && span <= splits * skeys) {
+      // the only split: the merge's arithmetic for one split (its weight is
+      // exp(0) = 1), done here without publishing the partial
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int hl = h0 + 4 * j, h = hk * kGroup + hl;
+        const float l = ((red_l[0][hl] + red_l[1][hl]) + red_l[2][hl]) + red_l[3][hl];
+        const float lse = hm[hl] + __logf(l);
+        const float ob = bf2f(f2bf((j == 0 ? o0 : o1) / l));
+        out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
+      }
+      return;
     }
     // device scope (sc1): the merge may run in a workgroup on another XCD
     store_dev(part_o + (pidx + (size_t)h0 * splits) * kD + d, o0);
     store_dev(part_o + (pidx + (size_t)(h0 + 4) * splits) * kD + d, o1);
     if (t < kGroup) {
-      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 0, red[t][0]);
-      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 1, red[t][1]);
+      const float lh = ((red_l[0][t] + red_l[1][t]) + red_l[2][t]) + red_l[3][t];
+      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 0, hm[t]);
+      store_dev(part_ml + (pidx + (size_t)t * splits) * 2 + 1, lh);
     }
   }
   // The last of the group's used splits to finish merges them: each wave's
@@ -276,16 +367,10 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   }
   __syncthreads();
   if (is_last)
-    decode_merge_group(part_o, part_ml, splits, used, span > splits * kDecChunk, b, hk, sinks,
+    decode_merge_group(part_o, part_ml, splits, used, span > splits * skeys, b, hk, sinks,
                        out);
 }
 
-// Sink scaling of attention.py:235-245: lse (natural log) -> s =
-// bf16(sigmoid(lse - sink)), out = bf16(bf16(o) * s).
-__device__ __forceinline__ float sink_factor(float lse, uint16_t sink) {
-  const float z = lse - bf2f(sink);
-  return bf2f(f2bf((float)(1.0 / (1.0 + exp(-(double)z)))));
-}
 
 // Decode attention, merge: the group's 8 query heads of sequence b over the
 // used splits (max, rescaled sums in split order), then lse, the sink factor
@@ -668,12 +753,12 @@ int attn_launch_qkv_rope_append(const void* qkv, const void* bias, int n, const 
 
 int attn_launch_decode(const void* q, int batch, const void* cache, const int* page_indptr,
                        const int* page_indices, int num_pages, const int* kv_len, int window,
-                       float sm_scale,
-                       const void* sinks, int splits, float* part_o, float* part_ml, int* arrive,
-                       void* out, hipStream_t s) {
+                       float sm_scale, const void* sinks, int splits, int cps, float* part_o,
+                       float* part_ml, int* arrive, void* out, hipStream_t s) {
+  if (cps < 1 || cps > attn::kDecMaxCps) return -6;
   hipLaunchKernelGGL(attn::decode_partial_kernel, dim3(splits, attn::kHkv, batch), dim3(256), 0, s,
                      (const uint16_t*)q, (const uint8_t*)cache, page_indptr, page_indices,
-                     num_pages, kv_len, window, sm_scale, splits, part_o, part_ml, arrive,
+                     num_pages, kv_len, window, sm_scale, splits, cps, part_o, part_ml, arrive,
                      (const uint16_t*)sinks, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }
