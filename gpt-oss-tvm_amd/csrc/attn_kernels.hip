@@ -498,8 +498,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t kt[2][kPfKeys * kKRow];
   __shared__ __align__(16) uint16_t vt[2][kD * kVRow];
-  const int b = blockIdx.x / tiles_per_seq, tile = blockIdx.x % tiles_per_seq;
-  const int hk = blockIdx.y;
+  // Workgroups are dispatched in linear order (x, then y): the linear index
+  // walks query tiles from the last, which under the causal mask attends to
+  // the most keys, so the longest tiles start first and the short ones fill
+  // the CUs they free (the tiles of one sequence otherwise ran as rounds each
+  // as long as its longest tile).
+  const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
+  const int per_tile = (int)(gridDim.x / tiles_per_seq) * kHkv;
+  const int tile = tiles_per_seq - 1 - lin / per_tile;
+  const int rest = lin % per_tile;
+  const int b = rest / kHkv, hk = rest % kHkv;
   const int qb = q_indptr[b], qn = q_indptr[b + 1] - qb;
   const int q0 = tile * kPfQ;
   if (q0 >= qn) return;
