@@ -46,10 +46,14 @@ __device__ __forceinline__ const uint16_t* kv_row(const uint8_t* cache, int page
 struct PageList {
   const int* ids;
   int count, pool;
-  __device__ __forceinline__ int page_of(int pos) const {
+  // the table entry of the page holding pos, and that entry clamped into the
+  // pool (split so that a loop can read entries ahead and clamp at use)
+  __device__ __forceinline__ int raw_page_of(int pos) const {
     const int i = min(pos / kPage, count - 1);
-    return min(max(ids[max(i, 0)], 0), pool - 1);
+    return ids[max(i, 0)];
   }
+  __device__ __forceinline__ int clamp(int id) const { return min(max(id, 0), pool - 1); }
+  __device__ __forceinline__ int page_of(int pos) const { return clamp(raw_page_of(pos)); }
 };
 
 // ---------------------------------------------------------------------------
@@ -531,6 +535,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     for (int ks = 0; ks < 2; ++ks) qa[qt][ks] = moe::as_bf16x8(src[ks * 4 + g]);
   }
   const float c2 = sm_scale * 1.4426950408889634f;  // scores in log2 units
+  const int x16 = (lane ^ 16) << 2, x32 = (lane ^ 32) << 2;  // ds_bpermute byte addresses
   f32x4 o[4][4];
   float m[4], l[4];
 #pragma unroll
@@ -549,27 +554,26 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   // key u / 8, 16-byte part u % 8); threads 256..511 hold V parts of keys 2m
   // and 2m + 1 (m = (t - 256) / 8), written transposed as key pairs.  Keys
   // past kv_len read the block's first key (finite, masked).
+  // The two keys a thread stages of a block: K threads keys u / 8 (u = t,
+  // t + 256), V threads keys 2m and 2m + 1.  Their page ids are read one
+  // block ahead (pg), so a block's loads never wait on the page table.
+  auto key_of = [&](int kb0, int j) {
+    const int key = t < 256 ? ((t + 256 * j) >> 3) : 2 * ((t - 256) >> 3) + j;
+    return kb0 + key < L ? kb0 + key : kb0;
+  };
+  int pg[2];
+  auto fetch_pages = [&](int kb0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pg[j] = pages.raw_page_of(key_of(kb0, j));
+  };
   u32x4 sr0, sr1;
   auto load = [&](int kb0) {
-    if (t < 256) {
+    const int kv = t < 256 ? 0 : 1, part = t & 7;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int u = t + 256 * j, key = u >> 3, part = u & 7;
-        const int pos = kb0 + key < L ? kb0 + key : kb0;
-        const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), 0, hk, pos % kPage) +
-                                        part * 8);
-        if (j == 0) sr0 = v; else sr1 = v;
-      }
-    } else {
-      const int tv = t - 256, m2 = tv >> 3, part = tv & 7;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int key = 2 * m2 + j;
-        const int pos = kb0 + key < L ? kb0 + key : kb0;
-        const u32x4 v = *(const u32x4*)(kv_row(cache, pages.page_of(pos), 1, hk, pos % kPage) +
-                                        part * 8);
-        if (j == 0) sr0 = v; else sr1 = v;
-      }
+    for (int j = 0; j < 2; ++j) {
+      const int pos = key_of(kb0, j);
+      const u32x4 v = *(const u32x4*)(kv_row(cache, pages.clamp(pg[j]), kv, hk, pos % kPage) + part * 8);
+      if (j == 0) sr0 = v; else sr1 = v;
     }
   };
   auto store = [&](int buf) {
@@ -591,14 +595,22 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   };
 
   if (kfirst <= kmax) {
+    fetch_pages(kfirst);
     load(kfirst);
+    if (kfirst + kPfKeys <= kmax) fetch_pages(kfirst + kPfKeys);
     store(0);
   }
+  // every load before the loop (Q, the first block, the next page ids) done:
+  // inside the loop the compiler then waits only for the block prefetch
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   int buf = 0;
   for (int kb0 = kfirst; kb0 <= kmax; kb0 += kPfKeys) {
     const bool more = kb0 + kPfKeys <= kmax;
-    if (more) load(kb0 + kPfKeys);  // in flight during this block's MFMAs
+    if (more) {
+      load(kb0 + kPfKeys);  // in flight during this block's MFMAs
+      if (kb0 + 2 * kPfKeys <= kmax) fetch_pages(kb0 + 2 * kPfKeys);
+    }
     bf16x8 ka[4][2];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
@@ -627,49 +639,72 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         st[kk] = mfma_bf16(ka[kk][0], qa[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
         st[kk] = mfma_bf16(ka[kk][1], qa[qt][1], st[kk]);
       }
-      // mask: key kb0 + 16 kk + 4 g + i for the query at position qpos
-      const int qpos = qpos0 + r;
-      float sv[16];
+      // mask: key kb0 + 16 kk + 4 g + i for the query at position qpos; a
+      // block that every row of the subtile sees whole (all blocks of a
+      // causal row but its diagonal one) skips it
+      const bool whole = kb0 + kPfKeys - 1 <= qpos0 && kb0 + kPfKeys <= L &&
+                         (window <= 0 || kb0 >= qpos0 + 15 - window + 1);
+      if (!whole) {
+        const int qpos = qpos0 + r;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb0 + kk * 16 + 4 * g + i;
+            const bool ok = key <= qpos && key < L && (window <= 0 || key >= qpos - window + 1);
+            if (!ok) st[kk][i] = -INFINITY;
+          }
+      }
+      // the row maximum of the raw scores: scaling by c2 > 0 keeps the order
       float bm = -INFINITY;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb0 + kk * 16 + 4 * g + i;
-          const bool ok = key <= qpos && key < L && (window <= 0 || key >= qpos - window + 1);
-          sv[kk * 4 + i] = ok ? st[kk][i] * c2 : -INFINITY;
-          bm = fmaxf(bm, sv[kk * 4 + i]);
-        }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-      const float mn = fmaxf(m[qt], bm);
-      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[qt] - mn);
+        for (int i = 0; i < 4; ++i) bm = fmaxf(bm, st[kk][i]);
+      bm = fmaxf(bm, __int_as_float(__builtin_amdgcn_ds_bpermute(x16, __float_as_int(bm))));
+      bm = fmaxf(bm, __int_as_float(__builtin_amdgcn_ds_bpermute(x32, __float_as_int(bm))));
+      const float mn = fmaxf(m[qt], bm * c2);
+      // alpha = 2^(m - mn) is exactly 1 for a row whose maximum did not grow:
+      // the rescale runs only when some row's did
+      if (__any(mn > m[qt])) {
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[qt][dt][i] *= alpha;
+        l[qt] *= alpha;
+      }
       m[qt] = mn;
+      // p = 2^(s c2 - mn); masked scores (-inf) give 0, also in a row that has
+      // seen no key yet (mn = -inf)
+      const float mneg = mn == -INFINITY ? 0.0f : -mn;
       float ps = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[qt][dt][i] *= alpha;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         // P enters the MFMA as two bf16 pieces, p = hi + lo to about 16 bits,
-        // so the products keep the fp32 probabilities' precision
-        bf16x8 ph, pl;
+        // so the products keep the fp32 probabilities' precision: hi = p
+        // truncated to bf16 (its top 16 bits), lo = bf16(p - hi) (the
+        // difference is exact in fp32)
+        uint32_t pb[8];
+        bf16x8 pl;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float sj = sv[s2 * 8 + j];
-          const float p = sj == -INFINITY ? 0.0f : exp2f(sj - mn);
+          const int kk = s2 * 2 + (j >> 2), i = j & 3;
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[kk][i], c2, mneg));
           ps += p;
-          ph[j] = (__bf16)p;
-          pl[j] = (__bf16)(p - (float)ph[j]);
+          pb[j] = __float_as_uint(p);
+          pl[j] = (__bf16)(p - __uint_as_float(pb[j] & 0xFFFF0000u));
         }
+        const bf16x8 ph = moe::as_bf16x8(u32x4{
+            __builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u), __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+            __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u), __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)});
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           o[qt][dt] = mfma_bf16(va[s2][dt], ph, o[qt][dt]);
           o[qt][dt] = mfma_bf16(va[s2][dt], pl, o[qt][dt]);
         }
       }
-      l[qt] = l[qt] * alpha + ps;
+      l[qt] += ps;
     }
     if (more) store(buf ^ 1);
     __syncthreads();

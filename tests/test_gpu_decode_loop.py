@@ -113,6 +113,7 @@ class _Replay:
     def __init__(self, eng, mp: AO.ModelParams):
         self.mp = mp
         self.io = {}
+        self.seen = {}      # (layer, kind) -> (GPU rows, oracle rows) of the run so far
         blocks = eng.model.model.block
         for i, blk in enumerate(blocks):
             for kind in ("attn", "mlp"):
@@ -127,6 +128,22 @@ class _Replay:
             self.io[(i, kind)] = (host_bf16(args[0].reshape(-1, H)), host_bf16(out.reshape(-1, H)))
         return f
 
+    def _bar(self, i, kind, got, ref, what):
+        """The block bar (max relative error 1e-2, MAE 1e-3) over the rows of
+        the run so far.  A decode step adds one row, too few values for a
+        max-normalised error on its own: two bf16 ulps in the row's largest
+        binade (0.25 against a maximum of 23.25) already exceed 1e-2, and the
+        chain of bf16 roundings (expert output, weighted sum, residual) gives
+        that from fp32 sums that differ in their last bits.  The block tests
+        apply the same bar over a sample of tokens."""
+        g0, r0 = self.seen.get((i, kind), (got[:0], ref[:0]))
+        g, r = np.concatenate([g0, got]), np.concatenate([r0, ref])
+        self.seen[(i, kind)] = (g, r)
+        m = O.compare_outputs(g, r)
+        assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, (what, i, kind, m)
+        m = O.compare_outputs(got, ref)                   # this step's rows alone
+        assert m["mae"] <= 1e-3, (what, i, kind, m)
+
     def check(self, logits_f32, what):
         for i, (ap, bp) in enumerate(self.mp.layers):
             x_in, got = self.io[(i, "attn")]
@@ -134,18 +151,20 @@ class _Replay:
                                               AO.SLIDING_WINDOW if i % 2 == 0 else 0)
             self.kc[i] = np.concatenate([self.kc[i], k])
             self.vc[i] = np.concatenate([self.vc[i], v])
-            m = O.compare_outputs(got, ref)
-            assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, (what, i, "attn", m)
+            self._bar(i, "attn", got, ref, what)
             x_in, got = self.io[(i, "mlp")]
-            tr = O.block_forward(x_in, bp)
-            m = O.compare_outputs(got, tr.out)
-            assert m["max_rel"] <= 1e-2 and m["mae"] <= 1e-3, (what, i, "mlp", m)
+            self._bar(i, "mlp", got, O.block_forward(x_in, bp).out, what)
         last_out = self.io[(len(self.mp.layers) - 1, "mlp")][1]
         h = O.rms_norm(last_out[-1:], self.mp.norm_w)   # the final norm (bit-exact kernels)
         own = AO.bf16_to_f32(AO.linear(h, self.mp.unembedding, None))[-1]
         d = O.compare_outputs(O.f32_to_bf16(logits_f32), O.f32_to_bf16(own))
-        ulp = np.spacing(np.abs(own).astype(np.float32)) * 2 ** 16     # one bf16 ulp
-        assert d["frac_diff"] <= 0.01 and np.all(np.abs(logits_f32 - own) <= ulp), (what, d)
+        # one bf16 ulp of each logit, or for a logit near zero after
+        # cancellation 2^-16 of the largest (fp32 summation order alone moves
+        # such a logit by several of its own ulps)
+        ulp = np.spacing(np.abs(own).astype(np.float32)) * 2 ** 16
+        floor = np.abs(own).max() * 2.0 ** -16
+        assert d["frac_diff"] <= 0.01 and np.all(np.abs(logits_f32 - own) <= np.maximum(ulp, floor)), \
+            (what, d)
 
 
 @pytest.fixture(scope="module")
