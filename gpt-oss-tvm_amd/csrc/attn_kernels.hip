@@ -467,11 +467,13 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
 // ---------------------------------------------------------------------------
 // Prefill / extend attention on v_mfma_f32_16x16x32_bf16.
 //
-// Workgroup = (query tile of 64 rows of one sequence, kv head hk): 8 waves,
-// wave w = query head 8 hk + w, so the 8 heads of a GQA group share each
-// key/value block staged in LDS.  Keys in blocks of 64 (four pages), double
-// buffered: the next block's global loads are in flight while the current
-// block's MFMAs run, one barrier per block.
+// Workgroup = (query tile of 64 rows of one sequence, kv head hk, half h of
+// its GQA group): 4 waves, wave w = query head 8 hk + 4 h + w, so 4 heads share
+// each key/value block staged in LDS.  At about 240 VGPRs a SIMD holds two
+// waves: two independent workgroups per CU, whose barriers and phases do not
+// line up, rather than one of 8 waves.  Keys in blocks of 64 (four pages),
+// double buffered: the next block's global loads are in flight while the
+// current block's MFMAs run, one barrier per block.
 //
 // The products are arranged so that only two facts of the MFMA's lane layout
 // matter: operand row (A) / column (B) = lane % 16, and result element i of
@@ -489,12 +491,25 @@ constexpr int kPfQ = 64;              // query rows per wave
 constexpr int kPfKeys = 64;           // keys per block
 constexpr int kKRow = kD + 8;         // K tile row (bf16), padded
 constexpr int kVRow = kPfKeys + 8;    // V^T tile row (bf16), padded
+constexpr int kPfWaves = 4;           // waves (query heads) per workgroup
+constexpr float kPfSlack = 8.0f;      // log2 headroom of the lazy softmax rescale
+constexpr int kPfHalves = kGroup / kPfWaves;  // workgroups per GQA group
+
+// max of x over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows) in
+// registers: swapping x with itself, v_permlane32_swap returns x of lanes
+// l & 31 and l | 32, v_permlane16_swap x of rows 2 (l / 32) and 2 (l / 32) + 1
+__device__ __forceinline__ float group_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(512) void prefill_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(
     const uint16_t* __restrict__ q, const int* __restrict__ q_indptr,
     const uint8_t* __restrict__ cache, const int* __restrict__ page_indptr,
     const int* __restrict__ page_indices, int num_pages, const int* __restrict__ kv_len,
@@ -506,12 +521,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   // walks query tiles from the last, which under the causal mask attends to
   // the most keys, so the longest tiles start first and the short ones fill
   // the CUs they free (the tiles of one sequence otherwise ran as rounds each
-  // as long as its longest tile).
+  // as long as its longest tile).  Within a tile: (sequence, half, kv head),
+  // so the two halves of a kv head's group are 8 workgroups apart and share
+  // an XCD (workgroups go round-robin over the 8 XCDs) and its L2.
   const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
-  const int per_tile = (int)(gridDim.x / tiles_per_seq) * kHkv;
+  const int per_tile = (int)(gridDim.x / tiles_per_seq) * kPfHalves * kHkv;
   const int tile = tiles_per_seq - 1 - lin / per_tile;
   const int rest = lin % per_tile;
-  const int b = rest / kHkv, hk = rest % kHkv;
+  const int b = rest / (kPfHalves * kHkv), half = rest / kHkv % kPfHalves, hk = rest % kHkv;
   const int qb = q_indptr[b], qn = q_indptr[b + 1] - qb;
   const int q0 = tile * kPfQ;
   if (q0 >= qn) return;
@@ -520,7 +537,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   const int t = threadIdx.x;
   const int wave = t >> 6, lane = t & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int head = hk * kGroup + wave;
+  const int head = hk * kGroup + half * kPfWaves + wave;
   const PageList pages{page_indices + page_indptr[b], page_indptr[b + 1] - page_indptr[b],
                        num_pages};
 
@@ -535,7 +552,6 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     for (int ks = 0; ks < 2; ++ks) qa[qt][ks] = moe::as_bf16x8(src[ks * 4 + g]);
   }
   const float c2 = sm_scale * 1.4426950408889634f;  // scores in log2 units
-  const int x16 = (lane ^ 16) << 2, x32 = (lane ^ 32) << 2;  // ds_bpermute byte addresses
   f32x4 o[4][4];
   float m[4], l[4];
 #pragma unroll
@@ -550,47 +566,42 @@ __global__ __launch_bounds__(512) void prefill_kernel(
   const int kmin = window > 0 ? max(0, P + q0 - window + 1) : 0;  // first key any row sees
   const int kfirst = kmin / kPfKeys * kPfKeys;
 
-  // Staging: threads 0..255 hold K units (u = t, t + 256 of the block's 512:
-  // key u / 8, 16-byte part u % 8); threads 256..511 hold V parts of keys 2m
-  // and 2m + 1 (m = (t - 256) / 8), written transposed as key pairs.  Keys
-  // past kv_len read the block's first key (finite, masked).
-  // The two keys a thread stages of a block: K threads keys u / 8 (u = t,
-  // t + 256), V threads keys 2m and 2m + 1.  Their page ids are read one
-  // block ahead (pg), so a block's loads never wait on the page table.
-  auto key_of = [&](int kb0, int j) {
-    const int key = t < 256 ? ((t + 256 * j) >> 3) : 2 * ((t - 256) >> 3) + j;
-    return kb0 + key < L ? kb0 + key : kb0;
-  };
-  int pg[2];
+  // Staging, 16-byte part t % 8 of four keys per thread (m = t / 8): K rows
+  // of keys m and m + 32 (j = 0, 1), V rows of keys 2m and 2m + 1 (j = 2, 3),
+  // the V pair written transposed as key pairs.  Keys past kv_len read the
+  // last key (finite, masked).  A block spans four pages, the same
+  // for every lane: their ids are scalar loads issued one block ahead (pid),
+  // each lane selecting the page of its key.
+  const int m8 = t >> 3, part = t & 7;
+  int pid[4];
   auto fetch_pages = [&](int kb0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) pg[j] = pages.raw_page_of(key_of(kb0, j));
+    for (int j = 0; j < 4; ++j) pid[j] = pages.ids[max(min(kb0 / kPage + j, pages.count - 1), 0)];
   };
-  u32x4 sr0, sr1;
+  u32x4 sr[4];
   auto load = [&](int kb0) {
-    const int kv = t < 256 ? 0 : 1, part = t & 7;
+    const int lim = L - 1 - kb0;  // keys past kv_len read key lim (finite, masked)
+    int page[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int pos = key_of(kb0, j);
-      const u32x4 v = *(const u32x4*)(kv_row(cache, pages.clamp(pg[j]), kv, hk, pos % kPage) + part * 8);
-      if (j == 0) sr0 = v; else sr1 = v;
+    for (int j = 0; j < 4; ++j) page[j] = pages.clamp(pid[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = min(j < 2 ? m8 + 32 * j : 2 * m8 + (j - 2), lim);
+      const int jp = key / kPage;
+      const int lo = (jp & 1) ? page[1] : page[0];
+      const int hi = (jp & 1) ? page[3] : page[2];
+      sr[j] = *(const u32x4*)(kv_row(cache, (jp & 2) ? hi : lo, j >> 1, hk, key % kPage) +
+                              part * 8);
     }
   };
   auto store = [&](int buf) {
-    if (t < 256) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int u = t + 256 * j, key = u >> 3, part = u & 7;
-        *(u32x4*)(kt[buf] + key * kKRow + part * 8) = j == 0 ? sr0 : sr1;
-      }
-    } else {
-      const int tv = t - 256, m2 = tv >> 3, part = tv & 7;
+    for (int j = 0; j < 2; ++j) *(u32x4*)(kt[buf] + (m8 + 32 * j) * kKRow + part * 8) = sr[j];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t a0 = (sr0[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        const uint32_t a1 = (sr1[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        *(uint32_t*)(vt[buf] + (part * 8 + e) * kVRow + 2 * m2) = a0 | (a1 << 16);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t a0 = (sr[2][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      const uint32_t a1 = (sr[3][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      *(uint32_t*)(vt[buf] + (part * 8 + e) * kVRow + 2 * m8) = a0 | (a1 << 16);
     }
   };
 
@@ -628,11 +639,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         const uint2 hi = *(const uint2*)(vr + 16 + 4 * g);
         va[s2][dt] = moe::as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
       }
-#pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
+    // One 16-row subtile against the block: a subtile whose rows see none of
+    // the block is skipped, one that does not see it whole is masked.
+    auto subtile = [&](int qt) {
       const int qpos0 = P + q0 + qt * 16;  // this subtile's positions: qpos0 .. qpos0 + 15
       // every key of the block masked for all 16 queries: nothing to add
-      if (qpos0 + 15 < kb0 || (window > 0 && qpos0 - window + 1 > kb0 + kPfKeys - 1)) continue;
+      if (qpos0 + 15 < kb0 || (window > 0 && qpos0 - window + 1 > kb0 + kPfKeys - 1)) return;
       f32x4 st[4];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -652,7 +664,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
           for (int i = 0; i < 4; ++i) {
             const int key = kb0 + kk * 16 + 4 * g + i;
             const bool ok = key <= qpos && key < L && (window <= 0 || key >= qpos - window + 1);
-            if (!ok) st[kk][i] = -INFINITY;
+            st[kk][i] = ok ? st[kk][i] : -INFINITY;
           }
       }
       // the row maximum of the raw scores: scaling by c2 > 0 keeps the order
@@ -661,23 +673,25 @@ __global__ __launch_bounds__(512) void prefill_kernel(
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) bm = fmaxf(bm, st[kk][i]);
-      bm = fmaxf(bm, __int_as_float(__builtin_amdgcn_ds_bpermute(x16, __float_as_int(bm))));
-      bm = fmaxf(bm, __int_as_float(__builtin_amdgcn_ds_bpermute(x32, __float_as_int(bm))));
+      bm = group_max(bm);
+      // The reference point m of a row moves to the new maximum only when some
+      // row's maximum exceeds its m by more than kPfSlack (log2 units): until
+      // then p = 2^(s c2 - m) stays below 2^kPfSlack, and o and l carry the
+      // same factor, so o / l and the lse m + log2(l) are unchanged.  The
+      // rescale then runs on the first blocks of a row and seldom after.
       const float mn = fmaxf(m[qt], bm * c2);
-      // alpha = 2^(m - mn) is exactly 1 for a row whose maximum did not grow:
-      // the rescale runs only when some row's did
-      if (__any(mn > m[qt])) {
+      if (__any(mn > m[qt] + kPfSlack)) {
         const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[qt][dt][i] *= alpha;
         l[qt] *= alpha;
+        m[qt] = mn;
       }
-      m[qt] = mn;
-      // p = 2^(s c2 - mn); masked scores (-inf) give 0, also in a row that has
-      // seen no key yet (mn = -inf)
-      const float mneg = mn == -INFINITY ? 0.0f : -mn;
+      // p = 2^(s c2 - m); masked scores (-inf) give 0, also in a row that has
+      // seen no key yet (m = -inf)
+      const float mneg = m[qt] == -INFINITY ? 0.0f : -m[qt];
       float ps = 0.f;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
@@ -705,7 +719,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         }
       }
       l[qt] += ps;
-    }
+    };
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) subtile(qt);
     if (more) store(buf ^ 1);
     __syncthreads();
     buf ^= 1;
@@ -811,7 +827,8 @@ int attn_launch_prefill(const void* q, const int* q_indptr, int batch, int max_q
                         int num_pages, const int* kv_len, int window, float sm_scale,
                         const void* sinks, void* out, hipStream_t s) {
   const int tiles = (max_q_len + attn::kPfQ - 1) / attn::kPfQ;
-  hipLaunchKernelGGL(attn::prefill_kernel, dim3(tiles * batch, attn::kHkv), dim3(512), 0, s,
+  hipLaunchKernelGGL(attn::prefill_kernel, dim3(tiles * batch, attn::kHkv * attn::kPfHalves),
+                     dim3(64 * attn::kPfWaves), 0, s,
                      (const uint16_t*)q, q_indptr, (const uint8_t*)cache, page_indptr, page_indices,
                      num_pages, kv_len, window, sm_scale, (const uint16_t*)sinks, tiles,
                      (uint16_t*)out);
