@@ -484,9 +484,11 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
 //    key subblock kk holds S[query l % 16][key 16 kk + 4 (l / 16) + i].
 //  * O^T += V^T P^T per 32 keys (A = 16 dims x 32 keys, B = 32 keys x 16
 //    queries, P as two bf16 pieces): P's operand slot j of lane l carries key
-//    4 (l / 16) + j (j < 4) or 16 + 4 (l / 16) + j - 4 (j >= 4) -- exactly the
+//    4 (l / 16) + j / 2 (j even) or 16 + 4 (l / 16) + (j - 1) / 2 (j odd) --
 //    scores lane l holds -- and V^T's slot j of lane l carries the same key,
-//    read from a transposed LDS tile.
+//    read from a transposed LDS tile whose 32-key halves are interleaved
+//    (position 2i key i, 2i + 1 key i + 16), so that a lane's 8 keys are one
+//    16-byte read.
 constexpr int kPfQ = 64;              // query rows per wave
 constexpr int kPfKeys = 64;           // keys per block
 constexpr int kKRow = kD + 8;         // K tile row (bf16), padded
@@ -566,42 +568,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int kmin = window > 0 ? max(0, P + q0 - window + 1) : 0;  // first key any row sees
   const int kfirst = kmin / kPfKeys * kPfKeys;
 
-  // Staging, 16-byte part t % 8 of four keys per thread (m = t / 8): K rows
-  // of keys m and m + 32 (j = 0, 1), V rows of keys 2m and 2m + 1 (j = 2, 3),
-  // the V pair written transposed as key pairs.  Keys past kv_len read the
-  // last key (finite, masked).  A block spans four pages, the same
-  // for every lane: their ids are scalar loads issued one block ahead (pid),
-  // each lane selecting the page of its key.
-  const int m8 = t >> 3, part = t & 7;
+  // Staging: load j brings page j of the block (keys 16 j .. 16 j + 15),
+  // threads 0..127 its K rows, threads 128..255 its V rows, 16-byte part
+  // t % 8 of key 16 j + c (c = (t % 128) / 8).  A load's page is the same for
+  // every lane: a scalar base (the page ids are scalar loads issued one block
+  // ahead, pid) plus a fixed lane offset.  V is written transposed, each
+  // 32-key half interleaved: position 2i holds key i, 2i + 1 key i + 16, the
+  // pair (loads 2h, 2h + 1) in one 32-bit store.  In a block that runs past
+  // kv_len, keys beyond it read key L - 1 (finite, masked).
+  const int kvsel = t >> 7, c = (t & 127) >> 3, part = t & 7;
+  const unsigned lane_base = (unsigned)((kvsel * kHkv + hk) * kHeadBlock) + part * 16;
+  const unsigned lane_off = lane_base + c * (kD * 2);
+  // page list index clamped to the page holding key L - 1: a page of the
+  // block wholly past kv_len resolves to that page
+  const int last_page = min(pages.count - 1, (L - 1) / kPage);
   int pid[4];
   auto fetch_pages = [&](int kb0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pid[j] = pages.ids[max(min(kb0 / kPage + j, pages.count - 1), 0)];
+    for (int j = 0; j < 4; ++j) pid[j] = pages.ids[max(min(kb0 / kPage + j, last_page), 0)];
   };
   u32x4 sr[4];
   auto load = [&](int kb0) {
-    const int lim = L - 1 - kb0;  // keys past kv_len read key lim (finite, masked)
-    int page[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) page[j] = pages.clamp(pid[j]);
+    const unsigned lim = (unsigned)(L - 1 - kb0);  // the block starts before kv_len
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int key = min(j < 2 ? m8 + 32 * j : 2 * m8 + (j - 2), lim);
-      const int jp = key / kPage;
-      const int lo = (jp & 1) ? page[1] : page[0];
-      const int hi = (jp & 1) ? page[3] : page[2];
-      sr[j] = *(const u32x4*)(kv_row(cache, (jp & 2) ? hi : lo, j >> 1, hk, key % kPage) +
-                              part * 8);
+      unsigned off = lane_off;
+      if (lim < (unsigned)(kPfKeys - 1)) {  // keys past L - 1 read key L - 1
+        const unsigned pj = min((unsigned)j, lim / kPage);
+        off = lane_base + (min((unsigned)(kPage * j + c), lim) - kPage * pj) * (kD * 2);
+      }
+      const uint8_t* pbase = cache + (size_t)(unsigned)pages.clamp(pid[j]) * kPageBytes;
+      sr[j] = *(const u32x4*)(pbase + off);
     }
   };
   auto store = [&](int buf) {
+    if (kvsel == 0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) *(u32x4*)(kt[buf] + (m8 + 32 * j) * kKRow + part * 8) = sr[j];
+      for (int j = 0; j < 4; ++j) *(u32x4*)(kt[buf] + (kPage * j + c) * kKRow + part * 8) = sr[j];
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t a0 = (sr[2][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      const uint32_t a1 = (sr[3][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      *(uint32_t*)(vt[buf] + (part * 8 + e) * kVRow + 2 * m8) = a0 | (a1 << 16);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t a0 = (sr[2 * h][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          const uint32_t a1 = (sr[2 * h + 1][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          *(uint32_t*)(vt[buf] + (part * 8 + e) * kVRow + 32 * h + 2 * c) = a0 | (a1 << 16);
+        }
     }
   };
 
@@ -629,16 +641,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int ks = 0; ks < 2; ++ks)
         ka[kk][ks] =
             moe::as_bf16x8(*(const u32x4*)(kt[buf] + (kk * 16 + r) * kKRow + ks * 32 + g * 8));
+    // V^T operand: positions 8g .. 8g + 7 of the half, keys 4g + i (slots 2i)
+    // and 16 + 4g + i (slots 2i + 1)
     bf16x8 va[2][4];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const uint16_t* vr = vt[buf] + (dt * 16 + r) * kVRow + s2 * 32;
-        const uint2 lo = *(const uint2*)(vr + 4 * g);
-        const uint2 hi = *(const uint2*)(vr + 16 + 4 * g);
-        va[s2][dt] = moe::as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-      }
+      for (int dt = 0; dt < 4; ++dt)
+        va[s2][dt] = moe::as_bf16x8(*(const u32x4*)(vt[buf] + (dt * 16 + r) * kVRow + s2 * 32 + 8 * g));
     // One 16-row subtile against the block: a subtile whose rows see none of
     // the block is skipped, one that does not see it whole is masked.
     auto subtile = [&](int qt) {
@@ -703,7 +713,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         bf16x8 pl;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int kk = s2 * 2 + (j >> 2), i = j & 3;
+          const int kk = s2 * 2 + (j & 1), i = j >> 1;  // the key V^T's slot j holds
           const float p = __builtin_amdgcn_exp2f(fmaf(st[kk][i], c2, mneg));
           ps += p;
           pb[j] = __float_as_uint(p);
