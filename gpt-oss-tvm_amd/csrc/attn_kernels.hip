@@ -519,6 +519,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t kt[2][kPfKeys * kKRow];
   __shared__ __align__(16) uint16_t vt[2][kD * kVRow];
+  // each lane's Q operands, parked in LDS (a lane reads back only what it
+  // wrote), leaving registers for two subtiles' scores at once
+  __shared__ __align__(16) u32x4 qs[kPfWaves][8][kWave];
   // Workgroups are dispatched in linear order (x, then y): the linear index
   // walks query tiles from the last, which under the causal mask attends to
   // the most keys, so the longest tiles start first and the short ones fill
@@ -545,13 +548,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 
   // this wave's Q operands: [query subtile][k step] (rows past the sequence
   // repeat its last query; their results are not stored)
-  bf16x8 qa[4][2];
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
     const int row = qb + min(q0 + qt * 16 + r, qn - 1);
     const u32x4* src = (const u32x4*)(q + ((size_t)row * kHq + head) * kD);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) qa[qt][ks] = moe::as_bf16x8(src[ks * 4 + g]);
+    for (int ks = 0; ks < 2; ++ks) qs[wave][qt * 2 + ks][lane] = src[ks * 4 + g];
   }
   const float c2 = sm_scale * 1.4426950408889634f;  // scores in log2 units
   f32x4 o[4][4];
@@ -649,18 +651,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
         va[s2][dt] = moe::as_bf16x8(*(const u32x4*)(vt[buf] + (dt * 16 + r) * kVRow + s2 * 32 + 8 * g));
-    // One 16-row subtile against the block: a subtile whose rows see none of
-    // the block is skipped, one that does not see it whole is masked.
-    auto subtile = [&](int qt) {
-      const int qpos0 = P + q0 + qt * 16;  // this subtile's positions: qpos0 .. qpos0 + 15
-      // every key of the block masked for all 16 queries: nothing to add
-      if (qpos0 + 15 < kb0 || (window > 0 && qpos0 - window + 1 > kb0 + kPfKeys - 1)) return;
-      f32x4 st[4];
+    // The four 16-row subtiles, software-pipelined: subtile qt + 1's scores
+    // (its Q operands read from LDS first) are issued in the same stretch of
+    // code as subtile qt's exponentials and P V products, so the MFMAs of one
+    // run while the vector ALUs work on the other.  A subtile whose rows see
+    // none of the block is not skipped: its mask sets every score to -inf, so
+    // p = 0 and o, l and m are unchanged.
+    bf16x8 q2[2];
+    f32x4 sa[4], sb[4];
+    auto read_q = [&](int qt) {
+      q2[0] = moe::as_bf16x8(qs[wave][qt * 2][lane]);
+      q2[1] = moe::as_bf16x8(qs[wave][qt * 2 + 1][lane]);
+    };
+    auto scores = [&](f32x4 (&st)[4]) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        st[kk] = mfma_bf16(ka[kk][0], qa[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
-        st[kk] = mfma_bf16(ka[kk][1], qa[qt][1], st[kk]);
+        st[kk] = mfma_bf16(ka[kk][0], q2[0], f32x4{0.f, 0.f, 0.f, 0.f});
+        st[kk] = mfma_bf16(ka[kk][1], q2[1], st[kk]);
       }
+    };
+    read_q(0);
+    scores(sa);
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      f32x4 (&st)[4] = (qt & 1) ? sb : sa;
+      f32x4 (&sn)[4] = (qt & 1) ? sa : sb;
+      if (qt < 3) read_q(qt + 1);
+      const int qpos0 = P + q0 + qt * 16;  // this subtile's positions: qpos0 .. qpos0 + 15
       // mask: key kb0 + 16 kk + 4 g + i for the query at position qpos; a
       // block that every row of the subtile sees whole (all blocks of a
       // causal row but its diagonal one) skips it
@@ -699,6 +716,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         l[qt] *= alpha;
         m[qt] = mn;
       }
+      if (qt < 3) scores(sn);
       // p = 2^(s c2 - m); masked scores (-inf) give 0, also in a row that has
       // seen no key yet (m = -inf)
       const float mneg = m[qt] == -INFINITY ? 0.0f : -m[qt];
@@ -729,9 +747,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
       }
       l[qt] += ps;
-    };
-#pragma unroll
-    for (int qt = 0; qt < 4; ++qt) subtile(qt);
+    }
     if (more) store(buf ^ 1);
     __syncthreads();
     buf ^= 1;
