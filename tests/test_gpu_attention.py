@@ -5,8 +5,10 @@ Bit-exact: RMSNorm, the QKV bias + YaRN RoPE (q and the cached k) and the
 appended v, bias + residual, the embedding gather.  Within tolerance (fp32
 softmax, probabilities as two bf16 pieces on the MFMA, against the oracle's
 fp64): decode and prefill / extend attention with the sink scaling, on
-scattered page tables, ragged batches, sliding windows, and the whole
-AttentionBlock at gpt-oss-20b shape.  Attention outputs are held to a
+scattered page tables, ragged batches, sliding windows, 4096-query prefills
+checked on sampled rows (a sharp softmax; row maxima that creep up block by
+block under the lazy rescale's headroom), and the whole AttentionBlock at
+gpt-oss-20b shape.  Attention outputs are held to a
 norm-relative max error of 1e-2 and a mean absolute error of 1e-3 relative to
 the mean magnitude (the block bar of the MoE path).
 """
@@ -104,13 +106,17 @@ def test_qkv_rope_append_bit_exact(A):
 class PagedSeqs:
     """Random keys / values of a few sequences laid out in a scattered page pool."""
 
-    def __init__(self, seed, lengths, pages=None):
+    def __init__(self, seed, lengths, pages=None, kv=None):
         rng = np.random.default_rng(seed)
         need = [-(-L // PAGE) for L in lengths]
         pool = pages or sum(need) + 3
         perm = rng.permutation(pool)
-        self.k = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
-        self.v = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
+        if kv is None:
+            self.k = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
+            self.v = [bf(rng.standard_normal((L, HKV, D))) for L in lengths]
+        else:   # given keys and values (bf16 bits) per sequence
+            self.k = [k for k, _ in kv]
+            self.v = [v for _, v in kv]
         cache = bf(rng.standard_normal((pool, 2, HKV, PAGE, D)))   # unused slots: garbage
         indptr, ids, off = [0], [], 0
         for L, k, v, npg in zip(lengths, self.k, self.v, need):
@@ -201,6 +207,64 @@ def test_prefill_attention(A, window, qlens):
         rows = slice(q_indptr[b], q_indptr[b + 1])
         o, lse = AO.attention(q[rows], seqs.k[b], seqs.v[b], np.arange(L - ql, L), window)
         close(got[rows], AO.sink_scale(o, lse, sinks))
+
+
+def _prefill_sampled(A, seqs, prefix, q, sinks, window, rows):
+    """One sequence's prefill (its last q.shape[0] positions are the queries)
+    checked on the sampled query rows: attention is per query, so the
+    oracle's output for those rows alone is their reference."""
+    n = q.shape[0]
+    L = prefix + n
+    out = torch.empty((n, HQ, D), dtype=torch.bfloat16, device="cuda")
+    A.prefill(bf16_dev(q), i32_dev(np.array([0, n], dtype=np.int32)), n, seqs.cache,
+              seqs.page_indptr, seqs.page_indices, seqs.kv_len, window, SCALE, bf16_dev(sinks),
+              out)
+    got = host_bf16(out)
+    o, lse = AO.attention(q[rows], seqs.k[0], seqs.v[0], np.arange(prefix, L)[rows], window)
+    close(got[rows], AO.sink_scale(o, lse, sinks))
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+
+
+def _sample_rows(n, seed):
+    """Rows at both ends, on both sides of every 64-row tile edge, and at random."""
+    rng = np.random.default_rng(seed)
+    edges = [e + d for e in range(64, n, 64 * 7) for d in (-1, 0)]
+    rows = set(range(16)) | set(range(n - 16, n)) | set(edges)
+    rows |= set(rng.choice(n, 64, replace=False).tolist())
+    return np.array(sorted(r for r in rows if 0 <= r < n))
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_prefill_attention_long_sharp(A, window):
+    """4096 queries after an unaligned 300-token prefix (64 query tiles, up to
+    69 key blocks each, the last block of every tile past its diagonal), with
+    q scaled by 4 so that the softmax is sharp and row maxima jump between
+    blocks (the lazy rescale's reference moves often)."""
+    prefix, n = 300, 4096
+    seqs = PagedSeqs(51, [prefix + n])
+    rng = np.random.default_rng(52)
+    q = bf(4.0 * rng.standard_normal((n, HQ, D)))
+    sinks = bf(rng.standard_normal(HQ))
+    _prefill_sampled(A, seqs, prefix, q, sinks, window, _sample_rows(n, 53))
+
+
+def test_prefill_attention_creeping_maximum(A):
+    """Keys with a component along a fixed direction u that grows with the
+    position, queries along u: every row's maximum score rises a little with
+    each 64-key block, by less than the 2^8 headroom of the lazy rescale, so
+    the reference point stays behind and p reaches about 2^8 before it
+    moves.  Scores span about 60 in log2 units along a row."""
+    n = 2048
+    rng = np.random.default_rng(54)
+    u = rng.standard_normal(D)
+    u /= np.linalg.norm(u)
+    pos = np.arange(n, dtype=np.float64)
+    k = 0.5 * rng.standard_normal((n, HKV, D)) + (pos * (40.0 / n))[:, None, None] * u
+    v = rng.standard_normal((n, HKV, D))
+    q = 0.5 * rng.standard_normal((n, HQ, D)) + 8.0 * u
+    seqs = PagedSeqs(55, [n], kv=[(bf(k), bf(v))])
+    sinks = bf(rng.standard_normal(HQ))
+    _prefill_sampled(A, seqs, 0, bf(q), sinks, 0, _sample_rows(n, 56))
 
 
 def _block(A, p, layer_idx):
