@@ -150,6 +150,12 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
 //    lane l holds, V^T's slot j of lane l the same key from the transposed
 //    tile; at the end the four waves' partial o are summed in wave order.
 constexpr int kDecChunk = 128;
+// the key of a chunk at V^T position p: each 64-key half interleaved,
+// position 2i key i, 2i + 1 key i + 32
+__device__ __forceinline__ int dec_key_at(int p) {
+  const int q = p & 63;
+  return (p & ~63) + ((q & 1) ? 32 + (q >> 1) : (q >> 1));
+}
 constexpr int kDecMaxCps = 8;
 constexpr int kDecKRow = kD + 8;         // padded K row (bf16)
 constexpr int kDecVRow = kDecChunk + 8;  // padded V^T row (bf16)
@@ -212,41 +218,36 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     qb[1] = moe::as_bf16x8(src[4 + g]);
   }
   __syncthreads();
-  // A chunk's loads: K 16-byte unit u = t + 256 j (key u / 8, part u % 8); V
-  // part t / 32 of keys 2 m, 2 m + 1, 64 + 2 m, 65 + 2 m (m = t % 32), written
-  // transposed as key pairs.  Keys past the chunk repeat its last key
-  // (finite; masked).
-  const int vpart = t >> 5, m2 = t & 31;
+  // A chunk's loads, K and V alike: 16-byte unit u = t + 256 j, key u / 8 =
+  // c + 32 j (c = t / 8), part t % 8 -- a wave reads eight whole 128-byte rows
+  // per instruction.  Keys past the chunk repeat its last key (finite;
+  // masked).  V is written transposed, each 64-key half interleaved: position
+  // 2i holds key i, 2i + 1 key i + 32 (the pair a thread holds, one 32-bit
+  // store), the 16-byte units of a V^T row XOR-swizzled by its 8-row group
+  // (the V part) so that the stores of a wave spread over the banks.
+  const int vc = t >> 3, vpart = t & 7;
   u32x4 kv[4], vv[4];
   auto load_chunk = [&](int c) {
     const int kc0 = k0 + c * kDecChunk, last = min(kDecChunk, nks - c * kDecChunk) - 1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int u = t + 256 * j;
-      const int pos = kc0 + min(u >> 3, last);
-      kv[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], 0, hk, pos % kPage) +
-                              (u & 7) * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int pos = kc0 + min((j >> 1) * 64 + 2 * m2 + (j & 1), last);
-      vv[j] = *(const u32x4*)(kv_row(cache, pid[pos / kPage - pg0], 1, hk, pos % kPage) +
-                              vpart * 8);
+      const int pos = kc0 + min(vc + 32 * j, last);
+      const uint16_t* kr = kv_row(cache, pid[pos / kPage - pg0], 0, hk, pos % kPage) + vpart * 8;
+      kv[j] = *(const u32x4*)kr;
+      vv[j] = *(const u32x4*)(kr + kHkv * kHeadBlock / 2);  // the V row of the same key
     }
   };
   auto store_chunk = [&]() {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int u = t + 256 * j;
-      *(u32x4*)(ks + (u >> 3) * kDecKRow + (u & 7) * 8) = kv[j];
-    }
+    for (int j = 0; j < 4; ++j) *(u32x4*)(ks + (vc + 32 * j) * kDecKRow + vpart * 8) = kv[j];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t a0 = (vv[2 * h2][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
         const uint32_t a1 = (vv[2 * h2 + 1][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        *(uint32_t*)(vt + (vpart * 8 + e) * kDecVRow + h2 * 64 + 2 * m2) = a0 | (a1 << 16);
+        const int unit = (8 * h2 + (vc >> 2)) ^ vpart;  // rows vpart * 8 + e: group vpart
+        *(uint32_t*)(vt + (vpart * 8 + e) * kDecVRow + unit * 8 + ((2 * vc) & 7)) = a0 | (a1 << 16);
       }
   };
   load_chunk(0);
@@ -260,17 +261,20 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   for (int c = 0; c < nch; ++c) {
     const int nkc = min(kDecChunk, nks - c * kDecChunk);
     if (c + 1 < nch) load_chunk(c + 1);  // in flight during this chunk's products
-    // scores of the wave's 32 keys
+    // scores of the keys at V^T positions 32 w .. 32 w + 31: A row r of tile
+    // kk is the key at position 32 w + 8 (r / 4) + 4 kk + r % 4, so result
+    // element i of lane (r, g) is the key at position 32 w + 8 g + 4 kk + i,
+    // the one V^T's operand slot 4 kk + i of the lane carries
     float sv[8];
     float mx = -INFINITY;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const uint16_t* kr = ks + (32 * wave + 16 * kk + r) * kDecKRow + 8 * g;
+      const uint16_t* kr = ks + dec_key_at(32 * wave + 8 * (r >> 2) + 4 * kk + (r & 3)) * kDecKRow + 8 * g;
       f32x4 st = dec_mfma(moe::as_bf16x8(*(const u32x4*)kr), qb[0], f32x4{0.f, 0.f, 0.f, 0.f});
       st = dec_mfma(moe::as_bf16x8(*(const u32x4*)(kr + 32)), qb[1], st);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = 32 * wave + 16 * kk + 4 * g + i;
+        const int key = dec_key_at(32 * wave + 8 * g + 4 * kk + i);
         sv[4 * kk + i] = key < nkc ? st[i] * sm_scale : -INFINITY;
         mx = fmaxf(mx, sv[4 * kk + i]);
       }
@@ -296,10 +300,9 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vr = vt + (16 * dt + r) * kDecVRow + 32 * wave;
-      const uint2 vlo = *(const uint2*)(vr + 4 * g);
-      const uint2 vhi = *(const uint2*)(vr + 16 + 4 * g);
-      const bf16x8 va = moe::as_bf16x8(u32x4{vlo.x, vlo.y, vhi.x, vhi.y});
+      const int row = 16 * dt + r;  // positions 32 w + 8 g .. + 7: one swizzled unit
+      const bf16x8 va = moe::as_bf16x8(
+          *(const u32x4*)(vt + row * kDecVRow + ((4 * wave + g) ^ ((row >> 3) & 7)) * 8));
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
       o[dt] = dec_mfma(va, ph, o[dt]);
