@@ -140,15 +140,18 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
 // Both products run on v_mfma_f32_16x16x32_bf16, with the lane facts the
 // prefill kernel below relies on (operand row / column = lane % 16; result
 // element i of lane l = row 4 (l / 16) + i, column l % 16; A and B pair their
-// operand slots by position): wave w takes keys 32 w .. 32 w + 31 of a chunk,
+// operand slots by position): wave w takes the keys at positions 32 w ..
+// 32 w + 31 of the chunk's V^T tile (dec_key_at: each 64-key half holds keys
+// i and i + 32 side by side),
 //  * S^T = K Q^T (A = 16 keys x 32 dims, B = 32 dims x 16 "queries": the 8
-//    heads, repeated): lane l holds S[head l % 16][key 32 w + 16 kk + 4 (l / 16)
-//    + i] for kk = 0, 1; scores in fp32 (times sm_scale), the chunk's maximum
-//    per head through LDS;
+//    heads, repeated): A row r of tile kk is the key at position 32 w + 8 (r /
+//    4) + 4 kk + r % 4, so lane l holds S[head l % 16][the keys at positions
+//    32 w + 8 (l / 16) + 4 kk + i] for kk = 0, 1; scores in fp32 (times
+//    sm_scale), the chunk's maximum per head through LDS;
 //  * O^T = V^T P^T over the wave's 32 keys (P as two bf16 pieces, about 16
-//    bits, as in the prefill kernel): P's slot j of lane l carries the key
-//    lane l holds, V^T's slot j of lane l the same key from the transposed
-//    tile; at the end the four waves' partial o are summed in wave order.
+//    bits, as in the prefill kernel): P's slot 4 kk + i of lane l carries
+//    that score, V^T's slot j of lane l position 32 w + 8 (l / 16) + j, the
+//    same key; at the end the four waves' partial o are summed in wave order.
 constexpr int kDecChunk = 128;
 // the key of a chunk at V^T position p: each 64-key half interleaved,
 // position 2i key i, 2i + 1 key i + 32
