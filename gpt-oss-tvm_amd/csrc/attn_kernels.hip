@@ -46,14 +46,12 @@ __device__ __forceinline__ const uint16_t* kv_row(const uint8_t* cache, int page
 struct PageList {
   const int* ids;
   int count, pool;
-  // the table entry of the page holding pos, and that entry clamped into the
-  // pool (split so that a loop can read entries ahead and clamp at use)
-  __device__ __forceinline__ int raw_page_of(int pos) const {
-    const int i = min(pos / kPage, count - 1);
-    return ids[max(i, 0)];
-  }
+  // a table entry clamped into the pool (callers that read entries ahead
+  // clamp them at use)
   __device__ __forceinline__ int clamp(int id) const { return min(max(id, 0), pool - 1); }
-  __device__ __forceinline__ int page_of(int pos) const { return clamp(raw_page_of(pos)); }
+  __device__ __forceinline__ int page_of(int pos) const {
+    return clamp(ids[max(min(pos / kPage, count - 1), 0)]);
+  }
 };
 
 // ---------------------------------------------------------------------------
