@@ -134,6 +134,16 @@ __device__ __forceinline__ f32x4 mfma_mx(const i32x8& a, const i32x8& b, f32x4 c
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
 }
 
+// x of lane l ^ 1 and of lane l ^ 2: DPP quad permutes [1,0,3,2] and
+// [2,3,0,1], a register move with no LDS round trip (a shuffle through
+// ds_bpermute waits for the LDS).  All lanes of the quad must be active.
+__device__ __forceinline__ float lane_xor1(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor2(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+}
+
 // A 64-bit value moved between lanes by one DPP pattern (two 32-bit moves);
 // lanes outside ROW_MASK get 0.
 template <int CTRL, int ROW_MASK = 0xF>

@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
             // the even lane takes token tt0, the odd lane token tt0 + 1
             const bool odd = (r & 1) != 0;
             const float send = odd ? y0 : y1;  // what the partner needs
-            const float recv = __shfl_xor(send, 1, kWave);
+            const float recv = lane_xor1(send);
             const float glu = odd ? recv : y0;
             const float lin = odd ? y1 : recv;
             const float xg = fminf(glu, limit);
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
           float amax = 0.0f;
 #pragma unroll
           for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
-          amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-          amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+          amax = fmaxf(amax, lane_xor1(amax));
+          amax = fmaxf(amax, lane_xor2(amax));
           const uint32_t sc = e8m0_for_amax(amax);
           const float inv = __uint_as_float((254u - sc) << 23);
           const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(256) void moe_pieces_kernel(const void* __restrict_
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(r[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+    amax = fmaxf(amax, lane_xor1(amax));
+    amax = fmaxf(amax, lane_xor2(amax));
     const uint32_t s = e8m0_for_amax(amax);
     const float inv = __uint_as_float((254u - s) << 23);                           // 2^(127 - s)
     const float sc = s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u);  // 2^(s - 127)
@@ -499,8 +499,8 @@ __device__ __forceinline__ void mx_pass(
             float amax = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            amax = fmaxf(amax, lane_xor1(amax));
+            amax = fmaxf(amax, lane_xor2(amax));
             const uint32_t sc = e8m0_for_amax(amax);
             const float inv = __uint_as_float((254u - sc) << 23);
             const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
@@ -700,8 +700,8 @@ __device__ __forceinline__ void mx_pass(
             const float y1 = (acc[3] + acc[2]) + bn;
             const int tt0 = gi * TPG + 2 * g;
             if constexpr (kEpi == 1 || kEpi == 3) {
-              const float l0 = __shfl_xor(y0, 1, kWave);  // odd rows hold the linear half
-              const float l1 = __shfl_xor(y1, 1, kWave);
+              const float l0 = lane_xor1(y0);  // odd rows hold the linear half
+              const float l1 = lane_xor1(y1);
               if ((r & 1) == 0) {
                 const float yy[2] = {y0, y1}, ll[2] = {l0, l1};
   #pragma unroll
@@ -938,8 +938,8 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+        amax = fmaxf(amax, lane_xor1(amax));
+        amax = fmaxf(amax, lane_xor2(amax));
         const uint32_t sc = e8m0_for_amax(amax);
         const float inv = __uint_as_float((254u - sc) << 23);
         const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);

@@ -136,8 +136,8 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            amax = fmaxf(amax, lane_xor1(amax));
+            amax = fmaxf(amax, lane_xor2(amax));
             const uint32_t sc = e8m0_for_amax(amax);
             const float inv = __uint_as_float((254u - sc) << 23);
             const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
@@ -370,8 +370,8 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(rr[q]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            amax = fmaxf(amax, lane_xor1(amax));
+            amax = fmaxf(amax, lane_xor2(amax));
             const uint32_t sc = e8m0_for_amax(amax);
             const float inv = __uint_as_float((254u - sc) << 23);
             const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
