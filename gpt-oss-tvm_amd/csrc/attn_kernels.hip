@@ -473,7 +473,7 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
 //
 // Workgroup = (query tile of 64 rows of one sequence, kv head hk, half h of
 // its GQA group): 4 waves, wave w = query head 8 hk + 4 h + w, so 4 heads share
-// each key/value block staged in LDS.  At about 240 VGPRs a SIMD holds two
+// each key/value block staged in LDS.  At 256 VGPRs a SIMD holds two
 // waves: two independent workgroups per CU, whose barriers and phases do not
 // line up, rather than one of 8 waves.  Keys in blocks of 64 (four pages),
 // double buffered: the next block's global loads are in flight while the
