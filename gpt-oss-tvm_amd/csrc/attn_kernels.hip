@@ -494,6 +494,7 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
 //    (position 2i key i, 2i + 1 key i + 16), so that a lane's 8 keys are one
 //    16-byte read.
 constexpr int kPfQ = 64;              // query rows per wave
+constexpr int kPfSub = kPfQ / 16;     // 16-row subtiles per wave
 constexpr int kPfKeys = 64;           // keys per block
 constexpr int kKRow = kD + 8;         // K tile row (bf16), padded
 constexpr int kVRow = kPfKeys + 8;    // V^T tile row (bf16), padded
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __align__(16) uint16_t vt[2][kD * kVRow];
   // each lane's Q operands, parked in LDS (a lane reads back only what it
   // wrote), leaving registers for two subtiles' scores at once
-  __shared__ __align__(16) u32x4 qs[kPfWaves][8][kWave];
+  __shared__ __align__(16) u32x4 qs[kPfWaves][2 * kPfSub][kWave];
   // Workgroups are dispatched in linear order (x, then y): the linear index
   // walks query tiles from the last, which under the causal mask attends to
   // the most keys, so the longest tiles start first and the short ones fill
@@ -553,17 +554,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // this wave's Q operands: [query subtile][k step] (rows past the sequence
   // repeat its last query; their results are not stored)
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
+  for (int qt = 0; qt < kPfSub; ++qt) {
     const int row = qb + min(q0 + qt * 16 + r, qn - 1);
     const u32x4* src = (const u32x4*)(q + ((size_t)row * kHq + head) * kD);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) qs[wave][qt * 2 + ks][lane] = src[ks * 4 + g];
   }
   const float c2 = sm_scale * 1.4426950408889634f;  // scores in log2 units
-  f32x4 o[4][4];
-  float m[4], l[4];
+  f32x4 o[kPfSub][4];
+  float m[kPfSub], l[kPfSub];
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
+  for (int qt = 0; qt < kPfSub; ++qt) {
     m[qt] = -INFINITY;
     l[qt] = 0.f;
 #pragma unroll
@@ -655,7 +656,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
         va[s2][dt] = moe::as_bf16x8(*(const u32x4*)(vt[buf] + (dt * 16 + r) * kVRow + s2 * 32 + 8 * g));
-    // The four 16-row subtiles, software-pipelined: subtile qt + 1's scores
+    // The 16-row subtiles, software-pipelined: subtile qt + 1's scores
     // (its Q operands read from LDS first) are issued in the same stretch of
     // code as subtile qt's exponentials and P V products, so the MFMAs of one
     // run while the vector ALUs work on the other.  A subtile whose rows see
@@ -677,10 +678,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     read_q(0);
     scores(sa);
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
+    for (int qt = 0; qt < kPfSub; ++qt) {
       f32x4 (&st)[4] = (qt & 1) ? sb : sa;
       f32x4 (&sn)[4] = (qt & 1) ? sa : sb;
-      if (qt < 3) read_q(qt + 1);
+      if (qt < kPfSub - 1) read_q(qt + 1);
       const int qpos0 = P + q0 + qt * 16;  // this subtile's positions: qpos0 .. qpos0 + 15
       // mask: key kb0 + 16 kk + 4 g + i for the query at position qpos; a
       // block that every row of the subtile sees whole (all blocks of a
@@ -720,7 +721,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         l[qt] *= alpha;
         m[qt] = mn;
       }
-      if (qt < 3) scores(sn);
+      if (qt < kPfSub - 1) scores(sn);
       // p = 2^(s c2 - m); masked scores (-inf) give 0, also in a row that has
       // seen no key yet (m = -inf)
       const float mneg = m[qt] == -INFINITY ? 0.0f : -m[qt];
@@ -758,7 +759,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   // epilogue: row sums across the 4 lane groups, lse, sink factor, bf16
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
+  for (int qt = 0; qt < kPfSub; ++qt) {
     float lt = l[qt];
     lt += __shfl_xor(lt, 16, kWave);
     lt += __shfl_xor(lt, 32, kWave);
