@@ -470,6 +470,52 @@ def run_decode_loop(dev, prompt_len: int = 128, steps: int = 32) -> dict:
     return res
 
 
+def mfma_calibration(dev, size: int = 8192, reps: int = 20) -> dict:
+    """The matrix cores' achievable rate as the vendor library reaches it:
+    torch's bf16 matmul and fp8 scaled_mm (hipBLASLt) on size^3, timed with
+    HIP events over `reps` calls after a warmup.  A reference point for the
+    expert GEMMs' MFMA fractions, not a kernel of this build."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    a = torch.randn((size, size), generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn((size, size), generator=g, device=dev).to(torch.bfloat16)
+    flops = 2.0 * size ** 3
+    res = {"size": size}
+
+    def rate(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return flops / (e0.elapsed_time(e1) * 1e-3 / reps) / 1e12
+
+    tf = rate(lambda: torch.matmul(a, b))
+    res["bf16_tflops"] = round(tf, 1)
+    res["bf16_frac_of_2500"] = round(tf / BF16_PEAK_TFLOPS, 3)
+    for name in ("float8_e4m3fn", "float8_e4m3fnuz"):
+        dt = getattr(torch, name, None)
+        if dt is None:
+            continue
+        try:
+            a8, b8 = a.to(dt), b.t().contiguous().to(dt).t()
+            one = torch.ones((), device=dev, dtype=torch.float32)
+            tf8 = rate(lambda: torch._scaled_mm(a8, b8, scale_a=one, scale_b=one,
+                                                out_dtype=torch.bfloat16))
+            res["fp8_dtype"] = name
+            res["fp8_tflops"] = round(tf8, 1)
+            res["fp8_frac_of_5000"] = round(tf8 / 5000.0, 3)
+            break
+        except (RuntimeError, TypeError) as exc:
+            res[f"fp8_{name}_error"] = str(exc).splitlines()[0][:120]
+    return res
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -547,6 +593,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 512 MiB (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
+    ap.add_argument("--mfma-calibration", action="store_true",
+                    help="only time library GEMMs of 8192^3 through torch (hipBLASLt: bf16 "
+                         "matmul, fp8 scaled_mm) as the matrix cores' achievable rate, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -565,6 +614,9 @@ def main() -> int:
         return 0
 
     dev = torch.device("cuda:0")
+    if args.mfma_calibration:
+        print(json.dumps(mfma_calibration(dev)), flush=True)
+        return 0
     prim, blocks, xs = run_block_config(args.config, args.steps, args.warmup, args.weight_sets, dev)
     E, n, _, label = CONFIGS[args.config]
     us = prim["us_per_block"]
