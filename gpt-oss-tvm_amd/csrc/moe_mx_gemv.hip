@@ -349,9 +349,12 @@ __device__ __forceinline__ void mx_pass(
   // Direct-to-LDS staging of packed pieces (NCT == 23): a group's bytes tile
   // exactly into 1 KB windows, one 64-lane x 16-byte global_load_lds each.
   // A 16-byte slot is 16 code bytes of a piece row, the row's pad (never
-  // read) or 16 of its scale bytes.  Rows past the batch repeat its last
-  // token (finite data; their outputs are not stored).  No registers hold
-  // the data, so a batch's whole staging is in flight at once.
+  // read) or 16 of its scale bytes.  Rows past the batch are not loaded:
+  // their LDS bytes keep whatever they held (an MFMA output row depends on
+  // its own operand row only, and rows past the batch are neither stored nor
+  // combined with other rows; zero-filling them instead measured slower at
+  // 64 tokens).  No registers hold the data, so a batch's whole staging is
+  // in flight at once.
   constexpr bool kDirect = kEpi != 2 && NCT == 23;
   static_assert(mx_group_bytes(23) % 1024 == 0, "group windows");
   // kWait: the pieces were written by other workgroups of this launch with
@@ -367,15 +370,17 @@ __device__ __forceinline__ void mx_pass(
       const int m = in_rows ? o / kMxRowStride : (o - 16 * kMxRowStride) / kMxSclRow;
       const int within =
           in_rows ? o - m * kMxRowStride : o - 16 * kMxRowStride - m * kMxSclRow;
-      const int tt = min(gi * TPG + m / P, nb - 1);
-      const int row = arow_mode == 0   ? rowmap[tt] / k_top
-                      : arow_mode == 1 ? rowmap[tt]
-                                       : start + b0 + tt;
-      const size_t prow = (size_t)row * P + (m % P);
-      const uint8_t* src = in_rows ? q + prow * Kp + (within < Kp ? within : 0)
-                                   : qs + prow * kMxSclRow + within;
-      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(lds + wi * 1024), 16, 0,
-                                       kWait ? kCpolSc1 : 0);
+      const int tt = gi * TPG + m / P;
+      if (tt < nb) {
+        const int row = arow_mode == 0   ? rowmap[tt] / k_top
+                        : arow_mode == 1 ? rowmap[tt]
+                                         : start + b0 + tt;
+        const size_t prow = (size_t)row * P + (m % P);
+        const uint8_t* src = in_rows ? q + prow * Kp + (within < Kp ? within : 0)
+                                     : qs + prow * kMxSclRow + within;
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(lds + wi * 1024), 16, 0,
+                                         kWait ? kCpolSc1 : 0);
+      }
     }
   };
 
