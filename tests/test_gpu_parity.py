@@ -205,7 +205,8 @@ def test_many_tokens_per_expert(native):
                                           (32, 2880, 2880, 128, 39), (32, 2880, 64, 4096, 40),
                                           (128, 2880, 64, 1100, 41), (128, 256, 64, 4100, 42),
                                           (40, 192, 64, 1500, 43), (32, 2880, 2880, 2, 44),
-                                          (128, 2880, 64, 2, 45), (128, 256, 64, 1, 46)])
+                                          (128, 2880, 64, 2, 45), (128, 256, 64, 1, 46),
+                                          (12, 192, 64, 1, 47), (40, 192, 64, 1, 48)])
 def test_block_internal_routing(native, E, H, I, n, seed):
     """The block's own router and grouping (logits kernel — VALU fp64 dots up
     to 1024 tokens, fp64 MFMA dots above — then one workgroup of top-k +
