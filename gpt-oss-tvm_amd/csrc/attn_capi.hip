@@ -52,8 +52,9 @@ inline int status(int launch_rc) { return launch_rc == 0 ? MOE_OK : MOE_ERR_LAUN
 // Chunks of 128 keys per decode workgroup: more with larger batches, where
 // there are workgroups enough (a workgroup's fixed costs, the page-table
 // reads before its first loads and the published partial after its last
-// chunk, then spread over more keys).  It depends on the batch only, so a
-// call's results do not depend on the span bound (a captured graph fixes the
+// chunk, then spread over more keys).  It depends on the batch only (the
+// kernel makes a span of at most two chunks one split), so a call's results
+// do not depend on the span bound (a captured graph fixes the
 // bound at the pool's capacity).
 int64_t decode_cps(int64_t batch) { return batch >= 32 ? 8 : batch >= 8 ? 4 : batch >= 2 ? 2 : 1; }
 int64_t decode_splits(int64_t batch, int64_t max_span) {

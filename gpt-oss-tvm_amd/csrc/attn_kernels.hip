@@ -192,12 +192,17 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   const int wave = t >> 6, lane = t & 63, r = lane & 15, g = lane >> 4;
   const int L = kv_len[b];
   const int lo = window > 0 ? max(0, L - window) : 0;
-  const int skeys = kDecChunk * cps;
+  const int span = L - lo;
+  // keys per split: cps chunks, except that a span of at most two chunks is
+  // one split (its chunks in sequence cost less than publishing and merging
+  // partials); covered = the keys the caller's bound gives the splits
+  const int skeys =
+      kDecChunk * (span <= 2 * kDecChunk ? max(cps, (span + kDecChunk - 1) / kDecChunk) : cps);
+  const int covered = splits * kDecChunk * cps;
   const int k0 = lo + s * skeys;
   const int nks = max(0, min(skeys, L - k0));
   const size_t pidx = ((size_t)b * kHq + hk * kGroup) * splits + s;  // head h: + h * splits
   // the splits holding keys: the first ceil(span / skeys) (at most splits)
-  const int span = L - lo;
   const int used = min((span + skeys - 1) / skeys, splits);
   // a split past the attended range holds no keys and writes nothing (the
   // merge reads only the used splits); an empty range gives NaN outputs
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
       o0 += obuf[(w * kGroup + h0) * kD + d];
       o1 += obuf[(w * kGroup + h0 + 4) * kD + d];
     }
-    if (used == 1 && span <= splits * skeys) {
+    if (used == 1 && span <= covered) {
       // the only split: the merge's arithmetic for one split (its weight is
       // exp(0) = 1), done here without publishing the partial
 #pragma unroll
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   }
   __syncthreads();
   if (is_last)
-    decode_merge_group(part_o, part_ml, splits, used, span > splits * skeys, b, hk, sinks,
+    decode_merge_group(part_o, part_ml, splits, used, span > covered, b, hk, sinks,
                        out);
 }
 

@@ -152,6 +152,23 @@ def test_decode_attention(A, window):
         close(got[b:b + 1], AO.sink_scale(o, lse, sinks))
 
 
+@pytest.mark.parametrize("L", [129, 200, 256, 257, 600])
+def test_decode_attention_one_sequence(A, L):
+    """One sequence: a span of at most two 128-key chunks is one split (both
+    chunks in one workgroup, no merge), longer spans split by chunk and
+    merge; the span bound is far above the length."""
+    seqs = PagedSeqs(37 + L, [L])
+    rng = np.random.default_rng(38 + L)
+    q = bf(rng.standard_normal((1, HQ, D)))
+    sinks = bf(rng.standard_normal(HQ))
+    ws = A.decode_workspace(1, 4096)
+    out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device="cuda")
+    A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, 4096, 0,
+             SCALE, bf16_dev(sinks), out, ws)
+    o, lse = AO.attention(q, seqs.k[0], seqs.v[0], np.array([L - 1]), 0)
+    close(host_bf16(out), AO.sink_scale(o, lse, sinks))
+
+
 def test_decode_attention_reused_workspace_and_large_bound(A):
     """The last split of each (sequence, kv head) to finish merges the
     group; its arrival counts live in the workspace and are left zero, so
@@ -176,12 +193,15 @@ def test_decode_attention_reused_workspace_and_large_bound(A):
         np.testing.assert_array_equal(o, outs[0])
 
 
-def test_decode_span_too_small_is_nan(A):
-    seqs = PagedSeqs(33, [300])
+@pytest.mark.parametrize("L,bound", [(300, 200), (200, 100)])
+def test_decode_span_too_small_is_nan(A, L, bound):
+    """A span bound below the length gives NaN, also where the span would fit
+    one split of two chunks (the bound fixes the splits' reach)."""
+    seqs = PagedSeqs(33, [L])
     q = bf(np.random.default_rng(34).standard_normal((1, HQ, D)))
-    ws = A.decode_workspace(1, 300)
+    ws = A.decode_workspace(1, L)
     out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device="cuda")
-    A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, 200, 0,
+    A.decode(bf16_dev(q), seqs.cache, seqs.page_indptr, seqs.page_indices, seqs.kv_len, bound, 0,
              SCALE, bf16_dev(bf(np.zeros(HQ))), out, ws)
     assert np.isnan(O.bf16_to_f32(host_bf16(out))).all()
 
