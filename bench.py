@@ -147,24 +147,25 @@ def timed_steps(fn, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) / steps
 
 
-def staged_pass(blocks, xs, steps: int, stages, fused: bool, pieces_epilogue: bool) -> dict:
-    """Per-stage HIP events on the launch stream.  A spin kernel is queued first
-    so the host runs ahead of the GPU and the events time the kernels, not
-    gaps left by Python between launches (a staged call costs the host about
-    a millisecond: seven C calls, their output tensors and fourteen events,
-    more than a one-token block takes on the GPU)."""
+def marked_pass(blocks, xs, steps: int) -> dict:
+    """Per-stage times of the block's own launches (MLPBlock.forward_marked:
+    HIP events recorded on the launch stream between them).  A spin kernel is
+    queued first so that the host runs ahead of the GPU and the events time
+    the kernels, not gaps left by Python between calls."""
     import torch
     recs = []
     nw = len(blocks)
-    torch.cuda._sleep(int(2.4e9 * 1.5e-3 * steps))
+    torch.cuda._sleep(int(2.4e9 * 0.4e-3 * steps))
     for i in range(steps):
-        ev = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for s in stages}
-        blocks[i % nw].forward_staged(xs[i % nw], events=ev, fused_decode=fused,
-                                      pieces_epilogue=pieces_epilogue)
-        recs.append(ev)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(8)]
+        _, names = blocks[i % nw].forward_marked(xs[i % nw], ev)
+        recs.append((ev, names))
     torch.cuda.synchronize()
-    return {s: sum(r[s][0].elapsed_time(r[s][1]) for r in recs) / len(recs) * 1e3 for s in stages}
+    out: dict = {}
+    for ev, names in recs:
+        for j, name in enumerate(names):
+            out[name] = out.get(name, 0.0) + ev[j].elapsed_time(ev[j + 1]) * 1e3
+    return {k: v / len(recs) for k, v in out.items()}
 
 
 def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) -> tuple:
@@ -196,19 +197,8 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
 
     nk = n * K_TOP
     gemm = nk >= 48 * E
-    fused = False
-    if not gemm and n <= 128:
-        try:
-            blocks[0].forward_staged(xs[0], fused_decode=True)
-            fused = True
-        except RuntimeError as e:
-            log(f"mlp_decode not used: {e}")
-    torch.cuda.synchronize()
-    if fused:
-        stages = ("router", "permute", "pieces_t", "mlp_decode", "combine")
-    else:
-        stages = ("router", "permute", "pieces_t", "mlp1", "pieces_act", "mlp2", "combine")
-    stage_us = staged_pass(blocks, xs, min(steps, 100), stages, fused, gemm)
+    stage_us = marked_pass(blocks, xs, min(steps, 100))
+    fused = "decode" in stage_us
     log(f"{name} stage us: " + ", ".join(f"{s}={v:.1f}" for s, v in stage_us.items()))
 
     bb = block_bytes(n, avg_touched, E)
@@ -226,10 +216,11 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
         # token in and out); the act pieces written and read back inside the
         # launch are intermediates, listed apart and not counted
         alg = avg_touched * PER_EXPERT_BYTES + n * H * 4
-        t = stage_us["mlp_decode"]
+        t = stage_us["decode"]
         achieved = alg / (t * 1e-6) / 1e9
         roof = {"bound": "hbm",
-                "kernel": "moe_mx_decode_kernel (mlp1 + SwiGLU + act pieces + mlp2)",
+                "kernel": "moe_mx_decode_kernel (mlp1 + SwiGLU + act pieces + mlp2"
+                          + (" + gated combine)" if "gating" not in stage_us else ")"),
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": read_traffic(name, "moe::moe_mx_decode_kernel"),
@@ -248,24 +239,59 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
     else:
         f1 = 2 * nk * 2 * I * H
         t = stage_us["mlp1"]
-        achieved = f1 / (t * 1e-6) / 1e12
-        roof = {"bound": "mfma", "kernel": "moe_mx_gemm_kernel<2,2> (mlp1, act pieces epilogue)",
-                "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                # the MFMA executes every fp8 piece: algorithmic x pieces, at
-                # the fp8 (fp8 x fp4) dense rate
-                "fp8_hw_frac": round(achieved * PIECES_T / FP8_PEAK_TFLOPS, 4),
-                "traffic": read_traffic(name, "moe::moe_mx_gemm_kernel<2, 2>"),
-                "algorithmic_flops": int(f1), "avg_us": round(t, 2)}
+        tflops = f1 / (t * 1e-6) / 1e12
+        # mlp1's compulsory bytes: the touched experts' mlp1 weights, t's pieces
+        # in, act's three pieces out
+        b1 = (avg_touched * (2 * I * (H // 32) * 17 + 2 * I * 2) + n * H * PIECES_T
+              + nk * I * PIECES_ACT * 33 / 32)
+        gbs = b1 / (t * 1e-6) / 1e9
+        ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)     # flop per byte
+        kern = "moe_mx_gemm_kernel<2,2> (mlp1, act pieces epilogue)"
+        common = {"kernel": kern, "traffic": read_traffic(name, "moe::moe_mx_gemm_kernel<2, 2>"),
+                  "algorithmic_flops": int(f1), "algorithmic_bytes": int(b1),
+                  "intensity_flop_per_byte": round(bf / bb, 1), "avg_us": round(t, 2),
+                  # the MFMA executes every fp8 piece: algorithmic x pieces,
+                  # at the fp8 (fp8 x fp4) dense rate
+                  "fp8_hw_frac": round(tflops * PIECES_T / FP8_PEAK_TFLOPS, 4)}
+        if bf / bb < ridge:
+            # below the ridge (120B prefill 2048): HBM-bound
+            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "bf16_mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), **common}
+        else:
+            roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), **common}
         t2 = stage_us["mlp2"]
         f2 = 2 * nk * H * I
+        b2 = avg_touched * (H * (I // 32) * 17 + H * 2) + nk * I * PIECES_ACT * 33 / 32 + nk * H * 4
         res["mlp2"] = {"avg_us": round(t2, 2),
                        "frac": round(f2 / (t2 * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                       "fp8_hw_frac": round(f2 * PIECES_ACT / (t2 * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+                       "hbm_frac": round(b2 / (t2 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "fp8_hw_frac": round(f2 * PIECES_ACT / (t2 * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                       "traffic": read_traffic(name, "moe::moe_mx_gemm_kernel<3, 0>")}
     res["roofline"] = roof
     res["algorithmic_bytes"] = int(bb)
     res["algorithmic_flops"] = int(bf)
     return res, blocks, xs
+
+
+def mixed_stack(dev, layers: int = 24, n_dec: int = 32, n_pre: int = 2048):
+    """Config 4's layers: per layer one 20B block with its own seeded weights
+    (seed 2000 + layer) for the decode group and a view of it under the Zipf
+    router bias (beta 0.5) for the prefill group, chained in a MoEStack
+    reserved for n_dec and n_pre tokens (tests/test_gpu_graph.py checks this
+    same stack)."""
+    from model.stack import MoEStack
+    zb = zipf_bias(32, 0.5, dev)
+    pairs = []
+    for layer in range(layers):
+        dec = make_block(32, 2000 + layer, 0.0, dev)
+        pre = dec.with_gate_bias(dec.gate.bias.float() + zb)
+        pairs.append((dec, pre))
+    stack = MoEStack(pairs)
+    stack.reserve(n_dec, n_pre)
+    return stack
 
 
 def run_mixed(steps: int, warmup: int, dev, layers: int = 24, n_dec: int = 32,
@@ -276,16 +302,8 @@ def run_mixed(steps: int, warmup: int, dev, layers: int = 24, n_dec: int = 32,
     in one HIP graph (MoEStack: nothing allocated inside) and replayed."""
     import torch
 
-    from model.stack import MoEStack
     log(f"workload mixed24: {layers} layers, {n_dec} decode + {n_pre} prefill tokens")
-    pairs = []
-    zb = zipf_bias(32, 0.5, dev)
-    for layer in range(layers):
-        dec = make_block(32, 2000 + layer, 0.0, dev)
-        pre = dec.with_gate_bias(dec.gate.bias.float() + zb)
-        pairs.append((dec, pre))
-    stack = MoEStack(pairs)
-    stack.reserve(n_dec, n_pre)
+    stack = mixed_stack(dev, layers, n_dec, n_pre)
     gx = torch.Generator(device=dev)
     gx.manual_seed(9)
     xd = torch.randn((1, n_dec, H), generator=gx, device=dev).to(torch.bfloat16)
@@ -311,7 +329,7 @@ def run_mixed(steps: int, warmup: int, dev, layers: int = 24, n_dec: int = 32,
            "bf16_mfma_frac": round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4),
            "hbm_frac": round(bytes_ / sec / 1e9 / HBM_PEAK_GBS, 4),
            "algorithmic_flops": int(flops)}
-    del graph, stack, pairs
+    del graph, stack
     return res
 
 

@@ -89,6 +89,23 @@ constexpr int64_t kGemmMinTokens = 48;
 // count, then the y rows) sit at the launch's tail.
 constexpr int64_t kFusedCombineMaxTokens = 32;
 
+// moe_block_forward_marked: the caller's hipEvents recorded on the block's
+// stream before its first launch and after each stage (MOE_STAGE_*).
+constexpr int kMaxMarks = 8;
+struct Marks {
+  hipEvent_t const* ev;
+  int used;
+  int32_t stage[kMaxMarks];
+};
+
+inline int mark(Marks* m, int stage, hipStream_t s) {
+  if (!m) return MOE_OK;
+  if (m->used >= kMaxMarks) return MOE_ERR_SHAPE;
+  if (hipEventRecord(m->ev[m->used], s) != hipSuccess) return MOE_ERR_LAUNCH;
+  m->stage[m->used++] = stage;
+  return MOE_OK;
+}
+
 int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indptr,
                   const int32_t* sorted_pairs, int k_top, int arow_mode, int orow_mode,
                   const void* blocks, const void* scales, const void* bias, int E, int N, int K,
@@ -427,13 +444,18 @@ int moe_workspace_layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
   return MOE_OK;
 }
 
-int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
-                      const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,
-                      const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
-                      const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
-                      const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
-                      float alpha, float limit, uint16_t* out, void* workspace,
-                      size_t workspace_bytes, moe_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H,
+                              int64_t I, const uint16_t* norm_w, const uint16_t* gate_w,
+                              const uint16_t* gate_b, const uint8_t* mlp1_blocks,
+                              const uint8_t* mlp1_scales, const uint16_t* mlp1_bias,
+                              const uint8_t* mlp2_blocks, const uint8_t* mlp2_scales,
+                              const uint16_t* mlp2_bias, float eps, float alpha, float limit,
+                              uint16_t* out, void* workspace, size_t workspace_bytes,
+                              moe_stream_t stream, Marks* m) {
   int rc = check_dims(n, E, k, H, I);
   if (rc) return rc;
   if (n == 0) return MOE_OK;
@@ -469,15 +491,18 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
   // norm, t, its pieces and the logits (and sync[0..E] = 0: the decode
   // launch's counts and status); then top-k, softmax and grouping
   void* t_qs = (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT);
+  if ((rc = mark(m, MOE_STAGE_START, s))) return rc;
   if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
-                                     logits, t_pk, t_qs, sync, s)))
+                                     logits, t_pk, t_qs, sync, s)) ||
+      (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)))
     return rc;
   // the decode launch's arrival counts (fused combine) zeroed by the selection
   // kernel
   const bool fuse = !gemm && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
   if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
-                                    ei, pp, zero_ints, s)))
+                                    ei, pp, zero_ints, s)) ||
+      (rc = mark(m, MOE_STAGE_SELECT, s)))
     return rc;
   // Decode (at most 128 tokens, the shape and device fit): mlp1, the encoding
   // of act and mlp2 in one launch.
@@ -489,8 +514,11 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
                               mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
                               (int)I, nk, alpha, limit, act_pk, y, sync, sync + E,
                               fuse ? w : nullptr, x, fuse ? out : nullptr, counts, s);
-    if (rc == MOE_OK && !fuse)
-      return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s);
+    if (rc == MOE_OK && (rc = mark(m, MOE_STAGE_DECODE, s))) return rc;
+    if (rc == MOE_OK && !fuse) {
+      if ((rc = moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s))) return rc;
+      return mark(m, MOE_STAGE_GATING, s);
+    }
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
   }
   if (gemm) {
@@ -502,6 +530,7 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
                                  1, alpha, limit, act, (int)I, s))) {
     return rc;
   }
+  if ((rc = mark(m, MOE_STAGE_MLP1, s))) return rc;
   if (gemm) {
     if ((rc = expert_matmul(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
                             mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f, 0.f,
@@ -516,13 +545,54 @@ int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_
                                  0.f, y, (int)H, s)))
       return rc;
   } else {
-    if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s))) return rc;
+    if ((rc = moe_launch_pieces(act, 1, nk, (int)I, kPiecesAct, act_pk, s)) ||
+        (rc = mark(m, MOE_STAGE_ACT_PIECES, s)))
+      return rc;
     if ((rc = moe_launch_mx_gemv(act_pk, nk, kPiecesAct, indptr, sp, (int)k, 2, 0, mlp2_blocks,
                                  mlp2_scales, mlp2_bias, (int)E, (int)H, (int)I, (int)n, nk, 0, 0.f,
                                  0.f, y, (int)H, s)))
       return rc;
   }
-  return moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, nullptr, s);
+  if ((rc = mark(m, MOE_STAGE_MLP2, s)) ||
+      (rc = moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, nullptr, s)))
+    return rc;
+  return mark(m, MOE_STAGE_GATING, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H, int64_t I,
+                      const uint16_t* norm_w, const uint16_t* gate_w, const uint16_t* gate_b,
+                      const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                      const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                      const uint8_t* mlp2_scales, const uint16_t* mlp2_bias, float eps,
+                      float alpha, float limit, uint16_t* out, void* workspace,
+                      size_t workspace_bytes, moe_stream_t stream) {
+  return block_forward_impl(x, n, E, k, H, I, norm_w, gate_w, gate_b, mlp1_blocks, mlp1_scales,
+                            mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, eps, alpha, limit, out,
+                            workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_block_forward_marked(const uint16_t* x, int64_t n, int64_t E, int64_t k, int64_t H,
+                             int64_t I, const uint16_t* norm_w, const uint16_t* gate_w,
+                             const uint16_t* gate_b, const uint8_t* mlp1_blocks,
+                             const uint8_t* mlp1_scales, const uint16_t* mlp1_bias,
+                             const uint8_t* mlp2_blocks, const uint8_t* mlp2_scales,
+                             const uint16_t* mlp2_bias, float eps, float alpha, float limit,
+                             uint16_t* out, void* workspace, size_t workspace_bytes,
+                             void* const* events, int n_events, int32_t* stages, int32_t* n_marks,
+                             moe_stream_t stream) {
+  if (!events || !stages || !n_marks) return MOE_ERR_NULL;
+  if (n_events < kMaxMarks) return MOE_ERR_SHAPE;
+  Marks m{(hipEvent_t const*)events, 0, {}};
+  const int rc = block_forward_impl(x, n, E, k, H, I, norm_w, gate_w, gate_b, mlp1_blocks,
+                                    mlp1_scales, mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias,
+                                    eps, alpha, limit, out, workspace, workspace_bytes, stream, &m);
+  for (int i = 0; i < m.used; ++i) stages[i] = m.stage[i];
+  *n_marks = m.used;
+  return rc;
 }
 
 int moe_set_decode_spin_limit(int polls) { return moe_decode_spin_limit_exchange(polls); }

@@ -3,9 +3,11 @@
 // and a fixed uniform sample 0.5 at engine.py:40).
 //
 // The algorithm sorts the logits in descending order, takes e = exp((l - max)
-// / T), and returns the first element whose cumulative probability over the
-// top-p mass exceeds the uniform sample, where the top-p mass is the sum up to
-// and including the element at which the running sum reaches top_p.
+// / T) and p = e / sum(e); it returns the largest element at once when the
+// uniform sample is below p_max / top_p, and otherwise the first element whose
+// cumulative probability over the top-p mass exceeds the uniform sample, where
+// the top-p mass is the sum up to and including the element at which the
+// running sum reaches top_p.
 //
 // The model's logits are bf16 values (the unembedding's bf16 output cast to
 // fp32, model/transformer.py:95-100), so a sequence has at most 65536 distinct
@@ -196,6 +198,16 @@ __global__ __launch_bounds__(kSegBins) void select_kernel(State* __restrict__ st
       segpre[kSegs] = acc;
     }
     __syncthreads();
+    // TVM's short cut (SampleTopPFromProb): uniform < p_max / top_p returns
+    // the argmax before the top-p mass is formed.  The largest value's weight
+    // is exp(0) = 1, so p_max = 1 / total.  Uniform over the workgroup.
+    if ((double)uniform < (1.0 / segpre[kSegs]) / (double)top_p) {
+      if (t == 0) {
+        s.pick_key = mk;
+        s.pick_rank = 1;
+      }
+      return;
+    }
     // The segment whose range [segpre[p], segpre[p + 1]) holds a crossing
     // (strict: the first with segpre[p] <= x < segpre[p + 1], else the first
     // with segpre[p] < x <= segpre[p + 1]), then the bin: the segment's 1024

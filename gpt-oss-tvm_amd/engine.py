@@ -118,12 +118,15 @@ class Engine:
         are fixed device buffers refreshed by ``begin_forward`` before each
         replay, every MoE block's workspace is reserved for one token, and the
         decode attention's split count is fixed at the pool's capacity
-        (``static_span``).  The warm-up and capture steps are rolled back."""
+        (``static_span``).  The workspaces the graph captures are held for the
+        life of the model, so a later, longer prefill or extend (which grows
+        the eager workspaces) leaves them in place.  The warm-up and capture
+        steps are rolled back."""
         c = self.paged_kv_cache
         c.static_span = c.num_pages * 16
-        c.reserve_decode(1, c.static_span)
+        c.reserve_decode(1, c.static_span, for_graph=True)
         for blk in self.model.model.block:
-            blk.mlp.reserve(1)
+            blk.mlp.reserve(1, for_graph=True)
         token = self._token.clone()  # the warm-up step samples over it
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream())

@@ -92,6 +92,7 @@ class PagedKVCache:
          self._page_indices) = views
         self.tables: ForwardTables | None = None
         self._decode_ws: torch.Tensor | None = None
+        self._decode_ws_held: list = []
         # decode attention's key bound for a captured forward (0: per forward)
         self.static_span = 0
 
@@ -102,11 +103,18 @@ class PagedKVCache:
         import attn_native
         need = attn_native.decode_workspace_bytes(batch, span)
         if self._decode_ws is None or self._decode_ws.numel() < need:
+            # a buffer a captured graph holds stays alive in _decode_ws_held
             self._decode_ws = attn_native.decode_workspace(batch, span, self.data.device)
         return self._decode_ws
 
-    def reserve_decode(self, batch: int, span: int) -> None:
-        self.decode_workspace(batch, span)
+    def reserve_decode(self, batch: int, span: int, for_graph: bool = False) -> None:
+        """Size the decode workspace now.  With ``for_graph`` the buffer is
+        kept alive as long as the cache: a graph captured after this call
+        holds its address, and a later, larger call gets a new buffer rather
+        than freeing the captured one."""
+        ws = self.decode_workspace(batch, span)
+        if for_graph and all(h is not ws for h in self._decode_ws_held):
+            self._decode_ws_held.append(ws)
 
     # -- sequences (vm.builtin.kv_state_* of engine.py:41-53) -------------------
     def layer(self, i: int) -> torch.Tensor:

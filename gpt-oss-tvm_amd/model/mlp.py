@@ -109,6 +109,7 @@ class MLPBlock(torch.nn.Module):
         self.mlp1_bias = packed(E, 2 * I, dt=tdt)
         self.mlp2_bias = packed(E, H, dt=tdt)
         self._ws: torch.Tensor | None = None
+        self._ws_held: list = []
 
     # -- parameters ---------------------------------------------------------
 
@@ -174,13 +175,22 @@ class MLPBlock(torch.nn.Module):
     def _workspace(self, n: int, device) -> torch.Tensor:
         need = self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
+            # A buffer that a captured graph holds stays alive in _ws_held;
+            # eager calls that need more get a new one.
             self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
         return self._ws
 
-    def reserve(self, n: int) -> None:
+    def reserve(self, n: int, for_graph: bool = False) -> None:
         """Size the module's workspace for calls of up to n tokens now, so that
-        forward() allocates no workspace later (e.g. under graph capture)."""
-        self._workspace(n, self.mlp1_weight_blocks.device)
+        forward() allocates no workspace later (e.g. under graph capture).
+
+        With ``for_graph`` the buffer is also kept alive for as long as the
+        module lives: a graph captured after this call holds its raw address,
+        and a later, larger eager call replaces ``_ws`` with a new buffer
+        instead of freeing the captured one."""
+        ws = self._workspace(n, self.mlp1_weight_blocks.device)
+        if for_graph and all(h is not ws for h in self._ws_held):
+            self._ws_held.append(ws)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x [b, s, hidden] bf16 -> x + MoE(RMSNorm(x)) (model/mlp.py:371-402).
@@ -210,6 +220,20 @@ class MLPBlock(torch.nn.Module):
         return _native.block_forward(x2d, self.packed_params(), self.experts_per_token,
                                      self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit,
                                      workspace, out=out)
+
+    def forward_marked(self, x: torch.Tensor, events) -> tuple[torch.Tensor, list[str]]:
+        """forward with ``events`` (8 torch.cuda.Event) recorded on the current
+        stream around the block's own launches: events[0] before the first,
+        events[i] after stage i.  Returns (output, the stage names that
+        events[1:] close).  The kernels and results are forward's."""
+        b, seq_len, dim = x.shape
+        x2 = x.reshape(b * seq_len, dim).contiguous()
+        ws = self._workspace(x2.shape[0], x2.device)
+        out = torch.empty_like(x2)
+        names = _native.block_forward_marked(x2, self.packed_params(), self.experts_per_token,
+                                             self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit,
+                                             ws, out, events)
+        return out.reshape(b, seq_len, dim), names[1:]
 
     def forward_staged(self, x: torch.Tensor, events: dict | None = None,
                        fused_decode: bool = False, pieces_epilogue: bool = False) -> dict:

@@ -59,7 +59,13 @@ _SIGS = {
     "moe_block_forward_noalloc": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _P, _F, _F, _F, _P, _P], _INT),
     "moe_set_decode_spin_limit": ([_INT], _INT),
+    "moe_block_forward_marked": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+                                  _P, _F, _F, _F, _P, _P, _SZ, _P, _INT, _P, _P, _P], _INT),
 }
+
+# MOE_STAGE_* of include/moe_gfx950.h
+STAGE_NAMES = ("start", "router_logits", "select", "decode", "mlp1", "act_pieces", "mlp2",
+               "gating")
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
@@ -378,6 +384,36 @@ def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
         _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
         workspace.numel(), _stream()), "moe_block_forward")
     return out
+
+
+def block_forward_marked(x, params: dict, k, eps, alpha, limit, workspace, out, events):
+    """block_forward with ``events`` (at least 8 torch.cuda.Event) recorded on
+    the current stream before the block's first launch and after each of its
+    stages.  Returns the stage names the recorded events close, in order:
+    events[i - 1] -> events[i] times stage i (i >= 1)."""
+    n, H = x.shape
+    E = params["gate.weight"].shape[0]
+    inter = params["mlp2_weight_blocks"].shape[2] * 32
+    _expect(x, "x", torch.bfloat16)
+    _expect(out, "out", torch.bfloat16, (n, H))
+    _expect(workspace, "workspace", torch.uint8)
+    if len(events) < 8:
+        raise ValueError("block_forward_marked needs 8 events")
+    for ev in events:
+        if ev.cuda_event == 0:
+            ev.record()          # torch creates its events on first record
+    handles = (ctypes.c_void_p * len(events))(*[ev.cuda_event for ev in events])
+    stages = (ctypes.c_int32 * 8)()
+    used = ctypes.c_int32(0)
+    _check(_lib.moe_block_forward_marked(
+        _ptr(x), n, E, k, H, inter, _ptr(params["norm.weight"]), _ptr(params["gate.weight"]),
+        _ptr(params["gate.bias"]), _ptr(params["mlp1_weight_blocks"]),
+        _ptr(params["mlp1_weight_scales"]), _ptr(params["mlp1_bias"]),
+        _ptr(params["mlp2_weight_blocks"]), _ptr(params["mlp2_weight_scales"]),
+        _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
+        workspace.numel(), handles, len(events), stages, ctypes.byref(used), _stream()),
+        "moe_block_forward_marked")
+    return [STAGE_NAMES[stages[i]] for i in range(used.value)]
 
 
 def block_forward_noalloc(x, params: dict, k, eps, alpha, limit, out):

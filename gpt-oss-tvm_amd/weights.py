@@ -13,16 +13,24 @@ A layer's MoE parameters live under ``block.{i}.mlp.`` (the reference's
 Tensors land in torch-ROCm device memory; no DLPack hop is needed because the
 kernels take raw device pointers.
 
-Loading is checked before anything is copied: every tensor must exist, match
-its parameter's shape and dtype, and every E8M0 scale byte must lie in
-[2, 252].  Inside that range the expert matmuls (which feed the scale bytes
-to the block-scaled MFMA) give exactly the reference's dequantised weights
-(model/mlp.py:297-298, ``exp2(s - 127)``); outside it they do not (s = 255
-is +inf in the reference and NaN in the hardware's E8M0; s in {0, 1, 253,
-254} reach fp32 subnormals or overflow), so such a checkpoint is refused.
+Loading is checked before anything is copied: every tensor must exist and
+match its parameter's shape and dtype.  Every E8M0 scale byte is accepted, as
+the reference accepts it.  Inside [2, 252] the expert matmuls (which feed the
+scale bytes to the block-scaled MFMA) use exactly the reference's dequantised
+weights (model/mlp.py:297-298, ``exp2(s - 127)``).  Outside it a block that
+holds only zeros (every e2m1 code +-0) still contributes exactly zero, except
+at s = 255.  A block with a nonzero value can differ:
+  * s in {0, 1}: the weights are fp32 subnormals or the smallest normals
+    (2^-128 ... 6 x 2^-126), whose products the matrix cores may flush, an
+    absolute difference below 2^-120 per product;
+  * s in {253, 254}: the weights are 2^125 or more (+-inf in the reference
+    for the larger codes), so any dot product that uses them overflows in both;
+  * s = 255: +inf in the reference, NaN in the hardware's E8M0.
+Such blocks are counted and reported with a RuntimeWarning, not refused.
 """
 from __future__ import annotations
 
+import warnings
 from pathlib import Path
 from typing import Iterable
 
@@ -34,6 +42,18 @@ BYTES_PER_BLOCK = 16
 
 # E8M0 scale bytes for which the fused matmuls reproduce the reference exactly.
 SCALE_MIN, SCALE_MAX = 2, 252
+
+
+def blocks_outside_range(blocks: torch.Tensor, scales: torch.Tensor) -> int:
+    """MXFP4 blocks ([..., G, 16] u8 codes, [..., G] E8M0 bytes) on which the
+    fused matmuls may differ from the reference dequantisation: a scale byte
+    outside [SCALE_MIN, SCALE_MAX] on a block with a nonzero value, or 255 on
+    any block (0 x inf is NaN in the reference)."""
+    out = (scales < SCALE_MIN) | (scales > SCALE_MAX)
+    if not bool(out.any()):
+        return 0
+    nonzero = ((blocks & 0x77) != 0).any(dim=-1)   # e2m1 magnitude bits of both nibbles
+    return int((out & (nonzero | (scales == 255))).sum())
 
 _RENAMES = (
     ("model.", ""),
@@ -91,23 +111,30 @@ class TorchCheckpoint:
 
         ``prefix`` is prepended to each parameter name before the mapping
         (``mlp_prefix(i)`` for layer i's MoE block).  Everything is validated
-        first -- presence (KeyError), shape and dtype (ValueError), the E8M0
-        scale range (ValueError) -- so a refused checkpoint leaves the module
-        untouched.
+        first -- presence (KeyError), shape and dtype (ValueError) -- so a
+        refused checkpoint leaves the module untouched.  MXFP4 blocks whose
+        scale byte lies outside [2, 252] (``blocks_outside_range``) are
+        loaded and reported with a RuntimeWarning.
         """
         named = [(prefix + name, p) for name, p in module.named_parameters()]
         srcs = self.load_packed_params(named)
+        by_name = dict(zip((n for n, _ in named), srcs))
         for (name, p), src in zip(named, srcs):
             if tuple(src.shape) != tuple(p.shape) or src.dtype != p.dtype:
                 raise ValueError(f"{convert_key(name)}: checkpoint has {tuple(src.shape)} "
                                  f"{src.dtype}, parameter is {tuple(p.shape)} {p.dtype}")
+        for name, src in by_name.items():
             if name.endswith("weight_scales") and src.numel():
-                lo, hi = int(src.min()), int(src.max())
-                if lo < SCALE_MIN or hi > SCALE_MAX:
-                    raise ValueError(
-                        f"{convert_key(name)}: E8M0 scale bytes span [{lo}, {hi}], outside "
-                        f"[{SCALE_MIN}, {SCALE_MAX}] where the MXFP4 matmuls reproduce the "
-                        "reference dequantisation (model/mlp.py:297-298)")
+                blocks = by_name.get(name[:-len("scales")] + "blocks")
+                bad = blocks_outside_range(blocks, src) if blocks is not None else 0
+                if bad:
+                    lo, hi = int(src.min()), int(src.max())
+                    warnings.warn(
+                        f"{convert_key(name)}: {bad} MXFP4 blocks with nonzero values have E8M0 "
+                        f"scale bytes outside [{SCALE_MIN}, {SCALE_MAX}] (bytes span [{lo}, {hi}]);"
+                        " on them the matmuls may differ from the reference dequantisation "
+                        "(model/mlp.py:297-298): flushed subnormal products at 0 and 1, "
+                        "overflow at 253 and 254, NaN instead of inf at 255", RuntimeWarning)
         with torch.no_grad():
             for (_, p), src in zip(named, srcs):
                 p.copy_(src)
@@ -132,7 +159,7 @@ def scale_range(module: torch.nn.Module) -> tuple[int, int]:
     """(min, max) E8M0 scale byte over a block's MXFP4 weights.
 
     The fused matmuls dequantise exactly while 2 <= s <= 252 (every e2m1 value
-    times 2^(s-127) is a normal bf16); load_into refuses checkpoints outside.
+    times 2^(s-127) is a normal bf16); load_into warns about blocks outside.
     """
     lo, hi = 255, 0
     for name, p in module.named_parameters():

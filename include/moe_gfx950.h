@@ -272,6 +272,38 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
                       float alpha, float limit, uint16_t* out, void* workspace,
                       size_t workspace_bytes, moe_stream_t stream);
 
+/* Stages of moe_block_forward, in launch order; which ones run depends on n. */
+#define MOE_STAGE_START 0         /* before the first launch */
+#define MOE_STAGE_ROUTER_LOGITS 1 /* RMSNorm, t and its pieces, router logits */
+#define MOE_STAGE_SELECT 2        /* top-k, softmax and the grouping */
+#define MOE_STAGE_DECODE 3        /* mlp1 + SwiGLU + act pieces + mlp2 in one launch (+ combine, n <= 32) */
+#define MOE_STAGE_MLP1 4          /* mlp1 + SwiGLU (prefill GEMM: act pieces in its epilogue) */
+#define MOE_STAGE_ACT_PIECES 5    /* act's fp8 pieces (GEMV path above 2 pairs per expert) */
+#define MOE_STAGE_MLP2 6          /* mlp2 */
+#define MOE_STAGE_GATING 7        /* gated combine + residual */
+
+/*
+ * moe_block_forward with the caller's hipEvents (hipEvent_t, created by the
+ * caller, at least 8) recorded on `stream`: events[0] before the block's
+ * first launch, then one after each stage.  stages[i] (int32, 8 entries)
+ * receives the MOE_STAGE_* that events[i] closes and *n_marks the number of
+ * events recorded, so the elapsed time between events[i - 1] and events[i]
+ * is stage stages[i].  The launches and results are those of
+ * moe_block_forward; only the event records are added.
+ * No reference counterpart: a measurement hook for the block's own kernels
+ * (the reference's operators are timed by TVM's profiler).
+ */
+MOE_API int moe_block_forward_marked(const uint16_t* x, int64_t n, int64_t E, int64_t k,
+                                     int64_t H, int64_t I, const uint16_t* norm_w,
+                                     const uint16_t* gate_w, const uint16_t* gate_b,
+                                     const uint8_t* mlp1_blocks, const uint8_t* mlp1_scales,
+                                     const uint16_t* mlp1_bias, const uint8_t* mlp2_blocks,
+                                     const uint8_t* mlp2_scales, const uint16_t* mlp2_bias,
+                                     float eps, float alpha, float limit, uint16_t* out,
+                                     void* workspace, size_t workspace_bytes,
+                                     void* const* events, int n_events, int32_t* stages,
+                                     int32_t* n_marks, moe_stream_t stream);
+
 /*
  * moe_block_forward without a workspace argument, for callers that cannot
  * allocate (code under HIP graph capture, serving loops, harnesses that

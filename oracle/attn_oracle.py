@@ -259,11 +259,13 @@ def make_attn_params(seed: int, hidden: int = 2880, hq: int = N_Q_HEADS, hkv: in
 def sample_top_p_from_logits(logits: np.ndarray, temperature: float, top_p: float,
                              uniform_sample: float) -> int:
     """TVM's SampleTopPFromLogits, restated: sort descending by logit; argmax
-    if temperature < 1e-6; else e = exp((l - max) * (1 / T)), probabilities
-    e / sum(e) accumulated in sorted order, the top-p mass = the running sum up
-    to and including the element before which it was still below top_p, and
-    the first element whose cumulative probability over the top-p mass
-    exceeds uniform_sample is returned (the first maximum otherwise).
+    if temperature < 1e-6; else e = exp((l - max) * (1 / T)) and
+    probabilities p = e / sum(e); the first maximum if uniform_sample <
+    p_max / top_p (SampleTopPFromProb's short cut, taken before any sum); else
+    the probabilities accumulated in sorted order, the top-p mass = the running
+    sum up to and including the element before which it was still below
+    top_p, and the first element whose cumulative probability over the top-p
+    mass exceeds uniform_sample is returned (the first maximum otherwise).
 
     Canonical numerics: the exponent's argument in fp32 as written, exp
     rounded once to fp32 (through fp64), and the sums exact (fp64).  TVM adds
@@ -280,10 +282,13 @@ def sample_top_p_from_logits(logits: np.ndarray, temperature: float, top_p: floa
     arg = ((ls - ls[0]) * scale).astype(np.float32)
     e = np.exp(arg.astype(np.float64)).astype(np.float32).astype(np.float64)
     total = e.sum()
+    u32, tp32 = float(np.float32(uniform_sample)), float(np.float32(top_p))
+    if u32 < (1.0 / total) / tp32:          # e[0] = exp(0) = 1: p_max = 1 / total
+        return int(order[0])
     cums = np.cumsum(e) / total
     before = np.concatenate([[0.0], cums[:-1]])
-    top = cums[np.nonzero(before < float(np.float32(top_p)))[0][-1]]
-    hit = np.nonzero(float(np.float32(uniform_sample)) < cums / top)[0]
+    top = cums[np.nonzero(before < tp32)[0][-1]]
+    hit = np.nonzero(u32 < cums / top)[0]
     return int(order[hit[0]] if hit.size else order[0])
 
 

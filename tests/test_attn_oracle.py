@@ -148,14 +148,20 @@ def _serial_sampler(logits, temperature, top_p, u):
     ex = [float(np.float32(math.exp(float(np.float32((np.float32(logits[i]) - mx) * scale)))))
           for i in idx]
     total = math.fsum(ex)
+    probs = [v / total for v in ex]
+    u, top_p = float(np.float32(u)), float(np.float32(top_p))
+    if u < probs[0] / top_p:            # SampleTopPFromProb's short cut
+        return idx[0]
     cum, top, cums = 0.0, 0.0, []
-    for v in ex:
-        if cum < float(np.float32(top_p)):
-            top = cum + v / total
-        cum += v / total
+    for p in probs:
+        if cum < top_p:
+            top += p
+        else:
+            break
+        cum += p
         cums.append(cum)
     for i, c in zip(idx, cums):
-        if float(np.float32(u)) < c / top:
+        if u < c / top:
             return i
     return idx[0]
 
@@ -178,8 +184,29 @@ def test_sampler_closed_cases():
     p = e / e.sum()
     top = p[1] + p[2]
     assert p[1] < 0.9 <= top          # the running sum reaches top_p at the second leader
-    assert A.sample_top_p_from_logits(logits, 1.0, 0.9, float(p[1] / top) + 1e-3) == 2
+    # past both the first leader's share of the top-p mass and p_max / top_p
+    cut = max(float(p[1] / top), float(p[1] / 0.9))
+    assert A.sample_top_p_from_logits(logits, 1.0, 0.9, cut + 1e-3) == 2
     assert A.sample_top_p_from_logits(logits, 1.0, 0.9, float(p[1] / top) - 1e-3) == 1
+
+
+def test_sampler_short_cut_to_argmax():
+    """TVM's SampleTopPFromProb returns the argmax when uniform < p_max /
+    top_p, before it forms the top-p mass.  Here p_max is about 0.47 and the
+    top-p mass is the whole mass: at the engine's u = 0.5 and top_p = 0.9,
+    u < 0.47 / 0.9 = 0.52 picks the leader, although u exceeds the leader's
+    share of the top-p mass (0.47), where the crossing alone would pick the
+    second element."""
+    logits = np.array([2.0, 1.875, 0.5625], dtype=np.float32)   # bf16 values
+    e = np.exp(logits.astype(np.float64) - 2.0)
+    p = e / e.sum()
+    cums = np.cumsum(p)
+    top = cums[np.nonzero(np.concatenate([[0.0], cums[:-1]]) < 0.9)[0][-1]]
+    assert 0.45 < p[0] < 0.5 and p[0] / top < 0.5 < p[0] / 0.9
+    assert A.sample_top_p_from_logits(logits, 1.0, 0.9, 0.5) == 0
+    assert _serial_sampler(logits, 1.0, 0.9, 0.5) == 0
+    # above p_max / top_p the crossing decides: the second element
+    assert A.sample_top_p_from_logits(logits, 1.0, 0.9, float(p[0] / 0.9) + 1e-3) == 1
 
 
 def _small_params(seed, H=64):

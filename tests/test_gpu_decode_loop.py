@@ -77,6 +77,20 @@ def test_sampler_ties_take_index_order(A):
         assert got == AO.sample_top_p_from_logits(logits[0], 1.0, 0.9, u)
 
 
+def test_sampler_short_cut_to_argmax(A):
+    """TVM's SampleTopPFromProb returns the argmax when uniform < p_max /
+    top_p.  Three leaders with p_max about 0.47 over a flat tail (-30: no
+    mass to speak of): at u = 0.5, top_p = 0.9 the leader; just above
+    p_max / top_p the second one (the crossing)."""
+    logits = np.full((1, 4096), -30.0, dtype=np.float32)
+    logits[0, [700, 20, 3000]] = [2.0, 1.875, 0.5625]
+    ws = A.sample_workspace(1)
+    dev = bf16_dev(O.f32_to_bf16(logits))
+    for u, want in ((0.5, 700), (0.45, 700), (0.53, 20), (0.95, 3000)):
+        got = int(A.sample_top_p(dev, 1.0, 0.9, u, ws).item())
+        assert got == want == AO.sample_top_p_from_logits(logits[0], 1.0, 0.9, u), (u, got)
+
+
 def _model_from_oracle(mp: AO.ModelParams, config):
     from engine import Engine
     eng = Engine(config=config, max_total_seq_len=1024)
@@ -236,3 +250,46 @@ def test_graphed_decode_equals_eager(A, small_model):
         np.testing.assert_array_equal(got, ref_logits[k])
         assert int(t.item()) == toks[k], k
     assert eng.get_kv_total_seq_len() == 140 + steps
+
+
+def test_captured_step_survives_a_longer_extend(A, small_model):
+    """The captured decode step holds the raw addresses of every MoE block's
+    workspace.  A later turn that extends the sequence by more tokens than any
+    call before the capture (the reference's chat loop, chat.py:157-162) grows
+    the eager workspaces; the captured ones must stay alive and untouched by
+    eager work.  Sentinel buffers of the captured workspaces' sizes are
+    allocated after the extend (torch's allocator would hand a freed workspace
+    to them) and must be intact after the replays, and the replayed steps must
+    equal eager steps bit for bit."""
+    cfg, mp = small_model
+    eng = _model_from_oracle(mp, cfg)
+    rng = np.random.default_rng(904)
+    seq = eng.begin_sequence()
+    eng._token.copy_(eng.sample_device(
+        eng.prefill(rng.integers(0, cfg.vocab_size, 12).astype(np.int32), seq)))
+    eng.capture_decode(seq)
+    blocks = [blk.mlp for blk in eng.model.model.block]
+    captured = [m._ws.data_ptr() for m in blocks]
+    sizes = [m._ws.numel() for m in blocks]
+    logits = eng.extend(rng.integers(0, cfg.vocab_size, 200).astype(np.int32), seq)
+    assert all(m._ws.data_ptr() != p for m, p in zip(blocks, captured))   # grown
+    assert all(any(h.data_ptr() == p for h in m._ws_held) for m, p in zip(blocks, captured))
+    sentinels = [torch.full((sz,), 0x5A, dtype=torch.uint8, device="cuda") for sz in sizes]
+    tok0 = eng.sample_device(logits).clone()
+    eng._token.copy_(tok0)
+    steps = 3
+    graph_logits, toks = [], []
+    for _ in range(steps):
+        t = eng.decode_sample(seq)
+        graph_logits.append(eng.graph_logits.view(-1).cpu().numpy().copy())
+        toks.append(int(t.item()))
+    torch.cuda.synchronize()
+    for s in sentinels:
+        assert bool((s == 0x5A).all().item())
+    eng.popn(seq, steps)
+    eng._token.copy_(tok0)
+    for k in range(steps):
+        lg = eng.decode(eng._token, seq)
+        np.testing.assert_array_equal(lg.view(-1).cpu().numpy(), graph_logits[k])
+        assert int(eng.sample_device(lg).item()) == toks[k], k
+    assert eng.get_kv_total_seq_len() == 12 + 200 + steps

@@ -6,7 +6,8 @@ These tests write checkpoint-named safetensors files (the names the real
 gpt-oss checkpoint uses: block.N.mlp.mlp1_weight.blocks, norm.scale, ...),
 load them into MLPBlocks held in host memory, and cover the error paths:
 a missing file or tensor, a shape or dtype mismatch, and E8M0 scale bytes
-outside the range the fused matmuls reproduce exactly.
+outside the range the fused matmuls reproduce exactly (loaded, with a
+warning that counts the blocks concerned).
 """
 import os
 
@@ -129,18 +130,44 @@ def test_shape_and_dtype_mismatch(modules, tmp_path, what):
     assert torch.equal(blk.gate.weight.detach(), before)
 
 
-@pytest.mark.parametrize("bad", [0, 1, 253, 255])
-def test_scale_range_refused(modules, tmp_path, bad):
-    """Scale bytes where the fused MFMA path and the reference dequant differ
-    (s = 255: +inf in the reference, NaN in E8M0 hardware) are refused."""
+@pytest.mark.parametrize("bad", [0, 1, 253, 254, 255])
+def test_scale_bytes_outside_range_loaded_with_warning(modules, tmp_path, bad):
+    """Scale bytes where the fused MFMA path and the reference dequant can
+    differ (s = 255: +inf in the reference, NaN in E8M0 hardware; 0, 1:
+    subnormal weights; 253, 254: overflow) are loaded, as the reference loads
+    them, with a warning that counts the blocks."""
     W, cfg, MLPBlock = modules
     t = _layer_tensors(0, 62)
     key = "block.0.mlp.mlp1_weight.scales"
     t[key][1, 2, 1] = bad
+    t["block.0.mlp.mlp1_weight.blocks"][1, 2, 1, 0] = 0x21      # the block holds nonzero values
     save_file(t, os.path.join(tmp_path, "model.safetensors"))
     blk = MLPBlock(cfg, device="cpu")
-    with pytest.raises(ValueError, match=r"mlp1_weight.scales.*outside \[2, 252\]"):
+    with pytest.warns(RuntimeWarning, match=r"mlp1_weight.scales: 1 MXFP4 blocks .*outside \[2, 252\]"):
         W.TorchCheckpoint(tmp_path, "cpu").load_into(blk, prefix=W.mlp_prefix(0))
+    assert int(blk.mlp1_weight_scales[1, 2, 1]) == bad
+    assert torch.equal(blk.mlp1_weight_blocks.detach(), t["block.0.mlp.mlp1_weight.blocks"])
+
+
+@pytest.mark.parametrize("bad", [0, 1, 253, 254])
+def test_zero_blocks_outside_range_are_exact(modules, tmp_path, bad):
+    """A block of zeros (codes 0 and 8, +-0) contributes exactly zero at any
+    scale byte but 255: no warning."""
+    import warnings
+    W, cfg, MLPBlock = modules
+    t = _layer_tensors(0, 64)
+    t["block.0.mlp.mlp2_weight.scales"][3, 5, 0] = bad
+    t["block.0.mlp.mlp2_weight.blocks"][3, 5, 0, :] = torch.tensor([0x00, 0x80, 0x08, 0x88] * 4,
+                                                                  dtype=torch.uint8)
+    save_file(t, os.path.join(tmp_path, "model.safetensors"))
+    blk = MLPBlock(cfg, device="cpu")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        W.TorchCheckpoint(tmp_path, "cpu").load_into(blk, prefix=W.mlp_prefix(0))
+    assert W.scale_range(blk)[0 if bad < 2 else 1] == bad
+    assert W.blocks_outside_range(blk.mlp2_weight_blocks, blk.mlp2_weight_scales) == 0
+    blk.mlp2_weight_scales.data[3, 5, 0] = 255                     # 0 x inf: NaN in the reference
+    assert W.blocks_outside_range(blk.mlp2_weight_blocks, blk.mlp2_weight_scales) == 1
 
 
 @pytest.mark.parametrize("edge", [2, 252])

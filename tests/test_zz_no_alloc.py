@@ -5,6 +5,8 @@ Both run the same kernels, so the outputs must agree bit for bit; they are
 also held to the oracle's block bar.  Two calls in a row, the second with
 fewer tokens (the static scratch then holds the first call's contents), and
 one call past the scratch limit, which must be refused before any launch.
+Neither torch's allocator nor the device (its free bytes, which a hipMalloc
+inside the library would lower) may see an allocation after the first call.
 """
 import numpy as np
 import pytest
@@ -24,16 +26,20 @@ def test_noalloc_matches_workspace_entry_point():
     blk = make_block(p)
     params = blk.packed_params()
     H = 2880
-    for n, seed in ((200, 401), (64, 402), (5, 403)):
+    for i, (n, seed) in enumerate(((200, 401), (64, 402), (5, 403))):
         print(f"noalloc n={n}", flush=True)
         x = O.make_input(seed, n)
         xd = bf16_dev(x)
         ref = blk(xd.view(1, n, H)).view(n, H)
         out = torch.full((n, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
         before = torch.cuda.memory_allocated()
+        free_before = torch.cuda.mem_get_info()[0]   # the device's free bytes (hipMemGetInfo)
         native.block_forward_noalloc(xd, params, 4, 1e-5, 1.702, 7.0, out)
         torch.cuda.synchronize()
         assert torch.cuda.memory_allocated() == before
+        if i:   # after the first call (runtime set-up): no device allocation at all
+            assert torch.cuda.mem_get_info()[0] == free_before
         got = host_bf16(out)
         assert np.array_equal(got, host_bf16(ref))
         m = O.compare_outputs(got, O.block_forward(x, p).out)
