@@ -488,6 +488,39 @@ def run_decode_loop(dev, prompt_len: int = 128, steps: int = 32) -> dict:
     return res
 
 
+def hbm_calibration(dev, reps: int = 10) -> dict:
+    """Achievable HBM read bandwidth: the library's streaming-read kernel
+    (moe_hbm_read) over 2 and 4 GiB buffers (far beyond the 256 MB MALL),
+    swept over grid sizes and loads in flight; HIP events around `reps` reads
+    each, the best configuration reported with the whole sweep."""
+    import torch
+
+    import moe_native
+    sink = torch.zeros(1 << 15, dtype=torch.int32, device=dev)
+    sweep = []
+    for gib in (2, 4):
+        buf = torch.empty(gib << 30, dtype=torch.uint8, device=dev)
+        buf.fill_(0x5A)
+        for grid in (1024, 2048, 4096, 8192, 16384, 32768):
+            for unroll in (4, 8, 16):
+                moe_native.hbm_read(buf, grid, unroll, sink)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(reps):
+                    moe_native.hbm_read(buf, grid, unroll, sink)
+                b.record()
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / reps
+                sweep.append({"gib": gib, "grid": grid, "unroll": unroll, "us": round(us, 1),
+                              "gbs": round(buf.numel() / (us * 1e-6) / 1e9, 1)})
+        del buf
+    best = max(sweep, key=lambda r: r["gbs"])
+    log(f"hbm calibration: best {best['gbs']} GB/s ({best})")
+    return {"metric": "achievable HBM read bandwidth (streaming read, moe_hbm_read)",
+            "best_gbs": best["gbs"], "best": best, "peak_gbs": HBM_PEAK_GBS,
+            "best_frac_of_peak": round(best["gbs"] / HBM_PEAK_GBS, 4), "sweep": sweep}
+
+
 def mfma_calibration(dev, size: int = 8192, reps: int = 20) -> dict:
     """The matrix cores' achievable rate as the vendor library reaches it:
     torch's bf16 matmul and fp8 scaled_mm (hipBLASLt) on size^3, timed with
@@ -611,6 +644,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 512 MiB (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
+    ap.add_argument("--hbm-calibration", action="store_true",
+                    help="only sweep the streaming-read kernel over 2 and 4 GiB buffers (the "
+                         "achievable HBM read bandwidth), print it and exit")
     ap.add_argument("--mfma-calibration", action="store_true",
                     help="only time library GEMMs of 8192^3 through torch (hipBLASLt: bf16 "
                          "matmul, fp8 scaled_mm) as the matrix cores' achievable rate, then exit")
@@ -622,6 +658,9 @@ def main() -> int:
 
     import torch
 
+    if args.hbm_calibration:
+        print(json.dumps(hbm_calibration(torch.device("cuda:0"))), flush=True)
+        return 0
     if args.copy_calibration:
         src = torch.ones(512 << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)

@@ -29,6 +29,12 @@ int moe_select_chunks(int n);
 int moe_launch_select_group(const float* logits, int n, int E, int k, void* idx_out, void* w_out,
                             void* counts, void* indptr, void* sorted_pairs, void* token_indices,
                             void* expert_ids, void* pair_pos, int zero_ints, hipStream_t stream);
+int moe_launch_router_select(const void* x, const void* norm_w, const void* gate_w,
+                             const void* gate_b, int n, int H, int E, int k, float eps, void* t_out,
+                             float* logits, void* pq, void* pqs, void* zero_e, void* idx_out,
+                             void* w_out, void* indptr, void* sorted_pairs, void* token_indices,
+                             void* expert_ids, void* pair_pos, void* zero, int zero_ints,
+                             void* arrive, hipStream_t stream);
 size_t moe_pieces_q_bytes(int64_t rows, int64_t K, int pieces);
 size_t moe_pieces_total_bytes(int64_t rows, int64_t K, int pieces);
 int moe_launch_pieces(const void* x, int x_is_f32, int rows, int K, int pieces, void* packed,
@@ -56,6 +62,8 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
                       hipStream_t stream);
+int moe_launch_hbm_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink,
+                        hipStream_t stream);
 }
 
 namespace {
@@ -124,6 +132,12 @@ int expert_matmul(const void* packed, int rows, int pieces, const int32_t* indpt
                             alpha, limit, out, out_ld, s);
 }
 
+// Bytes [0, kCounterBytes) of the block workspace, at the same place for
+// every n: counters that are zero before the first call and that every call
+// leaves at zero (int 0: the router launch's finished workgroups).
+constexpr size_t kCounterBytes = 256;
+constexpr int kCounterRouter = 0;
+
 constexpr int kNumRegions = 15;
 constexpr int kRegionSync = 14;  // decode launch: E completion counts, then the status word
 constexpr int kPiecesT = 2;    // fp8 pieces of the bf16 normalised tokens (exact)
@@ -166,7 +180,7 @@ void layout(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I, size_t off[kN
       // counts and its status word (zeroed by the logits kernel)
       (size_t)(E + 1) * 4,
   };
-  size_t o = 0;
+  size_t o = kCounterBytes;
   for (int i = 0; i < kNumRegions; ++i) {
     off[i] = o;
     o = round_up(o + sizes[i], 256);
@@ -492,18 +506,31 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   // launch's counts and status); then top-k, softmax and grouping
   void* t_qs = (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT);
   if ((rc = mark(m, MOE_STAGE_START, s))) return rc;
-  if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
-                                     logits, t_pk, t_qs, sync, s)) ||
-      (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)))
-    return rc;
   // the decode launch's arrival counts (fused combine) zeroed by the selection
-  // kernel
   const bool fuse = !gemm && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
-  if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp, ti,
-                                    ei, pp, zero_ints, s)) ||
-      (rc = mark(m, MOE_STAGE_SELECT, s)))
+  // decode sizes: the logits launch's last workgroup runs the selection and
+  // grouping (one launch); otherwise two launches
+  rc = MOE_ERR_UNSUPPORTED;
+  if (!gemm && n <= 128) {
+    int32_t* arrive = (int32_t*)ws + kCounterRouter;
+    rc = moe_launch_router_select(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, (int)k, eps,
+                                  t, logits, t_pk, t_qs, sync, idx, w, indptr, sp, ti, ei, pp,
+                                  counts, zero_ints, arrive, s);
+    if (rc == MOE_OK && (rc = mark(m, MOE_STAGE_ROUTER, s))) return rc;
+  }
+  if (rc == MOE_ERR_UNSUPPORTED) {
+    if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
+                                       logits, t_pk, t_qs, sync, s)) ||
+        (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)))
+      return rc;
+    if ((rc = moe_launch_select_group(logits, (int)n, (int)E, (int)k, idx, w, counts, indptr, sp,
+                                      ti, ei, pp, zero_ints, s)) ||
+        (rc = mark(m, MOE_STAGE_SELECT, s)))
+      return rc;
+  } else if (rc) {
     return rc;
+  }
   // Decode (at most 128 tokens, the shape and device fit): mlp1, the encoding
   // of act and mlp2 in one launch.
   if (!gemm && n <= 128) {
@@ -597,6 +624,15 @@ int moe_block_forward_marked(const uint16_t* x, int64_t n, int64_t E, int64_t k,
 
 int moe_set_decode_spin_limit(int polls) { return moe_decode_spin_limit_exchange(polls); }
 
+int moe_hbm_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink,
+                 moe_stream_t stream) {
+  if (!src || !sink) return MOE_ERR_NULL;
+  if (bytes < 16 || bytes % 16 || grid < 1 || grid > (1 << 20)) return MOE_ERR_SHAPE;
+  if (!aligned16(src)) return MOE_ERR_ALIGN;
+  if (unroll != 4 && unroll != 8 && unroll != 16) return MOE_ERR_UNSUPPORTED;
+  return moe_launch_hbm_read(src, bytes, grid, unroll, sink, as_stream(stream));
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
@@ -615,8 +651,14 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<uintptr_t> g_scratch_addr[kMaxDevices];  // 0: not looked up yet
 
-// Device address of the current device's scratch.
-int scratch_address(void** out) {
+// Zeroes the workspace counters (a kernel, not a memset: the first call may
+// be captured in a graph).
+__global__ void zero_counters_kernel(uint32_t* p) { p[threadIdx.x] = 0u; }
+
+// Device address of the current device's scratch; the first lookup on a
+// device also zeroes the scratch's counters on `s`, ahead of the call's
+// kernels.
+int scratch_address(void** out, hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return MOE_ERR_LAUNCH;
   if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_UNSUPPORTED;
@@ -625,6 +667,9 @@ int scratch_address(void** out) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
       return MOE_ERR_LAUNCH;
+    hipLaunchKernelGGL(zero_counters_kernel, dim3(1), dim3(kCounterBytes / 4), 0, s,
+                       (uint32_t*)p);
+    if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
     a = (uintptr_t)p;
     g_scratch_addr[dev].store(a, std::memory_order_release);  // same value if raced
   }
@@ -650,10 +695,10 @@ int moe_block_forward_noalloc(const uint16_t* x, int64_t n, int64_t E, int64_t k
   layout(n, E, k, H, I, off, &total);
   if (total > kScratchBytes) return MOE_ERR_TOO_LARGE;
   void* ws = nullptr;
-  if ((rc = scratch_address(&ws))) return rc;
+  if ((rc = scratch_address(&ws, as_stream(stream)))) return rc;
   // every region the kernels read is written earlier in the same call (the
-  // counters are zeroed by the first kernel), so stale contents of the last
-  // call do no harm
+  // per-call counters are zeroed by the first kernel, the persistent ones are
+  // left at zero by every call), so stale contents of the last call do no harm
   return moe_block_forward(x, n, E, k, H, I, norm_w, gate_w, gate_b, mlp1_blocks, mlp1_scales,
                            mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, eps, alpha, limit, out,
                            ws, kScratchBytes, stream);

@@ -271,12 +271,37 @@ __global__ __launch_bounds__(64 * W) void moe_router_kernel(
 // interleaved 16-byte chunks of the slice (any K order serves, as long as
 // both operands use the same).  The slices' partial sums are added in slice
 // order through LDS, then rounded as above.
-template <bool kPieces, int S, int W, int TT, bool kMfma>
+// Outputs of the top-k, softmax and grouping that the last workgroup of the
+// logits launch runs (kSel): mlc-llm gating_softmax_topk + moe_cumsum /
+// get_indices / get_indptr (model/mlp_optimized.py:118-148).
+struct SelectArgs {
+  int k;
+  int32_t* idx;
+  uint16_t* w;
+  int32_t* indptr;
+  int32_t* sorted_pairs;
+  int32_t* token_indices;
+  int32_t* expert_ids;
+  int32_t* pair_pos;
+  int32_t* zero;     // ints zeroed on the way (the decode launch's arrival counts)
+  int zero_ints;
+  int32_t* arrive;   // workgroups done: zero before the first launch, left zero
+};
+
+// Keys and tokens the fused selection holds in LDS (n * roundup(E, 32)).
+constexpr int kFusedSelKeys = 4096;
+constexpr int kFusedSelTok = 128;
+
+__device__ void select_group_last(const float* logits, int n, int E, const SelectArgs& sel);
+
+template <bool kPieces, int S, int W, int TT, bool kMfma, bool kSel = false>
 __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
     const uint16_t* __restrict__ gate_w, const uint16_t* __restrict__ gate_b, int n, int H, int E,
     float eps, uint16_t* __restrict__ t_out, float* __restrict__ logits,
-    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs, int epw, int32_t* __restrict__ zero_e) {
+    uint8_t* __restrict__ pq, uint8_t* __restrict__ pqs, int epw, int32_t* __restrict__ zero_e,
+    SelectArgs sel) {
+  static_assert(!(kSel && kMfma), "the fused selection follows the VALU dots");
   constexpr int kChunks = 64 * S;                // 16-byte chunks of a row, at most
   constexpr int J = (kChunks + 64 * W - 1) / (64 * W);  // chunks per thread and token
   __shared__ u32x4 t_lds[TT][kChunks];
@@ -497,13 +522,35 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
       const double a = wave_sum_f64(acc[tt]);
       if (lane == 0 && tt < ntok) {
         const float d = bf2f(f64_to_bf16_via_f32(a));
-        logits[(size_t)(tok0 + tt) * E + e] = bf2f(f2bf(__fadd_rn(d, bias)));
+        const float lg = bf2f(f2bf(__fadd_rn(d, bias)));
+        float* dst = logits + (size_t)(tok0 + tt) * E + e;
+        // kSel: device scope (sc1), read by the last workgroup on any XCD
+        if constexpr (kSel) store_dev(dst, lg);
+        else *dst = lg;
       }
     }
     if (ei + 1 < epw) {
 #pragma unroll
       for (int i = 0; i < S; ++i) gv[i] = gn[i];
     }
+  }
+  if constexpr (kSel) {
+    // Every wave waits for its own logits stores (complete sc1 stores are
+    // visible at device scope), the workgroup meets, and one thread counts
+    // it in; the workgroup whose count completes the launch's total runs the
+    // selection over every token and resets the count for the next call.
+    __shared__ int last;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+      const int total = (int)(gridDim.x * gridDim.y);
+      const int prev =
+          __hip_atomic_fetch_add(sel.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == total - 1;
+      if (last) store_dev(sel.arrive, 0);
+    }
+    __syncthreads();
+    if (last) select_group_last(logits, n, E, sel);
   }
 }
 
@@ -599,20 +646,26 @@ constexpr int kSelTok = 256;
 // are summed in rank order (gathered by shuffle within the token's 8 lanes)
 // and slot j of idx and w is written.  ti (when given) receives the indices
 // at [t - t0][k]; expert counts go to hist (LDS).
+// kKeys / kTok: capacity of keys and of topi / topv (8 per token); kDev:
+// the logits are read with device-scope loads (written by other workgroups
+// of the same launch).
+template <int kKeys = kSelLds, int kTok = kSelTok, bool kDev = false>
 __device__ __forceinline__ void select_range(const float* __restrict__ logits, int t0, int nt,
                                              int E, int k, uint32_t* keys, int* topi,
                                              float* topv, int32_t* __restrict__ idx_out,
                                              uint16_t* __restrict__ w_out, int* ti, int* hist) {
   const int lane = threadIdx.x & 63;
   const int Ep = (E + 31) & ~31;
-  const int per = min(kSelLds / Ep, kSelTok);
+  const int per = min(kKeys / Ep, kTok);
   for (int b0 = 0; b0 < nt; b0 += per) {
     const int nbt = min(per, nt - b0);
     const float* src = logits + (size_t)(t0 + b0) * E;
     __syncthreads();  // the previous pass's rows are no longer read
     for (int i = threadIdx.x; i < nbt * Ep; i += blockDim.x) {
       const int r = i / Ep, c = i - r * Ep;
-      keys[i] = rank_key(c < E ? src[r * E + c] : -INFINITY, c);
+      float v = -INFINITY;
+      if (c < E) v = kDev ? load_dev(src + r * E + c) : src[r * E + c];
+      keys[i] = rank_key(v, c);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < nbt * Ep; i += blockDim.x) {
@@ -679,6 +732,32 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
   __syncthreads();
   place_pairs(idx_lds, 0, n * k, k, E, base, wcnt, sorted_pairs, token_indices, expert_ids,
               pair_pos);
+}
+
+// The selection and grouping of moe_select_permute_kernel, run by the last
+// workgroup of the logits launch (n * roundup(E, 32) <= kFusedSelKeys, any
+// block size up to 1024 threads): the logits are read with device-scope loads.
+__device__ void select_group_last(const float* logits, int n, int E, const SelectArgs& sel) {
+  __shared__ __align__(16) uint32_t keys[kFusedSelKeys];
+  __shared__ int topi[kFusedSelTok * 8];
+  __shared__ float topv[kFusedSelTok * 8];
+  __shared__ int idx_lds[kFusedSelTok * 8];
+  __shared__ int cnt[256];
+  __shared__ int base[256];
+  __shared__ int wcnt[16 * 256];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < sel.zero_ints; i += blockDim.x) sel.zero[i] = 0;
+  for (int e = tid; e < E; e += blockDim.x) {
+    cnt[e] = 0;
+    base[e] = 0;
+  }
+  select_range<kFusedSelKeys, kFusedSelTok, true>(logits, 0, n, E, sel.k, keys, topi, topv,
+                                                  sel.idx, sel.w, idx_lds, cnt);
+  __syncthreads();
+  expert_prefix(cnt, E, base, sel.indptr);
+  __syncthreads();
+  place_pairs(idx_lds, 0, n * sel.k, sel.k, E, base, wcnt, sel.sorted_pairs, sel.token_indices,
+              sel.expert_ids, sel.pair_pos);
 }
 
 // Tokens per chunk of the large-n grouping.  Ranking costs E^2 key
@@ -855,7 +934,7 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
 #define MOE_LG(PC, S, TT, MF)                                                                     \
   hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, TT, MF>),                           \
                      dim3((n + TT - 1) / TT, ey), dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, \
-                     E, eps, pt, logits, q, qs, epw, (int32_t*)zero_e)
+                     E, eps, pt, logits, q, qs, epw, (int32_t*)zero_e, moe::SelectArgs{})
 #define MOE_LG_TT(PC, S)                        \
   if (mfma) MOE_LG(PC, S, 16, true);            \
   else if (n <= 128) MOE_LG(PC, S, 1, false);   \
@@ -867,6 +946,53 @@ extern "C" int moe_launch_router_logits(const void* x, const void* norm_w, const
   }
 #undef MOE_LG_TT
 #undef MOE_LG
+  return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
+}
+
+// The logits launch of moe_launch_router_logits (one token per workgroup,
+// one expert per wave) followed, in its last workgroup to finish, by the
+// top-k, softmax and grouping of moe_launch_select_group: one launch instead
+// of two.  n * roundup(E, 32) <= 4096 keys (n <= 128 at E = 32); otherwise
+// kErrUnsupported and nothing is launched.  `arrive` (one int) must be zero
+// before the first launch; every launch leaves it zero.
+extern "C" int moe_launch_router_select(const void* x, const void* norm_w, const void* gate_w,
+                                        const void* gate_b, int n, int H, int E, int k, float eps,
+                                        void* t_out, float* logits, void* pq, void* pqs,
+                                        void* zero_e, void* idx_out, void* w_out, void* indptr,
+                                        void* sorted_pairs, void* token_indices, void* expert_ids,
+                                        void* pair_pos, void* zero, int zero_ints, void* arrive,
+                                        hipStream_t stream) {
+  if (n == 0) return moe::kOk;
+  if (H > 4096 || H % 8 || E > 256 || k < 1 || k > 8 || (pq && H % 32) || !arrive)
+    return moe::kErrUnsupported;
+  if (n > moe::kFusedSelTok || n * ((E + 31) & ~31) > moe::kFusedSelKeys) return moe::kErrUnsupported;
+  constexpr int W = 8;
+  const moe::SelectArgs sel{k,
+                            (int32_t*)idx_out,
+                            (uint16_t*)w_out,
+                            (int32_t*)indptr,
+                            (int32_t*)sorted_pairs,
+                            (int32_t*)token_indices,
+                            (int32_t*)expert_ids,
+                            (int32_t*)pair_pos,
+                            (int32_t*)zero,
+                            zero_ints,
+                            (int32_t*)arrive};
+  const uint16_t *px = (const uint16_t*)x, *pn = (const uint16_t*)norm_w,
+                 *pg = (const uint16_t*)gate_w, *pb = (const uint16_t*)gate_b;
+  uint16_t* pt = (uint16_t*)t_out;
+  uint8_t *q = (uint8_t*)pq, *qs = (uint8_t*)pqs;
+  const dim3 grid(n, (E + W - 1) / W);
+#define MOE_LS(PC, S)                                                                           \
+  hipLaunchKernelGGL((moe::moe_router_logits_kernel<PC, S, W, 1, false, true>), grid,          \
+                     dim3(64 * W), 0, stream, px, pn, pg, pb, n, H, E, eps, pt, logits, q, qs, 1, \
+                     (int32_t*)zero_e, sel)
+  if (H <= 64 * 6 * 8) {
+    if (pq) { MOE_LS(true, 6); } else { MOE_LS(false, 6); }
+  } else {
+    if (pq) { MOE_LS(true, 8); } else { MOE_LS(false, 8); }
+  }
+#undef MOE_LS
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }
 

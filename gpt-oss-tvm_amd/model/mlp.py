@@ -176,8 +176,9 @@ class MLPBlock(torch.nn.Module):
         need = self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
             # A buffer that a captured graph holds stays alive in _ws_held;
-            # eager calls that need more get a new one.
-            self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+            # eager calls that need more get a new one.  Zero-filled: the
+            # block's counters must start at zero (every call leaves them so).
+            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
         return self._ws
 
     def reserve(self, n: int, for_graph: bool = False) -> None:
@@ -211,7 +212,8 @@ class MLPBlock(torch.nn.Module):
     def forward_into(self, x2d: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
         """forward on x2d [n, hidden] into the caller's ``out`` [n, hidden] with the
         caller's ``workspace`` (uint8, at least workspace_bytes(n), 256-byte
-        aligned): nothing is allocated, so the call can be captured in a graph.
+        aligned, zero-filled when allocated: every call leaves its counters at
+        zero): nothing is allocated, so the call can be captured in a graph.
         Calls that share a workspace must not overlap (one stream, in order)."""
         n = x2d.shape[0]
         if workspace.numel() < self.workspace_bytes(n):

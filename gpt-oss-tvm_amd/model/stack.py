@@ -50,7 +50,7 @@ class MoEStack(torch.nn.Module):
         if len(ns) != self.groups:
             raise ValueError(f"reserve needs {self.groups} token counts, got {len(ns)}")
         dev = self.layers[0][0].mlp1_weight_blocks.device
-        self._ws = torch.empty(max(self.workspace_bytes(*ns), 256), dtype=torch.uint8, device=dev)
+        self._ws = torch.zeros(max(self.workspace_bytes(*ns), 256), dtype=torch.uint8, device=dev)
         self._bufs = [torch.empty((2, max(n, 1), self.hidden_size), dtype=torch.bfloat16, device=dev)
                       for n in ns]
         self._n = tuple(ns)

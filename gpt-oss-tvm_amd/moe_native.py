@@ -59,13 +59,14 @@ _SIGS = {
     "moe_block_forward_noalloc": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _P, _F, _F, _F, _P, _P], _INT),
     "moe_set_decode_spin_limit": ([_INT], _INT),
+    "moe_hbm_read": ([_P, _SZ, _INT, _INT, _P, _P], _INT),
     "moe_block_forward_marked": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _P, _F, _F, _F, _P, _P, _SZ, _P, _INT, _P, _P, _P], _INT),
 }
 
 # MOE_STAGE_* of include/moe_gfx950.h
 STAGE_NAMES = ("start", "router_logits", "select", "decode", "mlp1", "act_pieces", "mlp2",
-               "gating")
+               "gating", "router")
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
@@ -446,3 +447,15 @@ def set_decode_spin_limit(polls: int) -> int:
     """Bound of the decode launch's wait in polls (negative: the default); returns
     the previous bound.  Tests set 0 to force the reported give-up path."""
     return int(_lib.moe_set_decode_spin_limit(polls))
+
+
+def hbm_read(src: torch.Tensor, grid: int, unroll: int, sink: torch.Tensor) -> None:
+    """Streaming read of every byte of ``src`` (the HBM calibration kernel);
+    ``sink`` holds at least ``grid`` int32."""
+    if not src.is_cuda or not src.is_contiguous():
+        raise ValueError("src: a contiguous device tensor")
+    _expect(sink, "sink", torch.int32)
+    if sink.numel() < grid:
+        raise ValueError(f"sink: need {grid} ints")
+    _check(_lib.moe_hbm_read(_ptr(src), src.numel() * src.element_size(), grid, unroll,
+                             _ptr(sink), _stream()), "moe_hbm_read")

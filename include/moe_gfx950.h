@@ -249,10 +249,16 @@ MOE_API int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, flo
  * x [n, H] bf16 and the nine parameters in checkpoint layout (model/mlp.py:63-144)
  * -> out [n, H] bf16.  workspace: at least moe_workspace_bytes(n, E, k, H, I)
  * bytes, 256-byte aligned; its layout is given by moe_workspace_layout().
+ * Its first 256 bytes hold counters that must be zero before the first call
+ * (allocate the workspace zero-filled); every call leaves them at zero, so a
+ * workspace can serve calls of any n, in order on one stream.  (At decode
+ * sizes the router's logits launch counts its finished workgroups there and
+ * the last one runs the top-k, softmax and grouping.)
  */
 MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I);
 
-/* Byte offsets of the intermediates inside the block workspace, in this order:
+/* Byte offsets of the intermediates inside the block workspace (after the
+ * 256 bytes of counters), in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
  * t_pieces, act (fp32 [n*k, I]; where n*k > 2E it shares y's offset: its
  * last reader runs before y is written), act_pieces, y (fp32 [n*k, H], in a
@@ -281,6 +287,7 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
 #define MOE_STAGE_ACT_PIECES 5    /* act's fp8 pieces (GEMV path above 2 pairs per expert) */
 #define MOE_STAGE_MLP2 6          /* mlp2 */
 #define MOE_STAGE_GATING 7        /* gated combine + residual */
+#define MOE_STAGE_ROUTER 8        /* ROUTER_LOGITS + SELECT in one launch (decode sizes) */
 
 /*
  * moe_block_forward with the caller's hipEvents (hipEvent_t, created by the
@@ -348,6 +355,17 @@ MOE_API int moe_block_status(const void* workspace, int64_t n, int64_t E, int64_
  * that the failure is reported.  No reference counterpart (as above).
  */
 MOE_API int moe_set_decode_spin_limit(int polls);
+
+/*
+ * Streaming read of `bytes` (a multiple of 16, 16-byte aligned) at src by
+ * `grid` workgroups of 256 threads, each thread `unroll` (4, 8 or 16)
+ * 16-byte loads in flight per iteration; sink: `grid` uint32 (written only in
+ * the unlikely case the data fold to a fixed constant).  No reference
+ * counterpart: the achievable-HBM-bandwidth calibration the kernels' HBM
+ * fractions are read against.
+ */
+MOE_API int moe_hbm_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink,
+                         moe_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 MAX_REL, MAE = 1e-2, 1e-3
+THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
 
 
 @pytest.fixture(scope="module")
@@ -238,6 +239,36 @@ def test_block_internal_routing(native, E, H, I, n, seed):
         assert np.array_equal(host(region(i, torch.int32, nk)), ref), i
     m = O.compare_outputs(out, tr.out)
     assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, m
+    # the workspace's counters (its first 256 bytes) are back at zero
+    assert int(torch.count_nonzero(ws[:256])) == 0
+
+
+def test_block_workspace_reused_across_sizes(native, oracle_lib):
+    """One zero-filled workspace serves calls of different sizes in turn (the
+    router's arrival count sits at the workspace's start for every n and each
+    call leaves it at zero): decode sizes (one router launch whose last
+    workgroup selects and groups), a 300-token call (two router launches, the
+    GEMV path) and decode again.  Routing bit-exact and outputs in tolerance
+    every time; the counters zero after every call."""
+    p = O.make_params(50, num_experts=32, hidden=2880, inter=2880)
+    blk = make_block(p)
+    ws = torch.zeros(blk.workspace_bytes(300), dtype=torch.uint8, device="cuda")
+    offs_for = {}
+    for i, n in enumerate((64, 1, 300, 64, 100, 2, 64)):
+        print(f"reused workspace: call {i}, n={n}", flush=True)
+        x = O.make_input(60 + i, n)
+        out = torch.empty((n, 2880), dtype=torch.bfloat16, device="cuda")
+        blk.forward_into(bf16_dev(x), out, ws)
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ws[:256])) == 0, i
+        offs = offs_for.setdefault(n, native.workspace_layout(n, 32, 4, 2880, 2880))
+        _, idx_ref = O.topk_softmax(O.router_logits(O.rms_norm(x, p.norm_w), p.gate_w, p.gate_b), 4)
+        idx = host(ws[offs[1]: offs[1] + n * 16].view(torch.int32)).reshape(n, 4)
+        assert np.array_equal(idx, idx_ref), i
+        sel = np.arange(n) if n <= 16 else np.sort(np.random.default_rng(i).choice(n, 16, replace=False))
+        ref, _, _, _ = oracle_lib.block_forward(np.ascontiguousarray(x[sel]), p, nthreads=THREADS)
+        m = O.compare_outputs(host_bf16(out)[sel], ref)
+        assert m["max_rel"] <= MAX_REL and m["mae"] <= MAE, (i, m)
 
 
 @pytest.mark.parametrize("E,H,I,n,seed,skew", [(8, 192, 192, 200, 41, False),
