@@ -564,6 +564,17 @@ def mfma_calibration(dev, size: int = 8192, reps: int = 20) -> dict:
             break
         except (RuntimeError, TypeError) as exc:
             res[f"fp8_{name}_error"] = str(exc).splitlines()[0][:120]
+    # the attention block's prefill projections at 4096 tokens, as
+    # model/attention.py runs them (F.linear: x W^T, bf16, hipBLASLt)
+    for name, (m, nn, kk) in (("qkv_4096x5120x2880", (4096, 5120, 2880)),
+                               ("out_4096x2880x4096", (4096, 2880, 4096))):
+        x = torch.randn((m, kk), generator=g, device=dev).to(torch.bfloat16)
+        w = torch.randn((nn, kk), generator=g, device=dev).to(torch.bfloat16)
+        f = 2.0 * m * nn * kk
+        t = rate(lambda: torch.nn.functional.linear(x, w)) * f / flops   # rate() counts size^3
+        us = f / (t * 1e12) * 1e6
+        res[name] = {"tflops": round(t, 1), "frac_of_2500": round(t / BF16_PEAK_TFLOPS, 3),
+                     "us": round(us, 1)}
     return res
 
 

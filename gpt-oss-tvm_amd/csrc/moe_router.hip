@@ -739,6 +739,7 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
 // block size up to 1024 threads): the logits are read with device-scope loads.
 __device__ void select_group_last(const float* logits, int n, int E, const SelectArgs& sel) {
   __shared__ __align__(16) uint32_t keys[kFusedSelKeys];
+  __shared__ __align__(16) float lg[kFusedSelKeys];
   __shared__ int topi[kFusedSelTok * 8];
   __shared__ float topv[kFusedSelTok * 8];
   __shared__ int idx_lds[kFusedSelTok * 8];
@@ -746,13 +747,45 @@ __device__ void select_group_last(const float* logits, int n, int E, const Selec
   __shared__ int base[256];
   __shared__ int wcnt[16 * 256];
   const int tid = threadIdx.x;
+  // The n x E logits into LDS with device-scope loads, all issued before any
+  // is used: 16 bytes a thread when E % 4 == 0 (n E <= kFusedSelKeys <= 8
+  // blockDim.x: at most 2 loads a thread), else one float each (at most 8).
+  const int total = n * E;
+  if ((E & 3) == 0) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)logits, (short)0, total * 4, kBufferWord3);
+    u32x4 v[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = tid + j * (int)blockDim.x;
+      if (4 * q < total) v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, q * 16, 0, kCpolSc1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = tid + j * (int)blockDim.x;
+      if (4 * q < total) *(u32x4*)(lg + 4 * q) = v[j];
+    }
+  } else {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = tid + j * (int)blockDim.x;
+      if (i < total) v[j] = load_dev(logits + i);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = tid + j * (int)blockDim.x;
+      if (i < total) lg[i] = v[j];
+    }
+  }
   for (int i = tid; i < sel.zero_ints; i += blockDim.x) sel.zero[i] = 0;
   for (int e = tid; e < E; e += blockDim.x) {
     cnt[e] = 0;
     base[e] = 0;
   }
-  select_range<kFusedSelKeys, kFusedSelTok, true>(logits, 0, n, E, sel.k, keys, topi, topv,
-                                                  sel.idx, sel.w, idx_lds, cnt);
+  // (select_range starts with a barrier: lg is complete)
+  select_range<kFusedSelKeys, kFusedSelTok, false>(lg, 0, n, E, sel.k, keys, topi, topv,
+                                                   sel.idx, sel.w, idx_lds, cnt);
   __syncthreads();
   expert_prefix(cnt, E, base, sel.indptr);
   __syncthreads();
@@ -967,6 +1000,7 @@ extern "C" int moe_launch_router_select(const void* x, const void* norm_w, const
     return moe::kErrUnsupported;
   if (n > moe::kFusedSelTok || n * ((E + 31) & ~31) > moe::kFusedSelKeys) return moe::kErrUnsupported;
   constexpr int W = 8;
+  static_assert(moe::kFusedSelKeys <= 8 * 64 * W, "the staging's loads per thread");
   const moe::SelectArgs sel{k,
                             (int32_t*)idx_out,
                             (uint16_t*)w_out,
