@@ -588,21 +588,27 @@ __device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, 
     const int rank = __popcll(same & lt);
     if (ok && rank == 0) wcnt[wave * 256 + v] = __popcll(same);
     __syncthreads();
+    // per expert: the waves' counts become their exclusive prefix (in wave
+    // order) on top of base, and base moves past the round
+    const int nwv = (nthr + 63) >> 6;
+    for (int e = tid; e < E; e += nthr) {
+      int run = base[e];
+      for (int w = 0; w < nwv; ++w) {
+        const int c = wcnt[w * 256 + e];
+        wcnt[w * 256 + e] = run;
+        run += c;
+      }
+      base[e] = run;
+    }
+    __syncthreads();
     if (ok) {
-      int pos = base[v] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w * 256 + v];
+      const int pos = wcnt[wave * 256 + v] + rank;
       sorted_pairs[pos] = p;
       token_indices[pos] = p / k;
       expert_ids[pos] = v;
       pair_pos[p] = pos;
     } else if (inb) {
       pair_pos[p] = -1;
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += nthr) {
-      int s = 0;
-      for (int w = 0; w < 16; ++w) s += wcnt[w * 256 + e];
-      base[e] += s;
     }
     __syncthreads();
   }
@@ -673,9 +679,21 @@ __device__ __forceinline__ void select_range(const float* __restrict__ logits, i
       const uint32_t key = keys[i];
       const u32x4* kr = (const u32x4*)(keys + r * Ep);
       int rank = 0;
-      for (int o = 0; o < (Ep >> 2); ++o) {
-        const u32x4 q = kr[o];
-        rank += (q[0] > key) + (q[1] > key) + (q[2] > key) + (q[3] > key);
+      if (Ep <= 64) {
+        // up to 16 chunks of the row read at once (past Ep: the row's own
+        // first chunk again, not counted)
+        u32x4 q[16];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) q[o] = kr[o < (Ep >> 2) ? o : 0];
+#pragma unroll
+        for (int o = 0; o < 16; ++o)
+          if (o < (Ep >> 2))
+            rank += (q[o][0] > key) + (q[o][1] > key) + (q[o][2] > key) + (q[o][3] > key);
+      } else {
+        for (int o = 0; o < (Ep >> 2); ++o) {
+          const u32x4 q = kr[o];
+          rank += (q[0] > key) + (q[1] > key) + (q[2] > key) + (q[3] > key);
+        }
       }
       if (c < E && rank < k) {
         topi[r * 8 + rank] = c;
@@ -734,6 +752,68 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
               pair_pos);
 }
 
+// Maximum of v over this lane's 32-lane half of the wave, in registers: DPP
+// quad permutes, half-row and row mirrors (the row's maximum in every lane),
+// then v_permlane16_swap for the two rows of the half.  All lanes active.
+__device__ __forceinline__ uint32_t half_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+__device__ __forceinline__ double readlane_f64(double x, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Top-k + softmax of n tokens whose logits are in LDS (lg [n][E], E <= 32),
+// two tokens per wave, one per 32-lane half: lane e holds expert e's ranking
+// key; k rounds of the half's maximum (registers only) give the keys in rank
+// order, lane j keeping rank j's.  Lane j < k then takes its fp64
+// exponential against rank 0, the k are summed in rank order and slot j of
+// idx and w is written -- the arithmetic of select_range.  The indices also
+// go to ti (LDS, [t][k]) and the expert counts to hist (LDS).
+__device__ __forceinline__ void select_halves(const float* lg, int n, int E, int k,
+                                              int32_t* __restrict__ idx_out,
+                                              uint16_t* __restrict__ w_out, int* ti, int* hist) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int half = lane >> 5, e = lane & 31;
+  for (int t0 = 2 * wave; t0 < n; t0 += 2 * nw) {
+    const int t = t0 + half;
+    const bool live = t < n;
+    // keys below every real key (rank_key(-inf, e) >= 0x007F0000) pad the half
+    uint32_t key = (live && e < E) ? rank_key(lg[t * E + e], e) : 0u;
+    uint32_t win = 0u;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t m = half_max_u32(key);
+      if (e == j) win = m;
+      if (key == m) key = 0u;  // keys are distinct (the expert is in the low bits)
+    }
+    const uint32_t top0 = (uint32_t)__builtin_amdgcn_readlane((int)win, 0);
+    const uint32_t top1 = (uint32_t)__builtin_amdgcn_readlane((int)win, 32);
+    const uint32_t top = half ? top1 : top0;
+    const double ex = e < k ? exp((double)key_value(win) - (double)key_value(top)) : 0.0;
+    double s0 = readlane_f64(ex, 0), s1 = readlane_f64(ex, 32);
+    for (int jj = 1; jj < k; ++jj) {
+      s0 += readlane_f64(ex, jj);
+      s1 += readlane_f64(ex, 32 + jj);
+    }
+    const double sum = half ? s1 : s0;
+    if (live && e < k) {
+      const int ex_id = 0xFFFF - (int)(win & 0xFFFFu);
+      w_out[(size_t)t * k + e] = f64_to_bf16_via_f32(ex / sum);
+      idx_out[(size_t)t * k + e] = ex_id;
+      ti[t * k + e] = ex_id;
+      atomicAdd(&hist[ex_id], 1);
+    }
+  }
+}
+
 // The selection and grouping of moe_select_permute_kernel, run by the last
 // workgroup of the logits launch (n * roundup(E, 32) <= kFusedSelKeys, any
 // block size up to 1024 threads): the logits are read with device-scope loads.
@@ -783,9 +863,12 @@ __device__ void select_group_last(const float* logits, int n, int E, const Selec
     cnt[e] = 0;
     base[e] = 0;
   }
-  // (select_range starts with a barrier: lg is complete)
-  select_range<kFusedSelKeys, kFusedSelTok, false>(lg, 0, n, E, sel.k, keys, topi, topv,
-                                                   sel.idx, sel.w, idx_lds, cnt);
+  __syncthreads();  // lg and the counts are complete
+  if (E <= 32)
+    select_halves(lg, n, E, sel.k, sel.idx, sel.w, idx_lds, cnt);
+  else
+    select_range<kFusedSelKeys, kFusedSelTok, false>(lg, 0, n, E, sel.k, keys, topi, topv,
+                                                     sel.idx, sel.w, idx_lds, cnt);
   __syncthreads();
   expert_prefix(cnt, E, base, sel.indptr);
   __syncthreads();
