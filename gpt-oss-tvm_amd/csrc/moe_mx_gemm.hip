@@ -91,6 +91,20 @@ __device__ __forceinline__ uint32_t lds_u8(uint32_t a) {
   return v;
 }
 
+// The value of lane l + 16 for lane groups g = 0..2 (x's next 16-lane row)
+// and of lane l - 48 for g = 3 (y's row 0): one row down across the pair
+// (x, y).  v_permlane16_swap(D, S) swaps D's odd rows with S's even rows
+// (D' = [D0 S0 D2 S2], S' = [D1 S1 D3 S3]); v_permlane32_swap(D, S) swaps
+// D's upper half with S's lower half (D' = [D0 D1 S0 S1], S' = [D2 D3 S2 S3]).
+__device__ __forceinline__ float gm_row_down(float x, float y, int g) {
+  const int xi = __float_as_int(x), yi = __float_as_int(y);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);  // S' = [x1 x1 x3 x3]
+  const auto s32 = __builtin_amdgcn_permlane32_swap(xi, yi, false, false);  // [x0 x1 y0 y1], [x2 x3 y2 y3]
+  const auto a = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);  // D' = [x0 x2 y0 y2]
+  const auto c = __builtin_amdgcn_permlane16_swap(s32[1], s32[0], false, false);  // D' = [x2 x0 y2 y0]
+  return __int_as_float(g == 1 ? (int)a[0] : g == 3 ? (int)c[0] : (int)s16[1]);
+}
+
 template <int P, int kEpi>
 __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs, int Kp,
@@ -351,23 +365,42 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
     // c % 3), issue chunk c + 3 into that stage, then multiply chunk c from
     // registers while chunk c + 1's operands are read from LDS.  The barrier
     // carries no memory fence: a fence would wait for the loads in flight.
+    // Issue order within the step: the first six MFMAs straight after the
+    // barrier (their operands are in registers), then the B and first A
+    // operand reads, six more MFMAs, then the chunk loads and the other A
+    // reads, the last six MFMAs.  (Measured against the loads and reads
+    // ahead of the MFMAs, and against one MFMA between each pair of memory
+    // instructions: both are slower.)
     auto step = [&](int c, Ops& cu, Ops& nx, auto sv) {
       constexpr int S = decltype(sv)::value;           // stage of chunk c
       constexpr int S1 = (S + 1) % kGmStages;          // stage of chunk c + 1
       const bool more = c + 1 < NC;
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using SS1 = std::integral_constant<int, S1>;
       if (more) {
         wait_chunks(c + 2 < NC ? 1 : 0);
         __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        if (c + 3 < NC) issue_chunk(c + 3, S);
-        read_b(nx, c + 1, std::integral_constant<int, S1>{});
       }
-      gm_static_for<0, 3>([&](auto fv) {
-        constexpr int f = decltype(fv)::value;
-        if (more) read_a(nx, c + 1, std::integral_constant<int, S1>{}, fv);
-        if (f < nf) mfma_group(cu, fv);
-        __builtin_amdgcn_sched_barrier(0);
-      });
+      __builtin_amdgcn_sched_barrier(0);
+      if (0 < nf) mfma_group(cu, I0{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) {
+        read_b(nx, c + 1, SS1{});
+        read_a(nx, c + 1, SS1{}, I0{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (1 < nf) mfma_group(cu, I1{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) {
+        if (c + 3 < NC) issue_chunk(c + 3, S);
+        read_a(nx, c + 1, SS1{}, I1{});
+        read_a(nx, c + 1, SS1{}, I2{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (2 < nf) mfma_group(cu, I2{});
+      __builtin_amdgcn_sched_barrier(0);
       if (more) wait_ops(nx);
     };
     // Register sets alternate with the chunk parity and stages with c % 3,
@@ -418,6 +451,11 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
       // the share of the next quad (q + 1: lane + 16, or for g = 3 the next
       // f's lane group 0) comes by shuffle.  Sums run smallest piece first,
       // ((p2 + p1) + p0) + bias, as for the other piece counts.
+      // Branch-free (q % 3 varies with the lane group): operands by select,
+      // and the second token's value of a q % 3 = 0 quad is written by every
+      // lane, the others' into the spare row TPT, which is never read.  The
+      // exchange is by lane-row swaps (register moves, no LDS round trip).
+      static_assert((TPT + 1) * TWp * 4 <= kGmStages * kGmStage, "spare row");
 #pragma unroll
       for (int b = 0; b < 6; ++b) {
         const int cl = 96 * wn + 16 * b + r;
@@ -429,17 +467,14 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
 #pragma unroll
         for (int f = 0; f < 3; ++f) {
           const f32x4 a = acc[f][b];
-          const float down = __shfl_down(send[f], 16, kWave);
-          const float wrap = f < 2 ? __shfl_xor(send[f < 2 ? f + 1 : f], 48, kWave) : 0.0f;
-          const float recv = g < 3 ? down : wrap;
+          const float rv = gm_row_down(send[f], f < 2 ? send[f < 2 ? f + 1 : f] : 0.0f, g);
           const int q = 4 * f + g, qm = q % 3;
           const int tb = 16 * wm + (4 * q) / 3;
-          float y0;
-          if (qm == 0) y0 = ((a[2] + a[1]) + a[0]) + bn;
-          else if (qm == 1) y0 = ((recv + a[3]) + a[2]) + bn;
-          else y0 = ((a[3] + a[2]) + a[1]) + bn;
-          tile[(qm == 0 ? tb : tb + 1) * TWp + cl] = y0;
-          if (qm == 0) tile[(tb + 1) * TWp + cl] = (recv + a[3]) + bn;
+          const float v1 = qm == 0 ? a[2] : qm == 1 ? rv : a[3];
+          const float v2 = qm == 0 ? a[1] : qm == 1 ? a[3] : a[2];
+          const float v3 = qm == 0 ? a[0] : qm == 1 ? a[2] : a[1];
+          tile[(qm == 0 ? tb : tb + 1) * TWp + cl] = ((v1 + v2) + v3) + bn;
+          tile[(qm == 0 ? tb + 1 : TPT) * TWp + cl] = (rv + a[3]) + bn;
         }
       }
     } else {
