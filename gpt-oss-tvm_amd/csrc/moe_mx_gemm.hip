@@ -503,7 +503,11 @@ __global__ __launch_bounds__(kGmThreads) void moe_mx_gemm_kernel(
             const float xg = fminf(glu, limit);
             const float xl = fminf(fmaxf(lin, -limit), limit);
             const float z = __fmul_rn(alpha, xg);
-            const float sig = 1.0f / (1.0f + expf(-z));
+            // sigmoid from the hardware exp2 and reciprocal (v_exp_f32 of
+            // -z log2(e), v_rcp_f32: a few ulp of the correctly rounded value;
+            // the epilogue is VALU-bound and the library expf and division
+            // cost about 25 instructions per element)
+            const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-z));
             tile[(tt0 + (odd ? 1 : 0)) * TWp + (cl >> 1)] =
                 __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
           } else {
