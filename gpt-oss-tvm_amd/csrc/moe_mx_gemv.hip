@@ -196,15 +196,20 @@ __device__ __forceinline__ void mx_unit_prefix(const int* __restrict__ indptr, i
 // multiples of `align` tiles: one segment (one staging) per workgroup.  A
 // share that straddled two batches would stage twice and finish last.  With
 // more batches than workgroups, the units are split evenly and a share may
-// span several segments.
+// span several segments.  balance: also split evenly when the batch split
+// would load its busiest workgroups more than 1.25 times the average (q
+// workgroups for most batches gives ntiles / q tiles each against
+// ntiles * batches / grid on average: with q = 1, 140 batches on 256
+// workgroups put a whole batch on 116 of them at 1.7 times the average).
 __device__ __forceinline__ void mx_share(const int* pre, int E, int ntiles, int align, int xcds,
-                                         int& ubeg, int& uend) {
+                                         int& ubeg, int& uend, bool balance = false) {
   const int total = pre[E];  // < 2^31 (the launchers check)
   const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (int)(gridDim.x / xcds) +
                                 (int)(blockIdx.x / xcds)
                           : (int)blockIdx.x;
   const int nbatches = (int)(total / ntiles);
-  if (nbatches > 0 && nbatches <= (int)gridDim.x) {
+  if (nbatches > 0 && nbatches <= (int)gridDim.x &&
+      !(balance && 5 * ((int)gridDim.x / nbatches) * nbatches < 4 * (int)gridDim.x)) {
     const int q = (int)gridDim.x / nbatches, rmd = (int)gridDim.x % nbatches;
     int b, i, w;
     if (vb < rmd * (q + 1)) {
@@ -242,7 +247,8 @@ __device__ __forceinline__ int mx_expert_of(const int* pre, int E, int u) {
 // multiples of `align` tiles.  kWait: wait(e, b0, nb) runs before each
 // segment's staging, called by every thread and ending in a workgroup
 // barrier; the first segment's first tile loads are issued before it.
-// first: the share's first segment.
+// first: the share's first segment.  balance: mx_share's (the decode launch,
+// whose shares must be one segment each, leaves it off).
 template <int P, int kEpi, int NCT, bool kWait, class WaitFn>
 __device__ __forceinline__ void mx_pass(
     uint8_t* lds, const MxLds& L, const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs,
@@ -250,7 +256,7 @@ __device__ __forceinline__ void mx_pass(
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, int E, int groups_cap, float alpha,
     float limit, float* __restrict__ out, int out_ld, int xcds, int align, WaitFn&& wait,
-    MxSeg& first) {
+    MxSeg& first, bool balance = false) {
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
@@ -270,7 +276,7 @@ __device__ __forceinline__ void mx_pass(
   first.e = -1;
 
   int ubeg, uend;
-  mx_share(pre, E, ntiles, align, xcds, ubeg, uend);
+  mx_share(pre, E, ntiles, align, xcds, ubeg, uend, balance);
   if (ubeg >= uend) return;
   auto expert_of = [&](int u) { return mx_expert_of(pre, E, u); };
 
@@ -785,7 +791,7 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   MxSeg first;
   mx_pass<P, kEpi, NCT, false>(lds, L, q, qs, Kp, sorted_pairs, k_top, arow_mode, orow_mode,
                                blocks, scales, bias, N, G, E, groups_cap, alpha, limit, out,
-                               out_ld, xcds, 1, [](int, int, int) {}, first);
+                               out_ld, xcds, 1, [](int, int, int) {}, first, true);
 }
 
 // ---------------------------------------------------------------------------
