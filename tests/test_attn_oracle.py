@@ -67,13 +67,21 @@ def test_rope_is_a_scaled_rotation():
 
 
 def test_linear_two_roundings():
-    rng = np.random.default_rng(2)
-    x = bf(rng.standard_normal((3, 40)))
-    w = bf(rng.standard_normal((5, 40)) * 0.1)
-    b = bf(rng.standard_normal(5))
-    y = A.linear(x, w, b)
-    mm = bf((f(x) @ f(w).T).astype(np.float32))
-    np.testing.assert_array_equal(y, bf((f(mm) + f(b)).astype(np.float32)))
+    """nn.Linear as two bf16 ops (attention.py:206,254): bf16(bf16(x W^T) + b),
+    the products summed exactly.  Closed cases: x W^T = 1 + 2^-8 + 2^-10 rounds
+    to 1 + 2^-7 (above the midpoint 1 + 2^-8); adding b = 2^-8 lands exactly on
+    the midpoint between 1 + 2^-7 and 1 + 2^-6, which ties to the even 1 + 2^-6
+    -- one rounding of the exact 1 + 2^-7 + 2^-10 would give 1 + 2^-7.  And
+    [2^24, 1, -2^24] . [1, 1, 1] = 1 exactly, which an fp32 running sum (2^24 + 1
+    = 2^24) would lose."""
+    x = bf(np.array([[1.0, 2.0 ** -8, 2.0 ** -10], [2.0 ** 24, 1.0, -2.0 ** 24]]))
+    w = bf(np.array([[1.0, 1.0, 1.0]]))
+    y = f(A.linear(x, w, None)).ravel()
+    assert y[0] == 1.0 + 2.0 ** -7 and y[1] == 1.0
+    yb = f(A.linear(x[:1], w, bf(np.array([2.0 ** -8])))).ravel()
+    assert yb[0] == 1.0 + 2.0 ** -6
+    yn = f(A.linear(bf(-f(x[:1])), w, bf(np.array([-2.0 ** -8])))).ravel()
+    assert yn[0] == -(1.0 + 2.0 ** -6)  # ties to even in magnitude for either sign
 
 
 def _brute_attention(q, k, v, qpos, window, scale):
