@@ -774,13 +774,16 @@ __device__ __forceinline__ double readlane_f64(double x, int l) {
 // Top-k + softmax of n tokens whose logits are in LDS (lg [n][E], E <= 32),
 // two tokens per wave, one per 32-lane half: lane e holds expert e's ranking
 // key; k rounds of the half's maximum (registers only) give the keys in rank
-// order, lane j keeping rank j's.  Lane j < k then takes its fp64
-// exponential against rank 0, the k are summed in rank order and slot j of
-// idx and w is written -- the arithmetic of select_range.  The indices also
-// go to ti (LDS, [t][k]) and the expert counts to hist (LDS).
+// order, rank j's going to wk (LDS, [t][k]).  Then one thread per (token,
+// rank j) takes its fp64 exponential against rank 0 (ex, LDS), and one per
+// pair sums its token's k in rank order and writes slot j of idx and w -- the
+// arithmetic of select_range.  The indices also go to ti (LDS, [t][k]) and the
+// expert counts to hist (LDS).  The exponentials and quotients are spread
+// over every lane of the workgroup, not k of each half-wave.
 __device__ __forceinline__ void select_halves(const float* lg, int n, int E, int k,
                                               int32_t* __restrict__ idx_out,
-                                              uint16_t* __restrict__ w_out, int* ti, int* hist) {
+                                              uint16_t* __restrict__ w_out, int* ti, int* hist,
+                                              uint32_t* wk, double* ex) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int half = lane >> 5, e = lane & 31;
   for (int t0 = 2 * wave; t0 < n; t0 += 2 * nw) {
@@ -788,29 +791,28 @@ __device__ __forceinline__ void select_halves(const float* lg, int n, int E, int
     const bool live = t < n;
     // keys below every real key (rank_key(-inf, e) >= 0x007F0000) pad the half
     uint32_t key = (live && e < E) ? rank_key(lg[t * E + e], e) : 0u;
-    uint32_t win = 0u;
     for (int j = 0; j < k; ++j) {
       const uint32_t m = half_max_u32(key);
-      if (e == j) win = m;
+      if (live && e == j) wk[t * k + j] = m;
       if (key == m) key = 0u;  // keys are distinct (the expert is in the low bits)
     }
-    const uint32_t top0 = (uint32_t)__builtin_amdgcn_readlane((int)win, 0);
-    const uint32_t top1 = (uint32_t)__builtin_amdgcn_readlane((int)win, 32);
-    const uint32_t top = half ? top1 : top0;
-    const double ex = e < k ? exp((double)key_value(win) - (double)key_value(top)) : 0.0;
-    double s0 = readlane_f64(ex, 0), s1 = readlane_f64(ex, 32);
-    for (int jj = 1; jj < k; ++jj) {
-      s0 += readlane_f64(ex, jj);
-      s1 += readlane_f64(ex, 32 + jj);
-    }
-    const double sum = half ? s1 : s0;
-    if (live && e < k) {
-      const int ex_id = 0xFFFF - (int)(win & 0xFFFFu);
-      w_out[(size_t)t * k + e] = f64_to_bf16_via_f32(ex / sum);
-      idx_out[(size_t)t * k + e] = ex_id;
-      ti[t * k + e] = ex_id;
-      atomicAdd(&hist[ex_id], 1);
-    }
+  }
+  lds_barrier();
+  const int np = n * k;
+  for (int p = threadIdx.x; p < np; p += blockDim.x) {
+    const int t = p / k;
+    ex[p] = exp((double)key_value(wk[p]) - (double)key_value(wk[t * k]));
+  }
+  lds_barrier();
+  for (int p = threadIdx.x; p < np; p += blockDim.x) {
+    const int t0 = p / k * k;
+    double sum = ex[t0];
+    for (int jj = 1; jj < k; ++jj) sum += ex[t0 + jj];
+    const int ex_id = 0xFFFF - (int)(wk[p] & 0xFFFFu);
+    w_out[p] = f64_to_bf16_via_f32(ex[p] / sum);
+    idx_out[p] = ex_id;
+    ti[p] = ex_id;
+    atomicAdd(&hist[ex_id], 1);
   }
 }
 
@@ -908,15 +910,19 @@ __device__ void select_group_last(const float* logits, int n, int E, const Selec
     cnt[e] = 0;
     base[e] = 0;
   }
-  __syncthreads();  // lg and the counts are complete
-  if (E <= 32)
-    select_halves(lg, n, E, sel.k, sel.idx, sel.w, idx_lds, cnt);
+  // The barriers below wait for LDS only: nothing here reads back the
+  // global stores (the zeroed counters, idx, w, indptr), which the launch's
+  // end completes.
+  lds_barrier();  // lg and the counts are complete
+  if (E <= 32)  // (keys and topi are select_range's; here the ranks' scratch)
+    select_halves(lg, n, E, sel.k, sel.idx, sel.w, idx_lds, cnt, (uint32_t*)topi,
+                  (double*)keys);
   else
     select_range<kFusedSelKeys, kFusedSelTok, false>(lg, 0, n, E, sel.k, keys, topi, topv,
                                                      sel.idx, sel.w, idx_lds, cnt);
-  __syncthreads();
+  lds_barrier();
   expert_prefix(cnt, E, base, sel.indptr);
-  __syncthreads();
+  lds_barrier();
   place_pairs(idx_lds, 0, n * sel.k, sel.k, E, base, wcnt, sel.sorted_pairs, sel.token_indices,
               sel.expert_ids, sel.pair_pos);
 }
