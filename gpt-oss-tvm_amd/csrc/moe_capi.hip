@@ -97,6 +97,15 @@ constexpr int64_t kGemmMinTokens = 48;
 // count, then the y rows) sit at the launch's tail.
 constexpr int64_t kFusedCombineMaxTokens = 32;
 
+// The decode launch (mlp1, act's encoding and mlp2 in one persistent launch)
+// from this many tokens up.  One token takes separate launches (mlp1 GEMV,
+// mlp2 GEMV encoding act while staging it, gating kernel): its mlp1 is a
+// few tiles per workgroup, so the launch's chain of device-scope round trips
+// (act stored, count published, count polled, act staged) costs more than a
+// kernel boundary (block 32.0 us against 34.5; two tokens 42.9 against 43.2,
+// three 52.1 against 50.4, the launch ahead from there on).
+constexpr int64_t kDecodeLaunchMinTokens = 2;
+
 // moe_block_forward_marked: the caller's hipEvents recorded on the block's
 // stream before its first launch and after each stage (MOE_STAGE_*).
 constexpr int kMaxMarks = 8;
@@ -507,7 +516,8 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   void* t_qs = (char*)t_pk + moe_pieces_q_bytes(n, H, kPiecesT);
   if ((rc = mark(m, MOE_STAGE_START, s))) return rc;
   // the decode launch's arrival counts (fused combine) zeroed by the selection
-  const bool fuse = !gemm && n <= kFusedCombineMaxTokens;
+  const bool decode = !gemm && n >= kDecodeLaunchMinTokens && n <= 128;
+  const bool fuse = decode && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
   // decode sizes: the logits launch's last workgroup runs the selection and
   // grouping (one launch); otherwise two launches
@@ -531,9 +541,9 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   } else if (rc) {
     return rc;
   }
-  // Decode (at most 128 tokens, the shape and device fit): mlp1, the encoding
-  // of act and mlp2 in one launch.
-  if (!gemm && n <= 128) {
+  // Decode (2 to 128 tokens, the shape and device fit): mlp1, the encoding of
+  // act and mlp2 in one launch.
+  if (decode) {
     // up to kFusedCombineMaxTokens with the gated combine: the last of a
     // token's k mlp2 tiles to arrive writes its 16 columns of out (NaN if a
     // wait gave up); above, the gating kernel (NaN rows after a give-up)
