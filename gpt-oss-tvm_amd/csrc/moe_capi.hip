@@ -60,6 +60,13 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          float alpha, float limit, void* act_packed, void* y, void* done,
                          void* status, const void* w, const void* x, void* out, void* arrive,
                          hipStream_t stream);
+int moe_mx_token1_check(int k, int H, int I);
+int moe_launch_mx_token1_mlp1(const void* t_packed, const void* idx, const void* blocks,
+                              const void* scales, const void* bias, int k, int H, int I,
+                              float alpha, float limit, void* act, hipStream_t stream);
+int moe_launch_mx_token1_mlp2(const void* act, const void* idx, const void* w, const void* x,
+                              const void* blocks, const void* scales, const void* bias, int k,
+                              int H, int I, void* out, hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
                       hipStream_t stream);
 int moe_launch_hbm_read(const void* src, size_t bytes, int grid, int unroll, uint32_t* sink,
@@ -557,6 +564,17 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
       return mark(m, MOE_STAGE_GATING, s);
     }
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
+  }
+  // One token (the shape permitting): mlp1, then mlp2 with the gated combine,
+  // each wave on one weight tile (act by slot, [k][I] fp32).
+  if (n == 1 && !gemm && moe_mx_token1_check((int)k, (int)H, (int)I) == MOE_OK) {
+    if ((rc = moe_launch_mx_token1_mlp1(t_pk, idx, mlp1_blocks, mlp1_scales, mlp1_bias, (int)k,
+                                        (int)H, (int)I, alpha, limit, act, s)) ||
+        (rc = mark(m, MOE_STAGE_MLP1, s)) ||
+        (rc = moe_launch_mx_token1_mlp2(act, idx, w, x, mlp2_blocks, mlp2_scales, mlp2_bias,
+                                        (int)k, (int)H, (int)I, out, s)))
+      return rc;
+    return mark(m, MOE_STAGE_MLP2, s);
   }
   if (gemm) {
     if ((rc = mlp1_pieces(t_pk, n, k, E, H, I, indptr, sp, mlp1_blocks, mlp1_scales, mlp1_bias,

@@ -1046,6 +1046,268 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// One token: mlp1, then mlp2 with the gated combine, as two launches in which
+// every wave holds one 16-row weight tile and issues all of its loads at
+// once.  With one token a persistent pass gives each wave under one tile, so
+// its unit prefix (a global load ahead of the first weight address), its
+// two-stage pipeline and the gating launch after mlp2 are latency only.
+// Here the first weight address needs only the token's k expert indices, and
+// each mlp2 workgroup owns 16 output columns for all k experts (one wave per
+// slot), so the k rows are combined in LDS.  The arithmetic is that of
+// moe_mx_gemv_kernel (the same operand layout, the same MFMA chain over the
+// 23 chunks, the same epilogues and act encoding) and of moe_gating_kernel,
+// so the outputs equal those launches' bit for bit.
+
+constexpr int kT1Nct = 23;  // K chunks (K = 32 G with 89 <= G <= 92)
+constexpr int kT1Kp = kT1Nct * 128;
+
+// One wave's 16-row weight tile: 23 chunks, its scale bytes and the bias of
+// this lane's row.
+struct T1Tile {
+  u32x4 w[kT1Nct];
+  u32x4 sc0, sc1;
+  float bn;
+};
+
+// Block index of chunk c for lane group g: 4 c + g; only the last chunk can
+// pass K (then block G - 1 is re-read; its A bytes are zero).
+__device__ __forceinline__ int t1_blk(int c, int g, int G) {
+  return c < kT1Nct - 1 ? 4 * c + g : min(4 * c + g, G - 1);
+}
+
+__device__ __forceinline__ void t1_issue(T1Tile& t, const uint8_t* __restrict__ blocks,
+                                         const uint8_t* __restrict__ scales,
+                                         const uint16_t* __restrict__ bias, size_t row0, int G) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint8_t* st = scales + row0 * G;  // 16 rows x G bytes, contiguous
+  t.sc0 = *(const u32x4*)(st + min(lane, G - 1) * 16);
+  t.sc1 = *(const u32x4*)(st + min(lane + 64, G - 1) * 16);
+  t.bn = bf2f(bias[row0 + r]);
+  const uint8_t* wp = blocks + (row0 + r) * G * 16;
+  static_for<0, kT1Nct>([&](auto cv) {
+    constexpr int c = decltype(cv)::value;
+    t.w[c] = *(const u32x4*)(wp + t1_blk(c, g, G) * 16);
+  });
+}
+
+// The tile's scale bytes to this wave's LDS staging (16 G bytes), from which
+// lane (r, g) reads row r's byte of each block it multiplies.  Lanes past
+// the G units store unit G - 1 again (the bytes they loaded): no branch, so
+// the compiler cannot sink a scale load into one, behind the chunk loads.
+__device__ __forceinline__ void t1_stage_scales(const T1Tile& t, uint8_t* sstage, int G) {
+  const int lane = threadIdx.x & 63;
+  *(u32x4*)(sstage + min(lane, G - 1) * 16) = t.sc0;
+  *(u32x4*)(sstage + min(lane + 64, G - 1) * 16) = t.sc1;
+}
+
+// The MFMA chain of one tile over chunks 0..22 in order against A rows in
+// LDS: `arows` piece rows at `a_base` (row stride mx_row_stride(23)), their
+// scale rows right after them (kMxSclRow each).  MFMA rows at or past arows
+// read row 0: their outputs are not used.  ss: this wave's staged weight
+// scale bytes.
+__device__ __forceinline__ f32x4 t1_chain(const uint8_t* lds, uint32_t a_base, int arows,
+                                          uint32_t ss, const T1Tile& t, int G) {
+  constexpr int kRS = mx_row_stride(kT1Nct);
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int ra = r < arows ? r : 0;
+  const uint32_t ar = a_base + ra * kRS + 16 * g;
+  const uint32_t as = a_base + arows * kRS + ra * kMxSclRow + g * kMxSclRun;
+  const uint32_t sr = ss + r * G;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  static_for<0, kT1Nct>([&](auto cv) {
+    constexpr int c = decltype(cv)::value;
+    const u32x4 a0 = *(const u32x4*)(lds + ar + 128 * c);
+    const u32x4 a1 = *(const u32x4*)(lds + ar + 128 * c + 64);
+    const i32x8 A = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                     (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+    const uint32_t sa = *(const uint32_t*)(lds + as + (c & ~3));
+    const uint32_t sb = lds[sr + t1_blk(c, g, G)];
+    const i32x8 B = {(int)t.w[c][0], (int)t.w[c][1], (int)t.w[c][2], (int)t.w[c][3], 0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 0, 4, c & 3, (int)sa, 0,
+                                                           (int)sb);
+  });
+  return acc;
+}
+
+// mlp1 of one token with the interleaved SwiGLU epilogue: workgroup
+// (q, slot) holds 4 waves, wave v the weight tile 4 q + v (16 rows: 8 gate
+// and 8 linear, interleaved) of expert idx[slot]; act row `slot` ([k][I],
+// fp32) gets its 8 columns.  t's two pieces (rows 0 and 1 of tq, scale rows
+// of tqs) are staged in LDS.
+__global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
+    const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
+    const int* __restrict__ idx, const uint8_t* __restrict__ blocks,
+    const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G,
+    float alpha, float limit, float* __restrict__ act, int act_ld) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int kRS = mx_row_stride(kT1Nct);
+  constexpr int kUnits = kT1Kp / 16, kSclUnits = kMxSclRow / 16;
+  constexpr int kStage = 2 * (kUnits + kSclUnits);  // 16-byte units of the two piece rows
+  static_assert(kStage <= 2 * 256, "two units a thread");
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = blockIdx.y;
+  const int tile = blockIdx.x * 4 + wave;
+  const int e = __builtin_amdgcn_readfirstlane(idx[slot]);  // (a scalar load)
+  // the staging's loads first (they complete first), then the tile's
+  u32x4 sv[2];
+  uint32_t sd[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int u = min((int)threadIdx.x + 256 * i, kStage - 1);
+    const int p = u < 2 * kUnits ? u / kUnits : (u - 2 * kUnits) / kSclUnits;
+    const int c = u < 2 * kUnits ? u - p * kUnits : u - 2 * kUnits - p * kSclUnits;
+    sv[i] = u < 2 * kUnits ? *(const u32x4*)(tq + p * kT1Kp + c * 16)
+                           : *(const u32x4*)(tqs + p * kMxSclRow + c * 16);
+    sd[i] = u < 2 * kUnits ? p * kRS + c * 16 : 2 * kRS + p * kMxSclRow + c * 16;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  T1Tile t;
+  t1_issue(t, blocks, scales, bias, (size_t)e * N + (tile << 4), G);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) *(u32x4*)(lds + sd[i]) = sv[i];  // (repeats store the same bytes)
+  const uint32_t ss = 2 * kRS + 2 * kMxSclRow + wave * (16 * G);
+  t1_stage_scales(t, lds + ss, G);
+  lds_barrier();
+  f32x4 acc = t1_chain(lds, 0, 2, ss, t, G);
+  // the chain combines all 64 lanes: keep it out of the store branch below
+  asm volatile("" : "+v"(acc));
+  // lane group 0 holds the token (rows 0 and 1: its two pieces)
+  const float y0 = (acc[1] + acc[0]) + t.bn;
+  const float l0 = lane_xor1(y0);  // odd rows hold the linear half
+  if (g == 0 && (r & 1) == 0) {
+    const float xg = fminf(y0, limit);
+    const float xl = fminf(fmaxf(l0, -limit), limit);
+    const float z = __fmul_rn(alpha, xg);
+    const float sig = 1.0f / (1.0f + expf(-z));
+    const float v = __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+    act[(size_t)slot * act_ld + (((tile << 4) + r) >> 1)] = v;
+  }
+}
+
+// mlp2 of one token with the gated combine: workgroup c holds KT waves and
+// owns output columns 16 c .. 16 c + 15; wave s multiplies slot s's weight
+// tile (expert idx[s]) against the KT act rows, encoded into three pieces
+// while staged (rows 3 s + p, the P = 3 batch layout with the slots as its
+// tokens), and keeps its own slot's rows; the KT results meet in LDS and
+// out = bf16(x + bf16(sum_s y_s w_s)) is summed in slot order.
+template <int KT>
+__global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
+    const float* __restrict__ act, int K, const int* __restrict__ idx,
+    const uint16_t* __restrict__ gw, const uint16_t* __restrict__ x,
+    const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, int N, int G, uint16_t* __restrict__ out) {
+  static_assert(KT >= 1 && KT <= 5, "one 16-row operand group: 5 tokens of 3 pieces");
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int kRS = mx_row_stride(kT1Nct);
+  constexpr int kRows = 3 * KT;
+  constexpr int kThreads = 64 * KT;
+  constexpr int kBlk = kT1Nct * 4;                  // 32-element blocks per row (past K: zero)
+  constexpr int kTasks = KT * kBlk * 4;             // four threads per (row, block)
+  constexpr int kRounds = (kTasks + kThreads - 1) / kThreads;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t sbase = kRows * kRS + kRows * kMxSclRow;  // weight scale staging
+  float* const ys = (float*)(lds + sbase + KT * 16 * G);   // [KT][16]
+  const int e = __builtin_amdgcn_readfirstlane(idx[wave]);  // (a scalar load)
+  // the act values this thread encodes (loads first: they complete first)
+  f32x4 av[kRounds][2];
+#pragma unroll
+  for (int i = 0; i < kRounds; ++i) {
+    const int id = i * kThreads + (int)threadIdx.x;
+    const int idc = id < kTasks ? id : (id & 3);
+    const int rb = idc >> 2, tt = rb / kBlk, blk = rb - tt * kBlk;
+    const int k0 = blk * 32 + (idc & 3) * 8;
+    if (blk * 32 < K) {
+      const f32x4* src = (const f32x4*)(act + (size_t)tt * K + k0);
+      av[i][0] = src[0];
+      av[i][1] = src[1];
+    } else {
+      av[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      av[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  T1Tile t;
+  t1_issue(t, blocks, scales, bias, (size_t)e * N + ((size_t)blockIdx.x << 4), G);
+  __builtin_amdgcn_sched_barrier(0);
+  // Encode the KT rows into three pieces, as moe_pieces_kernel<3, true>
+  // does: four threads per 32-element block, the block maximum by lane
+  // exchange.  Whole quads past the end encode the first block and store
+  // nothing.
+#pragma unroll
+  for (int i = 0; i < kRounds; ++i) {
+    const int id = i * kThreads + (int)threadIdx.x;
+    const bool valid = id < kTasks;
+    const int idc = valid ? id : (id & 3);
+    const int quarter = idc & 3, rb = idc >> 2;
+    const int tt = rb / kBlk, blk = rb - tt * kBlk;
+    const int k0 = blk * 32 + quarter * 8;
+    const int c = blk >> 2, gg = blk & 3;
+    float rr[8] = {av[i][0][0], av[i][0][1], av[i][0][2], av[i][0][3],
+                   av[i][1][0], av[i][1][1], av[i][1][2], av[i][1][3]};
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(rr[j]));
+      amax = fmaxf(amax, lane_xor1(amax));
+      amax = fmaxf(amax, lane_xor2(amax));
+      const uint32_t sc = e8m0_for_amax(amax);
+      const float inv = __uint_as_float((254u - sc) << 23);
+      const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+      uint32_t lo, hi;
+      e4m3_piece8(rr, inv, scf, lo, hi);
+      if (valid) {
+        const int m = tt * 3 + p;
+        *(uint2*)(lds + m * kRS + k0) = make_uint2(lo, hi);
+        if (quarter == 0) lds[kRows * kRS + m * kMxSclRow + gg * kMxSclRun + c] = (uint8_t)sc;
+      }
+    }
+  }
+  const uint32_t ss = sbase + wave * (16 * G);
+  t1_stage_scales(t, lds + ss, G);
+  lds_barrier();
+  f32x4 acc = t1_chain(lds, 0, kRows, ss, t, G);
+  asm volatile("" : "+v"(acc));
+  // Rows 3 s + p hold piece p of slot s; lane group g holds rows 4 g .. 4 g + 3
+  // (the P = 3 epilogue of moe_mx_gemv_kernel: slot 1 straddles groups 0 and
+  // 1, slot 2 groups 1 and 2; sums run from the smallest piece up).
+  const float send = g == 1 ? acc[1] + acc[0] : acc[0];
+  const float recv = __shfl_down(send, 16, kWave);
+  float y;
+  int gs;
+  if (wave == 0) {
+    y = ((acc[2] + acc[1]) + acc[0]) + t.bn;
+    gs = 0;
+  } else if (wave == 1) {
+    y = (recv + acc[3]) + t.bn;
+    gs = 0;
+  } else if (wave == 2) {
+    y = ((recv + acc[3]) + acc[2]) + t.bn;
+    gs = 1;
+  } else if (wave == 3) {
+    y = ((acc[3] + acc[2]) + acc[1]) + t.bn;
+    gs = 2;
+  } else {
+    y = ((acc[2] + acc[1]) + acc[0]) + t.bn;
+    gs = 3;
+  }
+  if (g == gs) ys[wave * 16 + r] = y;
+  lds_barrier();
+  if (threadIdx.x < 16) {
+    // multiply and add round separately, as moe_gating_kernel does
+#pragma clang fp contract(off)
+    const int col = (blockIdx.x << 4) + (int)threadIdx.x;
+    float a = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KT; ++s) a = a + ys[s * 16 + threadIdx.x] * bf2f(gw[s]);
+    out[col] = f2bf(__fadd_rn(bf2f(x[col]), bf2f(f2bf(a))));
+  }
+}
+
 template <int P, int kEpi>
 int launch_mx(int NC, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const uint8_t* q,
               const uint8_t* qs, int Kp, const int* indptr, const int* sp, int k_top, int arow,
@@ -1327,6 +1589,51 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
 // value restores the default.  Returns the previous bound.
 int moe_decode_spin_limit_exchange(int polls) {
   return g_decode_spin_max.exchange(polls < 0 ? moe::kDecodeSpinMax : polls);
+}
+
+// kOk when the one-token launches (moe_mx_token1_*_kernel) take this shape:
+// k = 4 slots, H and I of 23 chunks of 128 (H, I multiples of 32).
+int moe_mx_token1_check(int k, int H, int I) {
+  using namespace moe;
+  if (k != 4) return kErrUnsupported;
+  if (H % 32 || I % 32 || (H + 127) / 128 != kT1Nct || (I + 127) / 128 != kT1Nct)
+    return kErrUnsupported;
+  return kOk;
+}
+
+// One token's mlp1 with SwiGLU: t pieces (2, one row) and the k expert
+// indices -> act rows by slot ([k][I], fp32).
+int moe_launch_mx_token1_mlp1(const void* t_packed, const void* idx, const void* blocks,
+                              const void* scales, const void* bias, int k, int H, int I,
+                              float alpha, float limit, void* act, hipStream_t stream) {
+  using namespace moe;
+  if (moe_mx_token1_check(k, H, I) != kOk) return kErrUnsupported;
+  const uint8_t* tq = (const uint8_t*)t_packed;
+  const int G = H / 32;
+  const size_t lds = 2 * mx_row_stride(kT1Nct) + 2 * kMxSclRow + 4 * 16 * G;
+  hipLaunchKernelGGL(moe_mx_token1_mlp1_kernel, dim3(2 * I / 64, k), dim3(256), lds, stream, tq,
+                     tq + moe_pieces_q_bytes(1, H, 2), (const int*)idx, (const uint8_t*)blocks,
+                     (const uint8_t*)scales, (const uint16_t*)bias, 2 * I, G, alpha, limit,
+                     (float*)act, I);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// One token's mlp2 with the gated combine and the residual: act rows by slot
+// ([k][I], fp32), the k expert indices and gate weights w, the token's x ->
+// out = bf16(x + bf16(sum_s y_s w_s)) ([H], bf16).
+int moe_launch_mx_token1_mlp2(const void* act, const void* idx, const void* w, const void* x,
+                              const void* blocks, const void* scales, const void* bias, int k,
+                              int H, int I, void* out, hipStream_t stream) {
+  using namespace moe;
+  if (moe_mx_token1_check(k, H, I) != kOk) return kErrUnsupported;
+  constexpr int KT = 4;
+  const int G = I / 32;
+  const size_t lds = 3 * KT * (mx_row_stride(kT1Nct) + kMxSclRow) + KT * 16 * G + KT * 16 * 4;
+  hipLaunchKernelGGL(moe_mx_token1_mlp2_kernel<KT>, dim3(H / 16), dim3(64 * KT), lds, stream,
+                     (const float*)act, I, (const int*)idx, (const uint16_t*)w,
+                     (const uint16_t*)x, (const uint8_t*)blocks, (const uint8_t*)scales,
+                     (const uint16_t*)bias, H, G, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 }  // extern "C"

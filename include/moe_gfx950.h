@@ -285,7 +285,7 @@ MOE_API int moe_block_forward(const uint16_t* x, int64_t n, int64_t E, int64_t k
 #define MOE_STAGE_DECODE 3        /* mlp1 + SwiGLU + act pieces + mlp2 in one launch (+ combine, n <= 32) */
 #define MOE_STAGE_MLP1 4          /* mlp1 + SwiGLU (prefill GEMM: act pieces in its epilogue) */
 #define MOE_STAGE_ACT_PIECES 5    /* act's fp8 pieces (GEMV path above 2 pairs per expert) */
-#define MOE_STAGE_MLP2 6          /* mlp2 */
+#define MOE_STAGE_MLP2 6          /* mlp2 (one token: with the gated combine) */
 #define MOE_STAGE_GATING 7        /* gated combine + residual */
 #define MOE_STAGE_ROUTER 8        /* ROUTER_LOGITS + SELECT in one launch (decode sizes) */
 
