@@ -334,9 +334,14 @@ __device__ __forceinline__ void mx_pass(
     });
   };
   // The scale bytes pass through LDS to reach the lane that needs each one.
+  // Lanes past the G units store unit G - 1 again (the bytes they loaded):
+  // with the stores under lane conditions, the compiler lost track of the
+  // loads still in flight across the branches and waited for all of them
+  // (vmcnt(0), the second half's loads included) before the tile's first
+  // MFMA.
   auto stage_scales = [&]() {
-    if (lane < G) *(u32x4*)(sstage + lane * 16) = sc0;
-    if (lane + 64 < G) *(u32x4*)(sstage + (lane + 64) * 16) = sc1;
+    *(u32x4*)(sstage + min(lane, G - 1) * 16) = sc0;
+    *(u32x4*)(sstage + min(lane + 64, G - 1) * 16) = sc1;
   };
   const uint32_t sstage_off = L.sstage + wave * (16 * G) + r * G;
   auto scale_b = [&](uint32_t ss, int c) -> uint32_t { return lds[ss + blk_of(c, g)]; };
@@ -473,7 +478,18 @@ __device__ __forceinline__ void mx_pass(
         if ((int)threadIdx.x < nb) rowmap[threadIdx.x] = sorted_pairs[start + b0 + (int)threadIdx.x];
         lds_barrier();
       }
-      if constexpr (kDirect) {
+      // Later segments stage through registers, not by direct-to-LDS loads:
+      // the compiler cannot tell which LDS bytes such a load writes, so with
+      // one inside this loop it waits for every load in flight (vmcnt(0))
+      // before each operand group's first MFMA, draining the two-stage tile
+      // pipeline; without one the chunk waits are exact (the GEMV passes at
+      // 120B decode 256: block 408-414 us against 416-420).  The decode
+      // launch's mlp1 pass (kEpi 3, one segment per workgroup, so this
+      // branch never runs there) keeps the direct staging and with it the
+      // drained waits: at decode 64 the launch measured 94.0 us that way,
+      // 94.9 with exact waits and 96.2 with an explicit vmcnt(0) at the same
+      // places (the code shapes differ).
+      if constexpr (kDirect && kEpi == 3) {
         fill_direct(start, b0, nb);
         wait_vmcnt<0>();
       } else if constexpr (kEpi == 2) {
@@ -545,13 +561,19 @@ __device__ __forceinline__ void mx_pass(
             const int row = arow_mode == 0 ? rowmap[tt] / k_top : arow_mode == 1 ? rowmap[tt] : j;
             const int gi = tt / TPG, m = (tt - gi * TPG) * P + p;
             const size_t prow = (size_t)row * P + p;
-            if (c < row16) {
-              v[i] = *(const u32x4*)(q + prow * Kp + c * 16);
-              dst[i] = gi * kMxGroupBytes + m * kMxRowStride + c * 16;
+            const uint8_t* src = c < row16 ? q + prow * Kp + c * 16
+                                           : qs + prow * kMxSclRow + (c - row16) * 16;
+            if constexpr (kWait) {
+              // other workgroups of this launch wrote the pieces (device scope)
+              const uint64_t lo = load_dev((const uint64_t*)src);
+              const uint64_t hi = load_dev((const uint64_t*)src + 1);
+              v[i] = u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
             } else {
-              v[i] = *(const u32x4*)(qs + prow * kMxSclRow + (c - row16) * 16);
-              dst[i] = gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow + (c - row16) * 16;
+              v[i] = *(const u32x4*)src;
             }
+            dst[i] = c < row16 ? gi * kMxGroupBytes + m * kMxRowStride + c * 16
+                               : gi * kMxGroupBytes + 16 * kMxRowStride + m * kMxSclRow +
+                                     (c - row16) * 16;
           }
 #pragma unroll
           for (int i = 0; i < kFill; ++i) *(u32x4*)(lds + dst[i]) = v[i];
