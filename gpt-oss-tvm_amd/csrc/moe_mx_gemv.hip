@@ -242,13 +242,87 @@ __device__ __forceinline__ int mx_expert_of(const int* pre, int E, int u) {
   return lo;
 }
 
+// The decode launch's shares with the workgroups weighted by cost.  Batches
+// lie expert after expert (tpb tokens each, an expert's last one the rest,
+// ntiles units each); a batch of nb tokens costs wa + ceil(nb / tpg) per
+// tile: a tile's MFMAs, A-operand reads and epilogue grow with its operand
+// groups (at decode 64, phase 2 took 0.96, 1.11 and 1.25-1.35 us per tile
+// and workgroup with 1, 2 and 3 groups; wa = 5 gives 6 : 7 : 8).  With NB
+// batches (NB <= grid) and W their total cost, batch b's workgroups start at
+// b + floor((grid - NB) * W_b / W), W_b the cost of the batches before it,
+// so each gets at least one and the rest in proportion to its cost.
+// Workgroup vb (numbered XCD-major as in mx_share) takes its equal share of
+// its batch's tiles, starting and ending on multiples of `align`.  indptr
+// may be the LDS copy.  Run by one wave; writes [ubeg, uend) to out[0],
+// out[1].
+__device__ __forceinline__ void mx_weighted_share(const int* __restrict__ indptr, int E, int tpb,
+                                                  int tpg, int wa, int ntiles, int align,
+                                                  int xcds, int* out) {
+  const int lane = threadIdx.x & 63;
+  const int grid = (int)gridDim.x;
+  const int vb = xcds > 1 ? (int)(blockIdx.x % xcds) * (grid / xcds) + (int)(blockIdx.x / xcds)
+                          : (int)blockIdx.x;
+  const int wfull = wa + (tpb + tpg - 1) / tpg;  // a full batch's cost
+  auto expert = [&](int e, int& nbat, int& wsum) {
+    nbat = 0;
+    wsum = 0;
+    if (e < E) {
+      const int cnt = indptr[e + 1] - indptr[e];
+      nbat = (cnt + tpb - 1) / tpb;
+      if (nbat > 0) wsum = (nbat - 1) * wfull + wa + (cnt - (nbat - 1) * tpb + tpg - 1) / tpg;
+    }
+  };
+  if (lane == 0) {
+    out[0] = 0;
+    out[1] = 0;
+  }
+  int NB = 0, W = 0;
+  for (int b = 0; b < E; b += 64) {
+    int nbat, wsum;
+    expert(b + lane, nbat, wsum);
+    NB += wave_sum(nbat);
+    W += wave_sum(wsum);
+  }
+  if (W == 0) return;
+  const int spare = grid - NB;
+  auto start_of = [&](int bi, int wp) { return bi + (int)((int64_t)spare * wp / W); };
+  int cb = 0, cw = 0;
+  for (int b = 0; b < E; b += 64) {
+    int nbat, wsum;
+    expert(b + lane, nbat, wsum);
+    int sb = nbat, sw = wsum;  // inclusive scans over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int tb = __shfl_up(sb, o, kWave), tw = __shfl_up(sw, o, kWave);
+      if (lane >= o) {
+        sb += tb;
+        sw += tw;
+      }
+    }
+    const int bb = cb + sb - nbat, wb = cw + sw - wsum;  // this expert's first batch, cost before it
+    for (int j = 0; j < nbat; ++j) {
+      const int s0 = start_of(bb + j, wb + j * wfull);
+      const int s1 = j + 1 < nbat ? start_of(bb + j + 1, wb + (j + 1) * wfull)
+                                  : start_of(bb + nbat, wb + wsum);
+      if (s0 <= vb && vb < s1) {
+        const int w = s1 - s0, i = vb - s0, na = ntiles / align, bi = bb + j;
+        out[0] = bi * ntiles + align * (na * i / w);
+        out[1] = bi * ntiles + align * (na * (i + 1) / w);
+      }
+    }
+    cb += __shfl(sb, 63, kWave);
+    cw += __shfl(sw, 63, kWave);
+  }
+}
+
 // One grouped GEMV pass over the units counted in L.pre (indptr in L.ipl).
 // align: with one segment per workgroup, shares of a batch start and end at
 // multiples of `align` tiles.  kWait: wait(e, b0, nb) runs before each
 // segment's staging, called by every thread and ending in a workgroup
 // barrier; the first segment's first tile loads are issued before it.
 // first: the share's first segment.  balance: mx_share's (the decode launch,
-// whose shares must be one segment each, leaves it off).
+// whose shares must be one segment each, leaves it off).  share (LDS, may be
+// null): [ubeg, uend) computed by the caller instead of mx_share's.
 template <int P, int kEpi, int NCT, bool kWait, class WaitFn>
 __device__ __forceinline__ void mx_pass(
     uint8_t* lds, const MxLds& L, const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs,
@@ -256,7 +330,7 @@ __device__ __forceinline__ void mx_pass(
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, int E, int groups_cap, float alpha,
     float limit, float* __restrict__ out, int out_ld, int xcds, int align, WaitFn&& wait,
-    MxSeg& first, bool balance = false) {
+    MxSeg& first, bool balance = false, const int* share = nullptr) {
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
@@ -276,7 +350,12 @@ __device__ __forceinline__ void mx_pass(
   first.e = -1;
 
   int ubeg, uend;
-  mx_share(pre, E, ntiles, align, xcds, ubeg, uend, balance);
+  if (share) {
+    ubeg = share[0];
+    uend = share[1];
+  } else {
+    mx_share(pre, E, ntiles, align, xcds, ubeg, uend, balance);
+  }
   if (ubeg >= uend) return;
   auto expert_of = [&](int u) { return mx_expert_of(pre, E, u); };
 
@@ -924,7 +1003,10 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   L2.pre = L1.tile_ctr + 16;
   const int* const ipl = (const int*)(lds + L1.ipl);
   constexpr int tpb2 = kMxMaxGroups * 5;  // (gcap2 == kMxMaxGroups)
-  if (threadIdx.x == 0) *(int*)(lds + L1.tile_ctr + 8) = 0;  // the combine's job count
+  // the 16 bytes at tile_ctr: [0] the pass's tile counter, [1..2] phase 2's
+  // share, [3] the combine's job count
+  int* const share2 = (int*)(lds + L1.tile_ctr + 4);
+  if (threadIdx.x == 0) *(int*)(lds + L1.tile_ctr + 12) = 0;
   if (wave == 0)
     mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
   else if (wave == 1)
@@ -937,6 +1019,11 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
       lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1, bias1, 2 * H, G, E,
       kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1);
   lds_barrier();  // every wave's SwiGLU outputs are in LDS
+  // Phase 2's share, weighted by the batches' operand groups, from the LDS
+  // copy of indptr (at the launch's start its global loads held every wave
+  // about 2 us at the first barrier); the publish barrier below makes it
+  // visible.
+  if (wave == 1) mx_weighted_share(ipl, E, tpb2, 5, 5, ntiles2, 1, xcds, share2);
   if (s1.e >= 0) {
     // Encode the share's act blocks: four threads per (token, 32-column
     // block), 8 columns each; the share that ends at column H also writes the
@@ -995,6 +1082,8 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     __syncthreads();
     if (threadIdx.x == 0)
       __hip_atomic_fetch_add(done + s1.e, s1.len, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    lds_barrier();  // (no share in phase 1) phase 2's share is in LDS
   }
 
   // Phase 2: wait for all of expert e's mlp1 tiles, then stage its pieces.
@@ -1033,7 +1122,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   MxSeg s2;
   mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
       lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
-      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2);
+      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2, false, share2);
 
   // The gated combine (with the residual), done by whichever workgroup writes
   // a token's last y tile: every workgroup holds one mlp2 segment (a batch's
@@ -1048,7 +1137,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const int nb = min(tpb2, ipl[s2.e + 1] - start - s2.b0);
     const int* rowmap = (const int*)(lds + L2.rowmap);  // the batch's sorted_pairs entries
     int* jobs = (int*)lds;                               // at most 15 x 180 ints
-    int* njobs = (int*)(lds + L2.tile_ctr + 8);          // zero since the start
+    int* njobs = (int*)(lds + L2.tile_ctr + 12);         // zero since the start
     for (int id = threadIdx.x; id < nb * s2.len; id += blockDim.x) {
       const int tt = id / s2.len, tile = s2.t0 + id - tt * s2.len;
       const int job = rowmap[tt] / k_top * ntiles2 + tile;
