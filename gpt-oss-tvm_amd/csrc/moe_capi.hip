@@ -59,6 +59,7 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
                          void* status, const void* w, const void* x, void* out, void* arrive,
+                         const void* logits, void* idx, void* route_w, void* const* route,
                          hipStream_t stream);
 int moe_mx_token1_check(int k, int H, int I);
 int moe_launch_mx_token1_mlp1(const void* t_packed, const void* idx, const void* blocks,
@@ -434,7 +435,8 @@ int moe_mlp_decode(const void* t_pieces, const int32_t* indptr, const int32_t* s
   return moe_launch_mx_decode(t_pieces, (int)n, indptr, sorted_pairs, (int)k, mlp1_blocks,
                               mlp1_scales, mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E,
                               (int)H, (int)I, (int)(n * k), alpha, limit, act_pieces, y, done,
-                              done + E, nullptr, nullptr, nullptr, nullptr, as_stream(stream));
+                              done + E, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                              nullptr, nullptr, as_stream(stream));
 }
 
 int moe_gemv_gating(const float* y, const uint16_t* w, const uint16_t* x, int64_t n, int64_t k,
@@ -526,8 +528,27 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   const bool decode = !gemm && n >= kDecodeLaunchMinTokens && n <= 128;
   const bool fuse = decode && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
-  // decode sizes: the logits launch's last workgroup runs the selection and
-  // grouping (one launch); otherwise two launches
+  // From kFusedCombineMaxTokens + 1 to 128 tokens (E <= 32, the launch
+  // fitting the device) the decode launch routes itself: the logits launch,
+  // the decode launch (each workgroup ranks the logits and groups the pairs;
+  // workgroup 0 writes idx, w and the grouping), the gating launch.
+  if (decode && !fuse && E <= 32 && n * E <= 4096 && nk <= 512 &&
+      moe_mx_decode_check((int)E, (int)H, (int)I, nk) == MOE_OK) {
+    void* const grouping[3] = {ti, ei, pp};
+    if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
+                                       logits, t_pk, t_qs, sync, s)) ||
+        (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)) ||
+        (rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
+                                   mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E,
+                                   (int)H, (int)I, nk, alpha, limit, act_pk, y, sync, sync + E,
+                                   nullptr, x, nullptr, counts, logits, idx, w, grouping, s)) ||
+        (rc = mark(m, MOE_STAGE_DECODE, s)) ||
+        (rc = moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s)))
+      return rc;
+    return mark(m, MOE_STAGE_GATING, s);
+  }
+  // other decode sizes: the logits launch's last workgroup runs the selection
+  // and grouping (one launch); otherwise two launches
   rc = MOE_ERR_UNSUPPORTED;
   if (!gemm && n <= 128) {
     int32_t* arrive = (int32_t*)ws + kCounterRouter;
@@ -557,7 +578,8 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
     rc = moe_launch_mx_decode(t_pk, (int)n, indptr, sp, (int)k, mlp1_blocks, mlp1_scales,
                               mlp1_bias, mlp2_blocks, mlp2_scales, mlp2_bias, (int)E, (int)H,
                               (int)I, nk, alpha, limit, act_pk, y, sync, sync + E,
-                              fuse ? w : nullptr, x, fuse ? out : nullptr, counts, s);
+                              fuse ? w : nullptr, x, fuse ? out : nullptr, counts, nullptr,
+                              nullptr, nullptr, nullptr, s);
     if (rc == MOE_OK && (rc = mark(m, MOE_STAGE_DECODE, s))) return rc;
     if (rc == MOE_OK && !fuse) {
       if ((rc = moe_launch_gating(y, w, x, (int)n, (int)k, (int)H, out, sync + E, s))) return rc;

@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "moe_common.h"
+#include "moe_select.h"
 
 namespace moe {
 
@@ -323,6 +324,8 @@ __device__ __forceinline__ void mx_weighted_share(const int* __restrict__ indptr
 // first: the share's first segment.  balance: mx_share's (the decode launch,
 // whose shares must be one segment each, leaves it off).  share (LDS, may be
 // null): [ubeg, uend) computed by the caller instead of mx_share's.
+// rowmap_ready: the caller put the first segment's sorted_pairs entries in
+// L.rowmap (the decode launch's own routing); they are not loaded.
 template <int P, int kEpi, int NCT, bool kWait, class WaitFn>
 __device__ __forceinline__ void mx_pass(
     uint8_t* lds, const MxLds& L, const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs,
@@ -330,7 +333,8 @@ __device__ __forceinline__ void mx_pass(
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, int E, int groups_cap, float alpha,
     float limit, float* __restrict__ out, int out_ld, int xcds, int align, WaitFn&& wait,
-    MxSeg& first, bool balance = false, const int* share = nullptr) {
+    MxSeg& first, bool balance = false, const int* share = nullptr,
+    bool rowmap_ready = false) {
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
   constexpr int kMxGroupBytes = mx_group_bytes(NCT);
@@ -483,9 +487,10 @@ __device__ __forceinline__ void mx_pass(
   if constexpr (kDirect && kWait) {
     // the first tile's loads go out before the wait, the staging after it
     const int start = ipl[sg.e], nb = min(tpb, ipl[sg.e + 1] - start - sg.b0);
-    if (arow_mode != 2 && (int)threadIdx.x < nb)
+    if (!rowmap_ready && arow_mode != 2 && (int)threadIdx.x < nb)
       rowmap[threadIdx.x] = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
-    const bool rm_lane = arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
+    const bool rm_lane =
+        !rowmap_ready && arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
     int rm = 0;
     if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
     if (threadIdx.x == 0) *tile_ctr = 0;
@@ -507,12 +512,13 @@ __device__ __forceinline__ void mx_pass(
     // in issue order, so the first MFMAs then wait for their own tile only
     // rather than for a whole chip-wide round of tile loads.
     const int start = ipl[sg.e], nb = min(tpb, ipl[sg.e + 1] - start - sg.b0);
-    if (arow_mode != 2) {
+    if (!rowmap_ready && arow_mode != 2) {
       if ((int)threadIdx.x < nb) rowmap[threadIdx.x] = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
       __syncthreads();  // (nothing else in flight)
     }
     fill_direct(start, sg.b0, nb);
-    const bool rm_lane = arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
+    const bool rm_lane =
+        !rowmap_ready && arow_mode == 2 && orow_mode == 0 && (int)threadIdx.x < nb;
     int rm = 0;
     if (rm_lane) rm = sorted_pairs[start + sg.b0 + (int)threadIdx.x];
     if (threadIdx.x == 0) *tile_ctr = 0;
@@ -973,6 +979,29 @@ __device__ __forceinline__ void combine4(__amdgpu_buffer_rsrc_t yr, const uint16
   }
   *(uint2*)(out + (size_t)tok * H + c0) = make_uint2(o[0], o[1]);
 }
+// The decode launch's own routing (kept null: indptr and sorted_pairs are
+// given).  With logits ([n][E] floats holding bf16 values, E <= 32, n E <=
+// kDecodeRouteKeys) every workgroup ranks them in LDS, counts and places the
+// pairs (the router's selection and stable grouping, the same code) and keeps
+// the row maps of its own two batches; workgroup 0 also writes the routing
+// outputs (idx, w, indptr, sorted_pairs, token_indices, expert_ids,
+// pair_pos), which the gating launch after it reads.  One logits launch then
+// does the router's work: its last-arriver selection (a device-scope count,
+// then one workgroup ranking every token) took about 9 of its 14 us at 64
+// tokens.
+struct DecodeRoute {
+  const float* logits;
+  int n;
+  int32_t* idx;
+  uint16_t* w;
+  int32_t* indptr;
+  int32_t* sorted_pairs;
+  int32_t* token_indices;
+  int32_t* expert_ids;
+  int32_t* pair_pos;
+};
+constexpr int kDecodeRouteKeys = 4096;
+
 __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
     const int* __restrict__ indptr, const int* __restrict__ sorted_pairs, int k_top,
@@ -981,7 +1010,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const uint8_t* __restrict__ scales2, const uint16_t* __restrict__ bias2, int H, int E,
     int gcap2, float alpha, float limit, uint8_t* aq, uint8_t* aqs, float* __restrict__ y,
     int* done, int* status, int spin_max, int prepoll, int xcds, const uint16_t* __restrict__ gw,
-    const uint16_t* __restrict__ resid, uint16_t* __restrict__ out, int* arrive) {
+    const uint16_t* __restrict__ resid, uint16_t* __restrict__ out, int* arrive, DecodeRoute rt) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kGroupBytes = mx_group_bytes(23);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1001,29 +1030,140 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   L1.act = kDecodeGroups1 * kGroupBytes;
   MxLds L2 = L1;
   L2.pre = L1.tile_ctr + 16;
+  L2.rowmap = L1.rowmap + 64;  // phase 1's batch: 16 entries at most, phase 2's: 15
   const int* const ipl = (const int*)(lds + L1.ipl);
   constexpr int tpb2 = kMxMaxGroups * 5;  // (gcap2 == kMxMaxGroups)
   // the 16 bytes at tile_ctr: [0] the pass's tile counter, [1..2] phase 2's
   // share, [3] the combine's job count
   int* const share2 = (int*)(lds + L1.tile_ctr + 4);
   if (threadIdx.x == 0) *(int*)(lds + L1.tile_ctr + 12) = 0;
-  if (wave == 0)
-    mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
-  else if (wave == 1)
-    mx_unit_prefix(indptr, E, tpb2, ntiles2, (int*)(lds + L2.pre), nullptr);
-  __syncthreads();
+  const bool route = rt.logits != nullptr;
+  if (route) {
+    // Scratch in the operand groups (free until phase 1's staging).
+    const int n = rt.n, np = n * k_top, tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63;
+    float* lg = (float*)lds;                  // [n][E]
+    uint32_t* wk = (uint32_t*)(lds + 16384);  // the ranked keys, [t][k]
+    int* pidx = (int*)(lds + 18432);          // each pair's expert
+    int* cnt = (int*)(lds + 20480);           // [E]
+    int* ipl2 = (int*)(lds + 21504);          // wave 1's copy of indptr, [E + 1]
+    int* const ipl_w = (int*)(lds + L1.ipl);
+    for (int i = tid; i < (n * E) >> 2; i += nthr)
+      ((f32x4*)lg)[i] = ((const f32x4*)rt.logits)[i];
+    for (int e = tid; e < E; e += nthr) cnt[e] = 0;
+    __syncthreads();
+    rank_halves(lg, n, E, k_top, wk, [&](int t, int j, uint32_t key) {
+      const int e = key_expert(key);
+      pidx[t * k_top + j] = e;
+      atomicAdd(&cnt[e], 1);
+    });
+    __syncthreads();
+    // indptr (the exclusive prefix of the counts), by the wave that needs it
+    auto wave_indptr = [&](int* dst) {
+      int carry = 0;
+      for (int b = 0; b < E; b += 64) {
+        const int e = b + lane;
+        const int c = e < E ? cnt[e] : 0;
+        int v = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int u = __shfl_up(v, o, kWave);
+          if (lane >= o) v += u;
+        }
+        if (e < E) dst[e] = carry + v - c;
+        carry += __shfl(v, 63, kWave);
+      }
+      if (lane == 0) dst[E] = carry;
+    };
+    // The pairs of batch (e, b0, nb) in the grouping's stable order (token,
+    // then slot, within an expert) by one wave: ballots over the pairs'
+    // experts rank each pair among its expert's; rank b0 + tt goes to
+    // rowmap[tt], and with `out` the batch's grouping entries (sorted
+    // position ipl[e] + rank) are written.
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    auto batch_pairs = [&](const int* ip, int e, int b0, int nb, int* rowmap, bool out) {
+      int seen = 0;
+      for (int c0 = 0; c0 < np; c0 += 64) {
+        const int p = c0 + lane;
+        const bool m = p < np && pidx[p] == e;
+        const uint64_t bal = __ballot(m);
+        const int r = seen + __popcll(bal & lt) - b0;
+        if (m && r >= 0 && r < nb) {
+          rowmap[r] = p;
+          if (out) {
+            const int pos = ip[e] + b0 + r;
+            rt.sorted_pairs[pos] = p;
+            rt.token_indices[pos] = p / k_top;
+            rt.expert_ids[pos] = e;
+            rt.pair_pos[p] = pos;
+          }
+        }
+        seen += __popcll(bal);
+      }
+    };
+    if (wave == 0) {
+      // phase 1's batch (mx_share's batch split, as mx_pass computes it)
+      int* pre1 = (int*)(lds + L1.pre);
+      wave_indptr(ipl_w);
+      mx_unit_prefix(ipl, E, tpb1, ntiles1, pre1, nullptr);
+      int ub, ue;
+      mx_share(pre1, E, ntiles1, 4, xcds, ub, ue);
+      if (ub < ue) {
+        const int e1 = mx_expert_of(pre1, E, ub);
+        const int b0 = (ub - pre1[e1]) / ntiles1 * tpb1;
+        batch_pairs(ipl, e1, b0, min(tpb1, ipl[e1 + 1] - ipl[e1] - b0), (int*)(lds + L1.rowmap),
+                    false);
+      }
+    } else if (wave == 1) {
+      // phase 2's batch (the weighted share); the workgroup whose share starts
+      // at the batch's first tile (one per batch) writes its grouping entries
+      int* pre2 = (int*)(lds + L2.pre);
+      wave_indptr(ipl2);
+      mx_unit_prefix(ipl2, E, tpb2, ntiles2, pre2, nullptr);
+      mx_weighted_share(ipl2, E, tpb2, 5, 5, ntiles2, 1, xcds, share2);
+      const int ub = share2[0], ue = share2[1];
+      if (ub < ue) {
+        const int e2 = mx_expert_of(pre2, E, ub);
+        const int b0 = (ub - pre2[e2]) / ntiles2 * tpb2;
+        batch_pairs(ipl2, e2, b0, min(tpb2, ipl2[e2 + 1] - ipl2[e2] - b0),
+                    (int*)(lds + L2.rowmap), (ub - pre2[e2]) % ntiles2 == 0);
+      }
+    } else if (wave == 2 && (int)blockIdx.x < n) {
+      // token blockIdx.x's gate weights and experts: the router's softmax
+      // (fp64, summed in rank order)
+      const int t = blockIdx.x;
+      const double ex = lane < k_top ? pair_exp(wk, t * k_top + lane, k_top) : 0.0;
+      double sum = readlane_f64(ex, 0);
+      for (int jj = 1; jj < k_top; ++jj) sum += readlane_f64(ex, jj);
+      if (lane < k_top) {
+        rt.w[t * k_top + lane] = f64_to_bf16_via_f32(ex / sum);
+        rt.idx[t * k_top + lane] = pidx[t * k_top + lane];
+      }
+    } else if (wave == 3 && blockIdx.x == 0) {
+      int* ipl3 = ipl2 + (E + 1);  // wave 3's copy
+      wave_indptr(ipl3);
+      for (int e = lane; e <= E; e += 64) rt.indptr[e] = ipl3[e];
+    }
+    __syncthreads();
+  } else {
+    if (wave == 0)
+      mx_unit_prefix(indptr, E, tpb1, ntiles1, (int*)(lds + L1.pre), (int*)(lds + L1.ipl));
+    else if (wave == 1)
+      mx_unit_prefix(indptr, E, tpb2, ntiles2, (int*)(lds + L2.pre), nullptr);
+    __syncthreads();
+  }
 
   MxSeg s1;
   auto no_wait = [](int, int, int) {};
   mx_pass<2, 3, 23, false, decltype(no_wait)&>(
       lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1, bias1, 2 * H, G, E,
-      kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1);
+      kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1, false, nullptr, route);
   lds_barrier();  // every wave's SwiGLU outputs are in LDS
   // Phase 2's share, weighted by the batches' operand groups, from the LDS
   // copy of indptr (at the launch's start its global loads held every wave
   // about 2 us at the first barrier); the publish barrier below makes it
   // visible.
-  if (wave == 1) mx_weighted_share(ipl, E, tpb2, 5, 5, ntiles2, 1, xcds, share2);
+  if (wave == 1 && !route) mx_weighted_share(ipl, E, tpb2, 5, 5, ntiles2, 1, xcds, share2);
   if (s1.e >= 0) {
     // Encode the share's act blocks: four threads per (token, 32-column
     // block), 8 columns each; the share that ends at column H also writes the
@@ -1122,7 +1262,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   MxSeg s2;
   mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
       lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
-      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2, false, share2);
+      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2, false, share2, route);
 
   // The gated combine (with the residual), done by whichever workgroup writes
   // a token's last y tile: every workgroup holds one mlp2 segment (a batch's
@@ -1665,17 +1805,32 @@ int moe_mx_decode_check(int E, int H, int I, int nk) {
 // workgroups whose bounded wait gave up (their y rows are wrong).
 // With out (and w, x, arrive: n * H / 16 ints, zero at launch) the launch also
 // writes out = bf16(x + bf16(sum_r y[t, r] w[t, r])) (the gated combine).
+// With logits (n x E, E <= 32, n E <= 4096 and a multiple of 4, 16-byte
+// aligned, nk <= 512; not with out) the
+// launch routes itself and writes idx, the gate weights route_w, indptr,
+// sorted_pairs and the other grouping arrays (route: token_indices,
+// expert_ids, pair_pos).
 int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          const void* sorted_pairs, int k_top, const void* blocks1,
                          const void* scales1, const void* bias1, const void* blocks2,
                          const void* scales2, const void* bias2, int E, int H, int I, int nk,
                          float alpha, float limit, void* act_packed, void* y, void* done,
                          void* status, const void* w, const void* x, void* out, void* arrive,
+                         const void* logits, void* idx, void* route_w, void* const* route,
                          hipStream_t stream) {
   using namespace moe;
   if (nk <= 0) return kOk;
   if (!done || !status) return kErrUnsupported;
   if (out && (!w || !x || !arrive || (H & 15))) return kErrUnsupported;
+  DecodeRoute rt{};
+  if (logits) {
+    if (out || !idx || !route_w || !route || E > 32 || (int64_t)n * E > kDecodeRouteKeys ||
+        (n * E) % 4 || nk > 512 || nk != n * k_top || ((uintptr_t)logits & 15u))
+      return kErrUnsupported;
+    rt = DecodeRoute{(const float*)logits, n, (int32_t*)idx, (uint16_t*)route_w,
+                     (int32_t*)indptr, (int32_t*)sorted_pairs, (int32_t*)route[0],
+                     (int32_t*)route[1], (int32_t*)route[2]};
+  }
   const int rc = moe_mx_decode_check(E, H, I, nk);
   if (rc != kOk) return rc;
   const int grid = kNumCUs;
@@ -1692,7 +1847,7 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                      aq, aq + moe_pieces_q_bytes(nk, I, 3), (float*)y, (int*)done,
                      (int*)status, g_decode_spin_max.load(std::memory_order_relaxed),
                      nk <= kDecodePrepollMaxPairs ? 1 : 0, grid % kNumXcds == 0 ? kNumXcds : 1,
-                     (const uint16_t*)w, (const uint16_t*)x, (uint16_t*)out, (int*)arrive);
+                     (const uint16_t*)w, (const uint16_t*)x, (uint16_t*)out, (int*)arrive, rt);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -9,6 +9,7 @@
 #include <cstdlib>
 
 #include "moe_common.h"
+#include "moe_select.h"
 
 namespace moe {
 
@@ -555,90 +556,6 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
 }
 
 
-// Placement of pairs [p0, p1) of a stable counting sort by expert, given
-// base[e] (LDS) = the sorted position of the chunk's first pair of expert e.
-// Within a round of 1024 pairs a pair's rank among same-expert pairs comes
-// from ballots, so pairs keep flattened (token, slot) order inside each
-// expert, exactly as np.argsort(kind="stable").  Pairs whose expert id is out
-// of range are not placed (pair_pos = -1).  All threads of the workgroup (at
-// most 1024) call it; a round is blockDim.x pairs.
-__device__ __forceinline__ void place_pairs(const int32_t* idx, int p0, int p1, int k, int E,
-                                            int* base, int* wcnt,
-                                            int32_t* __restrict__ sorted_pairs,
-                                            int32_t* __restrict__ token_indices,
-                                            int32_t* __restrict__ expert_ids,
-                                            int32_t* __restrict__ pair_pos) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int nthr = blockDim.x;
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int round0 = p0; round0 < p1; round0 += nthr) {
-    const int p = round0 + tid;
-    const bool inb = p < p1;
-    const int v = inb ? idx[p] : -1;
-    const bool ok = inb && v >= 0 && v < E;
-    for (int i = tid; i < 16 * E; i += nthr) wcnt[(i / E) * 256 + (i % E)] = 0;
-    __syncthreads();
-    uint64_t same = __ballot(ok);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = ((v >> b) & 1) != 0;
-      const uint64_t bb = __ballot(ok && bit);
-      same &= bit ? bb : ~bb;
-    }
-    const int rank = __popcll(same & lt);
-    if (ok && rank == 0) wcnt[wave * 256 + v] = __popcll(same);
-    __syncthreads();
-    // per expert: the waves' counts become their exclusive prefix (in wave
-    // order) on top of base, and base moves past the round
-    const int nwv = (nthr + 63) >> 6;
-    for (int e = tid; e < E; e += nthr) {
-      int run = base[e];
-      for (int w = 0; w < nwv; ++w) {
-        const int c = wcnt[w * 256 + e];
-        wcnt[w * 256 + e] = run;
-        run += c;
-      }
-      base[e] = run;
-    }
-    __syncthreads();
-    if (ok) {
-      const int pos = wcnt[wave * 256 + v] + rank;
-      sorted_pairs[pos] = p;
-      token_indices[pos] = p / k;
-      expert_ids[pos] = v;
-      pair_pos[p] = pos;
-    } else if (inb) {
-      pair_pos[p] = -1;
-    }
-    __syncthreads();
-  }
-}
-
-// Exclusive prefix over experts of tot[e] (LDS), by wave 0: base[e] +=
-// prefix, and indptr (when given) = the prefix with indptr[E] = the total.
-__device__ __forceinline__ void expert_prefix(const int* tot, int E, int* base,
-                                              int32_t* __restrict__ indptr) {
-  const int lane = threadIdx.x & 63;
-  if (threadIdx.x >= 64) return;
-  int carry = 0;
-  for (int b = 0; b < E; b += 64) {
-    const int e = b + lane;
-    const int c = e < E ? tot[e] : 0;
-    int v = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(v, o, 64);
-      if (lane >= o) v += t;
-    }
-    if (e < E) {
-      base[e] += carry + v - c;
-      if (indptr) indptr[e] = carry + v - c;
-    }
-    carry += __shfl(v, 63, 64);
-  }
-  if (indptr && lane == 0) indptr[E] = carry;
-}
-
 // Ranking keys staged in LDS for the selection: 16 K keys (64 KB) per pass,
 // at most kSelTok tokens.
 constexpr int kSelLds = 16384;
@@ -752,25 +669,6 @@ __global__ __launch_bounds__(1024) void moe_select_permute_kernel(
               pair_pos);
 }
 
-// Maximum of v over this lane's 32-lane half of the wave, in registers: DPP
-// quad permutes, half-row and row mirrors (the row's maximum in every lane),
-// then v_permlane16_swap for the two rows of the half.  All lanes active.
-__device__ __forceinline__ uint32_t half_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
-  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return max((uint32_t)b[0], (uint32_t)b[1]);
-}
-
-__device__ __forceinline__ double readlane_f64(double x, int l) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, x);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
-  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
 // Top-k + softmax of n tokens whose logits are in LDS (lg [n][E], E <= 32),
 // two tokens per wave, one per 32-lane half: lane e holds expert e's ranking
 // key; k rounds of the half's maximum (registers only) give the keys in rank
@@ -784,32 +682,14 @@ __device__ __forceinline__ void select_halves(const float* lg, int n, int E, int
                                               int32_t* __restrict__ idx_out,
                                               uint16_t* __restrict__ w_out, int* ti, int* hist,
                                               uint32_t* wk, double* ex) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int half = lane >> 5, e = lane & 31;
-  for (int t0 = 2 * wave; t0 < n; t0 += 2 * nw) {
-    const int t = t0 + half;
-    const bool live = t < n;
-    // keys below every real key (rank_key(-inf, e) >= 0x007F0000) pad the half
-    uint32_t key = (live && e < E) ? rank_key(lg[t * E + e], e) : 0u;
-    for (int j = 0; j < k; ++j) {
-      const uint32_t m = half_max_u32(key);
-      if (live && e == j) wk[t * k + j] = m;
-      if (key == m) key = 0u;  // keys are distinct (the expert is in the low bits)
-    }
-  }
+  rank_halves(lg, n, E, k, wk);
   lds_barrier();
   const int np = n * k;
-  for (int p = threadIdx.x; p < np; p += blockDim.x) {
-    const int t = p / k;
-    ex[p] = exp((double)key_value(wk[p]) - (double)key_value(wk[t * k]));
-  }
+  for (int p = threadIdx.x; p < np; p += blockDim.x) ex[p] = pair_exp(wk, p, k);
   lds_barrier();
   for (int p = threadIdx.x; p < np; p += blockDim.x) {
-    const int t0 = p / k * k;
-    double sum = ex[t0];
-    for (int jj = 1; jj < k; ++jj) sum += ex[t0 + jj];
-    const int ex_id = 0xFFFF - (int)(wk[p] & 0xFFFFu);
-    w_out[p] = f64_to_bf16_via_f32(ex[p] / sum);
+    const int ex_id = key_expert(wk[p]);
+    w_out[p] = pair_weight(ex, p, k);
     idx_out[p] = ex_id;
     ti[p] = ex_id;
     atomicAdd(&hist[ex_id], 1);
