@@ -979,16 +979,21 @@ __device__ __forceinline__ void combine4(__amdgpu_buffer_rsrc_t yr, const uint16
   }
   *(uint2*)(out + (size_t)tok * H + c0) = make_uint2(o[0], o[1]);
 }
-// The decode launch's own routing (kept null: indptr and sorted_pairs are
+// The decode launch's own routing (logits null: indptr and sorted_pairs are
 // given).  With logits ([n][E] floats holding bf16 values, E <= 32, n E <=
-// kDecodeRouteKeys) every workgroup ranks them in LDS, counts and places the
-// pairs (the router's selection and stable grouping, the same code) and keeps
-// the row maps of its own two batches; workgroup 0 also writes the routing
-// outputs (idx, w, indptr, sorted_pairs, token_indices, expert_ids,
-// pair_pos), which the gating launch after it reads.  One logits launch then
-// does the router's work: its last-arriver selection (a device-scope count,
-// then one workgroup ranking every token) took about 9 of its 14 us at 64
-// tokens.
+// kDecodeRouteKeys) every workgroup ranks them in LDS with the router's
+// ranking code, counts each expert's pairs, takes indptr from the counts and
+// finds its two batches' pairs in the grouping's stable order (token, then
+// slot, within an expert) by ballots over the pairs' experts, without a full
+// sort.  The routing outputs are written on the way, spread out: token t's
+// gate weights (the router's fp64 softmax) and experts by workgroup t, each
+// batch's grouping entries (sorted_pairs, token_indices, expert_ids,
+// pair_pos) by the workgroup whose mlp2 share starts at the batch's first
+// tile, indptr by workgroup 0; the gating launch after this one reads w.  The
+// router is then one logits launch: its last-arriver selection (a
+// device-scope count, then one workgroup ranking and grouping every token)
+// took about 9 of its 14 us at 64 tokens, and the routing here costs the
+// decode launch about 4.
 struct DecodeRoute {
   const float* logits;
   int n;
