@@ -219,7 +219,9 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
         t = stage_us["decode"]
         achieved = alg / (t * 1e-6) / 1e9
         roof = {"bound": "hbm",
-                "kernel": "moe_mx_decode_kernel (mlp1 + SwiGLU + act pieces + mlp2"
+                "kernel": "moe_mx_decode_kernel ("
+                          + ("routing + " if "router_logits" in stage_us else "")
+                          + "mlp1 + SwiGLU + act pieces + mlp2"
                           + (" + gated combine)" if "gating" not in stage_us else ")"),
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
