@@ -61,11 +61,12 @@ int moe_launch_mx_decode(const void* t_packed, int n, const void* indptr,
                          void* status, const void* w, const void* x, void* out, void* arrive,
                          const void* logits, void* idx, void* route_w, void* const* route,
                          hipStream_t stream);
-int moe_mx_token1_check(int k, int H, int I);
-int moe_launch_mx_token1_mlp1(const void* t_packed, const void* idx, const void* blocks,
-                              const void* scales, const void* bias, int k, int H, int I,
-                              float alpha, float limit, void* act, hipStream_t stream);
-int moe_launch_mx_token1_mlp2(const void* act, const void* idx, const void* w, const void* x,
+int moe_mx_token1_check(int E, int k, int H, int I);
+int moe_launch_mx_token1_mlp1(const void* t_packed, const void* logits, int E,
+                              void* const* route, const void* blocks, const void* scales,
+                              const void* bias, int k, int H, int I, float alpha, float limit,
+                              void* act, hipStream_t stream);
+int moe_launch_mx_token1_mlp2(const void* act, const void* logits, int E, const void* x,
                               const void* blocks, const void* scales, const void* bias, int k,
                               int H, int I, void* out, hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -528,6 +529,23 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   const bool decode = !gemm && n >= kDecodeLaunchMinTokens && n <= 128;
   const bool fuse = decode && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
+  // One token (the shape permitting): the logits launch, then mlp1 and mlp2
+  // with the gated combine, each wave on one weight tile (act by slot, [k][I]
+  // fp32); both route the token themselves from its logits, and mlp1's first
+  // workgroup writes idx, w and the grouping.
+  if (n == 1 && !gemm && moe_mx_token1_check((int)E, (int)k, (int)H, (int)I) == MOE_OK) {
+    void* const route[7] = {idx, w, indptr, sp, ti, ei, pp};
+    if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
+                                       logits, t_pk, t_qs, nullptr, s)) ||
+        (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)) ||
+        (rc = moe_launch_mx_token1_mlp1(t_pk, logits, (int)E, route, mlp1_blocks, mlp1_scales,
+                                        mlp1_bias, (int)k, (int)H, (int)I, alpha, limit, act, s)) ||
+        (rc = mark(m, MOE_STAGE_MLP1, s)) ||
+        (rc = moe_launch_mx_token1_mlp2(act, logits, (int)E, x, mlp2_blocks, mlp2_scales,
+                                        mlp2_bias, (int)k, (int)H, (int)I, out, s)))
+      return rc;
+    return mark(m, MOE_STAGE_MLP2, s);
+  }
   // From kFusedCombineMaxTokens + 1 to 128 tokens (E <= 32, the launch
   // fitting the device) the decode launch routes itself: the logits launch,
   // the decode launch (each workgroup ranks the logits and groups the pairs;
@@ -586,17 +604,6 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
       return mark(m, MOE_STAGE_GATING, s);
     }
     if (rc != MOE_ERR_UNSUPPORTED) return rc;
-  }
-  // One token (the shape permitting): mlp1, then mlp2 with the gated combine,
-  // each wave on one weight tile (act by slot, [k][I] fp32).
-  if (n == 1 && !gemm && moe_mx_token1_check((int)k, (int)H, (int)I) == MOE_OK) {
-    if ((rc = moe_launch_mx_token1_mlp1(t_pk, idx, mlp1_blocks, mlp1_scales, mlp1_bias, (int)k,
-                                        (int)H, (int)I, alpha, limit, act, s)) ||
-        (rc = mark(m, MOE_STAGE_MLP1, s)) ||
-        (rc = moe_launch_mx_token1_mlp2(act, idx, w, x, mlp2_blocks, mlp2_scales, mlp2_bias,
-                                        (int)k, (int)H, (int)I, out, s)))
-      return rc;
-    return mark(m, MOE_STAGE_MLP2, s);
   }
   if (gemm) {
     if ((rc = mlp1_pieces(t_pk, n, k, E, H, I, indptr, sp, mlp1_blocks, mlp1_scales, mlp1_bias,

@@ -1386,14 +1386,28 @@ __device__ __forceinline__ f32x4 t1_chain(const uint8_t* lds, uint32_t a_base, i
   return acc;
 }
 
+// The one-token launches route the token themselves from its E <= 32
+// logits (each wave: the router's one-token top-k and softmax, registers
+// only), so the router is its logits launch alone.  The first mlp1
+// workgroup writes the routing outputs.
+struct Token1Route {
+  int32_t* idx;
+  uint16_t* w;
+  int32_t* indptr;
+  int32_t* sorted_pairs;
+  int32_t* token_indices;
+  int32_t* expert_ids;
+  int32_t* pair_pos;
+};
+
 // mlp1 of one token with the interleaved SwiGLU epilogue: workgroup
 // (q, slot) holds 4 waves, wave v the weight tile 4 q + v (16 rows: 8 gate
-// and 8 linear, interleaved) of expert idx[slot]; act row `slot` ([k][I],
-// fp32) gets its 8 columns.  t's two pieces (rows 0 and 1 of tq, scale rows
-// of tqs) are staged in LDS.
+// and 8 linear, interleaved) of the expert of rank `slot`; act row `slot`
+// ([k][I], fp32) gets its 8 columns.  t's two pieces (rows 0 and 1 of tq,
+// scale rows of tqs) are staged in LDS.
 __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
-    const int* __restrict__ idx, const uint8_t* __restrict__ blocks,
+    const float* __restrict__ logits, int E, Token1Route rt, const uint8_t* __restrict__ blocks,
     const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G,
     float alpha, float limit, float* __restrict__ act, int act_ld) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -1403,10 +1417,11 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
   static_assert(kStage <= 2 * 256, "two units a thread");
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slot = blockIdx.y;
+  const int slot = blockIdx.y, k = gridDim.y;
   const int tile = blockIdx.x * 4 + wave;
-  const int e = __builtin_amdgcn_readfirstlane(idx[slot]);  // (a scalar load)
-  // the staging's loads first (they complete first), then the tile's
+  // the logits and the staging's loads first (they complete first), then the
+  // tile's, once the token's experts are known
+  const float v = lane < E ? logits[lane] : 0.0f;
   u32x4 sv[2];
   uint32_t sd[2];
 #pragma unroll
@@ -1419,9 +1434,16 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
     sd[i] = u < 2 * kUnits ? p * kRS + c * 16 : 2 * kRS + p * kMxSclRow + c * 16;
   }
   __builtin_amdgcn_sched_barrier(0);
+  int id;
+  uint16_t wt;
+  one_token_topk(v, E, k, id, wt);
+  const int e = __builtin_amdgcn_readlane(id, slot);
   T1Tile t;
   t1_issue(t, blocks, scales, bias, (size_t)e * N + (tile << 4), G);
   __builtin_amdgcn_sched_barrier(0);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
+    route_one_token(v, E, k, rt.idx, rt.w, rt.indptr, rt.sorted_pairs, rt.token_indices,
+                    rt.expert_ids, rt.pair_pos);
 #pragma unroll
   for (int i = 0; i < 2; ++i) *(u32x4*)(lds + sd[i]) = sv[i];  // (repeats store the same bytes)
   const uint32_t ss = 2 * kRS + 2 * kMxSclRow + wave * (16 * G);
@@ -1444,15 +1466,16 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
 }
 
 // mlp2 of one token with the gated combine: workgroup c holds KT waves and
-// owns output columns 16 c .. 16 c + 15; wave s multiplies slot s's weight
-// tile (expert idx[s]) against the KT act rows, encoded into three pieces
+// owns output columns 16 c .. 16 c + 15; wave s multiplies the weight tile of
+// the expert of rank s against the KT act rows, encoded into three pieces
 // while staged (rows 3 s + p, the P = 3 batch layout with the slots as its
 // tokens), and keeps its own slot's rows; the KT results meet in LDS and
-// out = bf16(x + bf16(sum_s y_s w_s)) is summed in slot order.
+// out = bf16(x + bf16(sum_s y_s w_s)) is summed in slot order (w: the
+// router's bf16 gate weights).
 template <int KT>
 __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
-    const float* __restrict__ act, int K, const int* __restrict__ idx,
-    const uint16_t* __restrict__ gw, const uint16_t* __restrict__ x,
+    const float* __restrict__ act, int K, const float* __restrict__ logits, int E,
+    const uint16_t* __restrict__ x,
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, uint16_t* __restrict__ out) {
   static_assert(KT >= 1 && KT <= 5, "one 16-row operand group: 5 tokens of 3 pieces");
@@ -1467,8 +1490,10 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t sbase = kRows * kRS + kRows * kMxSclRow;  // weight scale staging
   float* const ys = (float*)(lds + sbase + KT * 16 * G);   // [KT][16]
-  const int e = __builtin_amdgcn_readfirstlane(idx[wave]);  // (a scalar load)
-  // the act values this thread encodes (loads first: they complete first)
+  uint16_t* const wsl = (uint16_t*)(ys + KT * 16);          // [KT] gate weights
+  // the logits and the act values this thread encodes first (they complete
+  // first), then the tile's loads, once the token's experts are known
+  const float v = lane < E ? logits[lane] : 0.0f;
   f32x4 av[kRounds][2];
 #pragma unroll
   for (int i = 0; i < kRounds; ++i) {
@@ -1486,9 +1511,14 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  int id;
+  uint16_t wt;
+  one_token_topk(v, E, KT, id, wt);
+  const int e = __builtin_amdgcn_readlane(id, wave);
   T1Tile t;
   t1_issue(t, blocks, scales, bias, (size_t)e * N + ((size_t)blockIdx.x << 4), G);
   __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0 && lane < KT) wsl[lane] = wt;
   // Encode the KT rows into three pieces, as moe_pieces_kernel<3, true>
   // does: four threads per 32-element block, the block maximum by lane
   // exchange.  Whole quads past the end encode the first block and store
@@ -1559,7 +1589,7 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
     const int col = (blockIdx.x << 4) + (int)threadIdx.x;
     float a = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KT; ++s) a = a + ys[s * 16 + threadIdx.x] * bf2f(gw[s]);
+    for (int s = 0; s < KT; ++s) a = a + ys[s * 16 + threadIdx.x] * bf2f(wsl[s]);
     out[col] = f2bf(__fadd_rn(bf2f(x[col]), bf2f(f2bf(a))));
   }
 }
@@ -1863,45 +1893,53 @@ int moe_decode_spin_limit_exchange(int polls) {
 }
 
 // kOk when the one-token launches (moe_mx_token1_*_kernel) take this shape:
-// k = 4 slots, H and I of 23 chunks of 128 (H, I multiples of 32).
-int moe_mx_token1_check(int k, int H, int I) {
+// E <= 32 experts, k = 4 slots, H and I of 23 chunks of 128 (H, I multiples
+// of 32).
+int moe_mx_token1_check(int E, int k, int H, int I) {
   using namespace moe;
-  if (k != 4) return kErrUnsupported;
+  if (k != 4 || E < k || E > 32) return kErrUnsupported;
   if (H % 32 || I % 32 || (H + 127) / 128 != kT1Nct || (I + 127) / 128 != kT1Nct)
     return kErrUnsupported;
   return kOk;
 }
 
-// One token's mlp1 with SwiGLU: t pieces (2, one row) and the k expert
-// indices -> act rows by slot ([k][I], fp32).
-int moe_launch_mx_token1_mlp1(const void* t_packed, const void* idx, const void* blocks,
-                              const void* scales, const void* bias, int k, int H, int I,
-                              float alpha, float limit, void* act, hipStream_t stream) {
+// One token's mlp1 with SwiGLU: t pieces (2, one row) and its E logits ->
+// act rows by slot ([k][I], fp32); route: idx, w, indptr, sorted_pairs,
+// token_indices, expert_ids, pair_pos, written by the first workgroup.
+int moe_launch_mx_token1_mlp1(const void* t_packed, const void* logits, int E,
+                              void* const* route, const void* blocks, const void* scales,
+                              const void* bias, int k, int H, int I, float alpha, float limit,
+                              void* act, hipStream_t stream) {
   using namespace moe;
-  if (moe_mx_token1_check(k, H, I) != kOk) return kErrUnsupported;
+  if (moe_mx_token1_check(E, k, H, I) != kOk) return kErrUnsupported;
+  const Token1Route rt{(int32_t*)route[0], (uint16_t*)route[1], (int32_t*)route[2],
+                       (int32_t*)route[3], (int32_t*)route[4], (int32_t*)route[5],
+                       (int32_t*)route[6]};
   const uint8_t* tq = (const uint8_t*)t_packed;
   const int G = H / 32;
   const size_t lds = 2 * mx_row_stride(kT1Nct) + 2 * kMxSclRow + 4 * 16 * G;
   hipLaunchKernelGGL(moe_mx_token1_mlp1_kernel, dim3(2 * I / 64, k), dim3(256), lds, stream, tq,
-                     tq + moe_pieces_q_bytes(1, H, 2), (const int*)idx, (const uint8_t*)blocks,
+                     tq + moe_pieces_q_bytes(1, H, 2), (const float*)logits, E, rt,
+                     (const uint8_t*)blocks,
                      (const uint8_t*)scales, (const uint16_t*)bias, 2 * I, G, alpha, limit,
                      (float*)act, I);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 // One token's mlp2 with the gated combine and the residual: act rows by slot
-// ([k][I], fp32), the k expert indices and gate weights w, the token's x ->
-// out = bf16(x + bf16(sum_s y_s w_s)) ([H], bf16).
-int moe_launch_mx_token1_mlp2(const void* act, const void* idx, const void* w, const void* x,
+// ([k][I], fp32), the token's E logits and x -> out = bf16(x + bf16(sum_s
+// y_s w_s)) ([H], bf16).
+int moe_launch_mx_token1_mlp2(const void* act, const void* logits, int E, const void* x,
                               const void* blocks, const void* scales, const void* bias, int k,
                               int H, int I, void* out, hipStream_t stream) {
   using namespace moe;
-  if (moe_mx_token1_check(k, H, I) != kOk) return kErrUnsupported;
+  if (moe_mx_token1_check(E, k, H, I) != kOk) return kErrUnsupported;
   constexpr int KT = 4;
   const int G = I / 32;
-  const size_t lds = 3 * KT * (mx_row_stride(kT1Nct) + kMxSclRow) + KT * 16 * G + KT * 16 * 4;
+  const size_t lds =
+      3 * KT * (mx_row_stride(kT1Nct) + kMxSclRow) + KT * 16 * G + KT * 16 * 4 + KT * 2;
   hipLaunchKernelGGL(moe_mx_token1_mlp2_kernel<KT>, dim3(H / 16), dim3(64 * KT), lds, stream,
-                     (const float*)act, I, (const int*)idx, (const uint16_t*)w,
+                     (const float*)act, I, (const float*)logits, E,
                      (const uint16_t*)x, (const uint8_t*)blocks, (const uint8_t*)scales,
                      (const uint16_t*)bias, H, G, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;

@@ -696,45 +696,16 @@ __device__ __forceinline__ void select_halves(const float* lg, int n, int E, int
   }
 }
 
-// One token (E <= 32, k <= 8) by one wave, registers only: the same ranking
-// keys, k rounds of the half-wave maximum and fp64 softmax as select_halves
-// (lanes 0..31), then the stable counting sort of its k pairs by expert from
-// lane reads (a pair's position: the pairs of a lower expert, and those of
-// its expert with a lower slot), and indptr (lane e: the pairs of an expert
-// below e).  The same outputs as the workgroup form, bit for bit, with no
-// LDS round trip or barrier.
+// One token (E <= 32, k <= 8) by one wave: route_one_token (moe_select.h).
+// The logits were written by other workgroups of this launch (device-scope
+// loads).
 __device__ __forceinline__ void select_one_token(const float* logits, int E,
                                                  const SelectArgs& sel) {
-  const int lane = threadIdx.x & 63, k = sel.k;
+  const int lane = threadIdx.x & 63;
   const float v = lane < E ? load_dev(logits + lane) : 0.0f;
   for (int i = lane; i < sel.zero_ints; i += 64) sel.zero[i] = 0;
-  uint32_t key = lane < E ? rank_key(v, lane) : 0u;
-  uint32_t win = 0u;
-  for (int j = 0; j < k; ++j) {
-    const uint32_t m = half_max_u32(key);
-    if (lane == j) win = m;
-    if (key == m) key = 0u;
-  }
-  const uint32_t top = (uint32_t)__builtin_amdgcn_readlane((int)win, 0);
-  const double ex = lane < k ? exp((double)key_value(win) - (double)key_value(top)) : 0.0;
-  double sum = readlane_f64(ex, 0);
-  for (int jj = 1; jj < k; ++jj) sum += readlane_f64(ex, jj);
-  const int id = 0xFFFF - (int)(win & 0xFFFFu);
-  int below_e = 0, pos = 0;  // lane e: pairs of experts below e; lane j < k: pair j's position
-  for (int q = 0; q < k; ++q) {
-    const int xq = __builtin_amdgcn_readlane(id, q);
-    below_e += xq < lane ? 1 : 0;
-    pos += (xq < id || (xq == id && q < lane)) ? 1 : 0;
-  }
-  if (lane <= E) sel.indptr[lane] = below_e;
-  if (lane < k) {
-    sel.w[lane] = f64_to_bf16_via_f32(ex / sum);
-    sel.idx[lane] = id;
-    sel.sorted_pairs[pos] = lane;
-    sel.token_indices[pos] = 0;
-    sel.expert_ids[pos] = id;
-    sel.pair_pos[lane] = pos;
-  }
+  route_one_token(v, E, sel.k, sel.idx, sel.w, sel.indptr, sel.sorted_pairs, sel.token_indices,
+                  sel.expert_ids, sel.pair_pos);
 }
 
 // The selection and grouping of moe_select_permute_kernel, run by the last

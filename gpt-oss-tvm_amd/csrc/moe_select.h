@@ -73,6 +73,58 @@ __device__ __forceinline__ uint16_t pair_weight(const double* ex, int p, int k) 
   return f64_to_bf16_via_f32(ex[p] / sum);
 }
 
+// One token's top-k and softmax by one wave (E <= 32, k <= 8), registers
+// only: lane e < E holds expert e's logit v; the same ranking keys, k rounds
+// of the half-wave maximum and fp64 softmax against rank 0, summed in rank
+// order, as the workgroup forms.  Lanes j < k get rank j's expert (id) and
+// gate weight (w, bf16); every lane of the wave must call it.
+__device__ __forceinline__ void one_token_topk(float v, int E, int k, int& id, uint16_t& w) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key = lane < E ? rank_key(v, lane) : 0u;
+  uint32_t win = 0u;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t m = half_max_u32(key);
+    if (lane == j) win = m;
+    if (key == m) key = 0u;
+  }
+  const uint32_t top = (uint32_t)__builtin_amdgcn_readlane((int)win, 0);
+  const double ex = lane < k ? exp((double)key_value(win) - (double)key_value(top)) : 0.0;
+  double sum = readlane_f64(ex, 0);
+  for (int jj = 1; jj < k; ++jj) sum += readlane_f64(ex, jj);
+  id = key_expert(win);
+  w = lane < k ? f64_to_bf16_via_f32(ex / sum) : (uint16_t)0;
+}
+
+// One token's routing outputs by one wave: one_token_topk, then the stable
+// counting sort of its k pairs by expert from lane reads (a pair's position:
+// the pairs of a lower expert, and those of its expert with a lower slot) and
+// indptr (lane e: the pairs of an expert below e) -- the same outputs as the
+// workgroup forms, bit for bit, with no LDS round trip or barrier.
+__device__ __forceinline__ void route_one_token(float v, int E, int k, int32_t* idx, uint16_t* w,
+                                                int32_t* indptr, int32_t* sorted_pairs,
+                                                int32_t* token_indices, int32_t* expert_ids,
+                                                int32_t* pair_pos) {
+  const int lane = threadIdx.x & 63;
+  int id;
+  uint16_t wt;
+  one_token_topk(v, E, k, id, wt);
+  int below_e = 0, pos = 0;  // lane e: pairs of experts below e; lane j < k: pair j's position
+  for (int q = 0; q < k; ++q) {
+    const int xq = __builtin_amdgcn_readlane(id, q);
+    below_e += xq < lane ? 1 : 0;
+    pos += (xq < id || (xq == id && q < lane)) ? 1 : 0;
+  }
+  if (lane <= E) indptr[lane] = below_e;
+  if (lane < k) {
+    w[lane] = wt;
+    idx[lane] = id;
+    sorted_pairs[pos] = lane;
+    token_indices[pos] = 0;
+    expert_ids[pos] = id;
+    pair_pos[lane] = pos;
+  }
+}
+
 // Placement of pairs [p0, p1) of a stable counting sort by expert, given
 // base[e] (LDS) = the sorted position of the chunk's first pair of expert e.
 // Within a round of 1024 pairs a pair's rank among same-expert pairs comes

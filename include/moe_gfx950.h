@@ -251,9 +251,10 @@ MOE_API int moe_swiglu(const float* x, int64_t rows, int64_t d, float alpha, flo
  * bytes, 256-byte aligned; its layout is given by moe_workspace_layout().
  * Its first 256 bytes hold counters that must be zero before the first call
  * (allocate the workspace zero-filled); every call leaves them at zero, so a
- * workspace can serve calls of any n, in order on one stream.  (At decode
- * sizes the router's logits launch counts its finished workgroups there and
- * the last one runs the top-k, softmax and grouping.)
+ * workspace can serve calls of any n, in order on one stream.  (From 2 to 32
+ * tokens the router's logits launch counts its finished workgroups there and
+ * the last one runs the top-k, softmax and grouping; at one token and from 33
+ * to 128 tokens the launches after the logits launch route themselves.)
  */
 MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, int64_t I);
 
