@@ -9,9 +9,13 @@
 // rounding (the matmul's output dtype), then the epilogue's own bf16 ops.
 // HBM-bound on W.  A workgroup takes RW rows of W; its 4 waves split K (wave
 // w takes the 16-byte chunks w * 64 + lane + 256 i of each row), so a row's
-// bytes stream from four waves at once, all of a lane's loads issued before
-// anything else; the four partial sums are added in wave order through LDS
-// (deterministic).  The tokens x are staged in LDS.
+// bytes stream from four waves at once; the four partial sums are added in
+// wave order through LDS (deterministic).  The tokens x are staged in LDS.
+// Loads complete in issue order, so everything small that the workgroup
+// needs (its x chunks, the epilogue's bias, residual, positions, slots and
+// RoPE frequencies) is loaded before the W rows, and the epilogue's cos and
+// sin are taken while W streams: the RMSNorm and the epilogue then wait for
+// nothing behind the W loads.
 #include "moe_common.h"
 
 namespace gemv {
@@ -86,10 +90,44 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
 #pragma unroll
     for (int i = 0; i < RW; ++i) rows[i] = blockIdx.x * RW + i;
   }
-  // Every W load of this lane goes out first (K <= 4096: at most two rounds of
-  // 256 16-byte chunks), with the norm weight's chunks when the rows are
-  // normalised, so the staging of x runs under their latency.
+  // x's chunks of this thread (one token: at eight, holding them would cost
+  // occupancy) and the epilogue's operands first (they are needed first),
+  // then every W load of this lane (K <= 4096: at most two rounds of 256
+  // 16-byte chunks) with the norm weight's chunks when the rows are
+  // normalised.
   const bool norm = a.norm_w != nullptr;
+  constexpr bool kEarlyX = MM == 1;
+  u32x4 xr[kEarlyX ? 1 : 0 + 1][kIters];
+  if constexpr (kEarlyX) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int c = it * kThreads + t;
+      xr[0][it] = c < chunks ? *(const u32x4*)(a.x + c * 8) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // the epilogue task of this thread (one per row or rope pair, and token)
+  constexpr int kTasks = EPI == kQkv ? RW / 2 : RW;
+  const bool task = t < kTasks * M;
+  const int ti = task ? t / M : 0, tm = task ? t % M : 0;
+  float eb0 = 0.f, eb1 = 0.f, er = 0.f, cs = 0.f, sn = 0.f, ifq = 0.f;
+  int eslot = -1, epos = 0;
+  if constexpr (EPI == kBiasResidual) {
+    const int n = rows[ti];
+    if (task && n < N) {
+      eb0 = bf2f(a.bias[n]);
+      er = bf2f(a.res[(size_t)tm * N + n]);
+    }
+  } else if constexpr (EPI == kQkv) {
+    const int nlo = rows[2 * ti], nhi = rows[2 * ti + 1];
+    if (task) {
+      eb0 = bf2f(a.bias[nlo]);
+      eb1 = bf2f(a.bias[nhi]);
+      eslot = a.slots[tm];
+      epos = a.positions[tm];
+      ifq = a.inv_freq[nlo % kD];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   u32x4 wv[kIters][RW];
   u32x4 nwv[kIters];
 #pragma unroll
@@ -101,13 +139,28 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
                                               : u32x4{0u, 0u, 0u, 0u};
     nwv[it] = (norm && c < chunks) ? *(const u32x4*)(a.norm_w + c * 8) : u32x4{0u, 0u, 0u, 0u};
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // the RoPE factors while W streams
+  if constexpr (EPI == kQkv) {
+    if (task && rows[2 * ti] / kD < kHq + kHkv) {
+      const float freq = (float)epos * ifq;
+      const double fd = (double)freq;
+      cs = bf2f(f2bf((float)cos(fd))) * a.conc;
+      sn = bf2f(f2bf((float)sin(fd))) * a.conc;
+    }
+  }
   // Stage x; for the RMSNorm, the sum of squares of the bf16 values in fp64
   // (exact for rows spanning less than 2^37) on the way, as the standalone
   // kernel: r = fp32(1 / sqrt(ss / K + eps)), t = bf16(fp32(x r) w)
-  for (int m = 0; m < M; ++m) {
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    if (m >= M) break;
     double ss = 0.0;
-    for (int c = t; c < chunks; c += kThreads) {
-      const u32x4 v = *(const u32x4*)(a.x + (size_t)m * K + c * 8);
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int c = it * kThreads + t;
+      if (c >= chunks) continue;
+      const u32x4 v = kEarlyX ? xr[0][it] : *(const u32x4*)(a.x + (size_t)m * K + c * 8);
       *(u32x4*)(xs + m * K + c * 8) = v;
       if (norm) {
 #pragma unroll
@@ -177,39 +230,35 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
     return ((part[0][i][m] + part[1][i][m]) + part[2][i][m]) + part[3][i][m];
   };
   if constexpr (EPI == kPlain || EPI == kBiasResidual) {
-    if (t < RW * M) {
-      const int i = t / M, m = t % M, n = rows[i];
+    if (task) {
+      const int i = ti, m = tm, n = rows[i];
       if (n < N) {
         const uint16_t y = f2bf(total(i, m));
         if constexpr (EPI == kPlain) {
           a.out[(size_t)m * N + n] = y;
         } else {
-          const float tb = bf2f(f2bf(bf2f(y) + bf2f(a.bias[n])));
-          a.out[(size_t)m * N + n] = f2bf(bf2f(a.res[(size_t)m * N + n]) + tb);
+          const float tb = bf2f(f2bf(bf2f(y) + eb0));
+          a.out[(size_t)m * N + n] = f2bf(er + tb);
         }
       }
     }
   } else {
     // bias (its own bf16 rounding), then YaRN RoPE of q / k heads exactly as
     // the standalone append kernel does, then q out or the cache slot
-    if (t < (RW / 2) * M) {
-      const int i = t / M, m = t % M;
-      const int nlo = rows[2 * i], nhi = rows[2 * i + 1];
+    if (task) {
+      const int i = ti, m = tm;
+      const int nlo = rows[2 * i];
       const int head = nlo / kD, d = nlo % kD;
-      float lo = bf2f(f2bf(bf2f(f2bf(total(2 * i, m))) + bf2f(a.bias[nlo])));
-      float hi = bf2f(f2bf(bf2f(f2bf(total(2 * i + 1, m))) + bf2f(a.bias[nhi])));
+      float lo = bf2f(f2bf(bf2f(f2bf(total(2 * i, m))) + eb0));
+      float hi = bf2f(f2bf(bf2f(f2bf(total(2 * i + 1, m))) + eb1));
       if (head < kHq + kHkv) {
-        const float freq = (float)a.positions[m] * a.inv_freq[d];
-        const double fd = (double)freq;
-        const float c = bf2f(f2bf((float)cos(fd))) * a.conc;
-        const float s = bf2f(f2bf((float)sin(fd))) * a.conc;
-        const float nl = lo * c - hi * s;
-        const float nh = lo * s + hi * c;
+        const float nl = lo * cs - hi * sn;
+        const float nh = lo * sn + hi * cs;
         lo = nl;
         hi = nh;
       }
       const uint16_t blo = f2bf(lo), bhi = f2bf(hi);
-      const int slot = a.slots[m];
+      const int slot = eslot;
       if (head < kHq) {
         uint16_t* qo = a.q_out + ((size_t)m * kHq + head) * kD;
         qo[d] = blo;
