@@ -14,6 +14,9 @@ namespace moe {
 // status (if not null): nonzero when the producer of y reported incomplete
 // results (the decode launch's bounded wait gave up); every output is then
 // written as NaN, so a wrong result cannot pass for a right one.
+// KT > 0: k == KT known at compile time (the loads of every slot issued
+// without a branch between them); KT == 0: any k <= 8.
+template <int KT>
 __global__ __launch_bounds__(256) void moe_gating_kernel(const float* __restrict__ y,
                                                          const uint16_t* __restrict__ w,
                                                          const uint16_t* __restrict__ x, int k,
@@ -25,37 +28,45 @@ __global__ __launch_bounds__(256) void moe_gating_kernel(const float* __restrict
   const int tok = blockIdx.y;
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= N) return;
-  if (status && *status != 0) {
-    *(uint2*)(out + (size_t)tok * N + c) = make_uint2(0x7FC07FC0u, 0x7FC07FC0u);
-    return;
-  }
-  // all k loads first (k <= 8), then the in-order sum
-  f32x4 v[8];
-  float wr[8];
+  // Every load in one round: the k rows and weights, the residual and the
+  // status word, so the kernel waits for one memory round trip, not for the
+  // status before the rows.  Then the in-order sum.  (With k known only at
+  // run time the compiler waits for each slot's weight inside its branch.)
+  if constexpr (KT > 0) k = KT;
+  constexpr int kMax = KT > 0 ? KT : 8;
+  f32x4 v[kMax];
+  uint16_t wraw[kMax];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    if (r < k) {
+  for (int r = 0; r < kMax; ++r) {
+    if (KT > 0 || r < k) {
       v[r] = *(const f32x4*)(y + ((size_t)tok * k + r) * N + c);
-      wr[r] = bf2f(w[(size_t)tok * k + r]);
+      wraw[r] = w[(size_t)tok * k + r];
     }
   }
+  uint16_t xr[4] = {0, 0, 0, 0};
+  if (x) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[i] = x[(size_t)tok * N + c + i];
+  }
+  const int st = status ? *status : 0;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    if (r < k) {
+  for (int r = 0; r < kMax; ++r) {
+    if (KT > 0 || r < k) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + v[r][i] * wr[r];
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + v[r][i] * bf2f(wraw[r]);
     }
   }
   uint16_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint16_t g = f2bf(acc[i]);
-    o[i] = x ? f2bf(__fadd_rn(bf2f(x[(size_t)tok * N + c + i]), bf2f(g))) : g;
+    o[i] = x ? f2bf(__fadd_rn(bf2f(xr[i]), bf2f(g))) : g;
   }
   uint2 pk;
   pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
   pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+  if (st != 0) pk = make_uint2(0x7FC07FC0u, 0x7FC07FC0u);
   *(uint2*)(out + (size_t)tok * N + c) = pk;
 }
 
@@ -78,9 +89,14 @@ extern "C" int moe_launch_gating(const void* y, const void* w, const void* x, in
                                  void* out, const void* status, hipStream_t stream) {
   if (n == 0) return moe::kOk;
   const dim3 grid((N / 4 + 255) / 256, n);
-  hipLaunchKernelGGL(moe::moe_gating_kernel, grid, dim3(256), 0, stream, (const float*)y,
-                     (const uint16_t*)w, (const uint16_t*)x, k, N, (uint16_t*)out,
-                     (const int*)status);
+  if (k == 4)
+    hipLaunchKernelGGL(moe::moe_gating_kernel<4>, grid, dim3(256), 0, stream, (const float*)y,
+                       (const uint16_t*)w, (const uint16_t*)x, k, N, (uint16_t*)out,
+                       (const int*)status);
+  else
+    hipLaunchKernelGGL(moe::moe_gating_kernel<0>, grid, dim3(256), 0, stream, (const float*)y,
+                       (const uint16_t*)w, (const uint16_t*)x, k, N, (uint16_t*)out,
+                       (const int*)status);
   return hipGetLastError() == hipSuccess ? moe::kOk : moe::kErrLaunch;
 }
 
