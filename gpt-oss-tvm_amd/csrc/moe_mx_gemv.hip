@@ -333,7 +333,7 @@ __device__ __forceinline__ void mx_pass(
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, int E, int groups_cap, float alpha,
     float limit, float* __restrict__ out, int out_ld, int xcds, int align, WaitFn&& wait,
-    MxSeg& first, bool balance = false, const int* share = nullptr,
+    MxSeg& first, int nthr, bool balance = false, const int* share = nullptr,
     bool rowmap_ready = false) {
   constexpr int TPG = 16 / P;  // tokens per 16-row operand group
   constexpr int kMxRowStride = mx_row_stride(NCT);
@@ -341,7 +341,10 @@ __device__ __forceinline__ void mx_pass(
   const int lane = threadIdx.x & 63;
   // wave index in a scalar register: branches on it are uniform
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = blockDim.x >> 6;
+  // nthr = blockDim.x, read once by the caller: blockDim comes from the
+  // dispatch packet by a vector load, so each read waits for every load in
+  // flight before it (the tile loads, in a later segment's staging)
+  const int nwaves = nthr >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int ntiles = N >> 4;
   const int tpb = groups_cap * TPG;
@@ -538,7 +541,7 @@ __device__ __forceinline__ void mx_pass(
 
   if (NCT * 128 > Kp) {  // zero the K tail of every staged row once
     const int tail16 = (NCT * 128 - Kp) >> 4;
-    for (int u = threadIdx.x; u < groups_cap * 16 * tail16; u += blockDim.x) {
+    for (int u = threadIdx.x; u < groups_cap * 16 * tail16; u += nthr) {
       const int row = u / tail16, c = u - row * tail16;
       *(u32x4*)(lds + (row >> 4) * kMxGroupBytes + (row & 15) * kMxRowStride + Kp + c * 16) =
           u32x4{0u, 0u, 0u, 0u};
@@ -587,7 +590,7 @@ __device__ __forceinline__ void mx_pass(
         const int K = G * 32;
         const int nblk = NCT * 4;
         const int tasks = nb * nblk * 4;
-        for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
+        for (int t0q = 0; t0q < tasks; t0q += nthr) {
           const int id = t0q + threadIdx.x;
           const bool valid = id < tasks;
           const int idc = valid ? id : (id & 3);
@@ -634,12 +637,12 @@ __device__ __forceinline__ void mx_pass(
         const int row16 = Kp >> 4;
         const int units = row16 + kMxSclRow / 16;
         const int total_units = nb * P * units;
-        for (int u0 = threadIdx.x; u0 < total_units; u0 += kFill * blockDim.x) {
+        for (int u0 = threadIdx.x; u0 < total_units; u0 += kFill * nthr) {
           u32x4 v[kFill];
           uint32_t dst[kFill];
 #pragma unroll
           for (int i = 0; i < kFill; ++i) {
-            const int uu = min(u0 + i * (int)blockDim.x, total_units - 1);
+            const int uu = min(u0 + i * nthr, total_units - 1);
             const int rp = uu / units, c = uu - rp * units;
             const int tt = rp / P, p = rp - tt * P;
             const int j = start + b0 + tt;
@@ -898,7 +901,8 @@ __global__ __launch_bounds__(NCT == 23 ? 768 : 512) void moe_mx_gemv_kernel(
   MxSeg first;
   mx_pass<P, kEpi, NCT, false>(lds, L, q, qs, Kp, sorted_pairs, k_top, arow_mode, orow_mode,
                                blocks, scales, bias, N, G, E, groups_cap, alpha, limit, out,
-                               out_ld, xcds, 1, [](int, int, int) {}, first, true);
+                               out_ld, xcds, 1, [](int, int, int) {}, first, (int)blockDim.x,
+                               true);
 }
 
 // ---------------------------------------------------------------------------
@@ -1019,7 +1023,8 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kGroupBytes = mx_group_bytes(23);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = blockDim.x >> 6;
+  const int nthr = blockDim.x;  // read once (a vector load from the dispatch packet)
+  const int nwaves = nthr >> 6;
   const int G = H >> 5, Kp = 23 * 128;
   const int ntiles1 = (2 * H) >> 4, ntiles2 = H >> 4;
   const int tpb1 = kDecodeGroups1 * 8;
@@ -1045,7 +1050,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   const bool route = rt.logits != nullptr;
   if (route) {
     // Scratch in the operand groups (free until phase 1's staging).
-    const int n = rt.n, np = n * k_top, tid = threadIdx.x, nthr = blockDim.x;
+    const int n = rt.n, np = n * k_top, tid = threadIdx.x;
     const int lane = tid & 63;
     float* lg = (float*)lds;                  // [n][E]
     uint32_t* wk = (uint32_t*)(lds + 16384);  // the ranked keys, [t][k]
@@ -1057,7 +1062,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
       ((f32x4*)lg)[i] = ((const f32x4*)rt.logits)[i];
     for (int e = tid; e < E; e += nthr) cnt[e] = 0;
     __syncthreads();
-    rank_halves(lg, n, E, k_top, wk, [&](int t, int j, uint32_t key) {
+    rank_halves(lg, n, E, k_top, wk, nwaves, [&](int t, int j, uint32_t key) {
       const int e = key_expert(key);
       pidx[t * k_top + j] = e;
       atomicAdd(&cnt[e], 1);
@@ -1162,7 +1167,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   auto no_wait = [](int, int, int) {};
   mx_pass<2, 3, 23, false, decltype(no_wait)&>(
       lds, L1, tq, tqs, Kp, sorted_pairs, k_top, 0, 1, blocks1, scales1, bias1, 2 * H, G, E,
-      kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1, false, nullptr, route);
+      kDecodeGroups1, alpha, limit, nullptr, 0, xcds, 4, no_wait, s1, nthr, false, nullptr, route);
   lds_barrier();  // every wave's SwiGLU outputs are in LDS
   // Phase 2's share, weighted by the batches' operand groups, from the LDS
   // copy of indptr (at the launch's start its global loads held every wave
@@ -1179,7 +1184,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const int nbt = nblk + (s1.t0 + s1.len == ntiles1 ? 4 * 23 - G : 0);
     const int tasks = nb * nbt * 4;
     const float* act = (const float*)(lds + L1.act);
-    for (int t0q = 0; t0q < tasks; t0q += blockDim.x) {
+    for (int t0q = 0; t0q < tasks; t0q += nthr) {
       const int id = t0q + threadIdx.x;
       const bool valid = id < tasks;
       const int idc = valid ? id : (id & 3);
@@ -1267,7 +1272,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
   MxSeg s2;
   mx_pass<3, 0, 23, true, decltype(wait_mlp1)&>(
       lds, L2, aq, aqs, Kp, sorted_pairs, k_top, 2, 0, blocks2, scales2, bias2, H, G, E,
-      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2, false, share2, route);
+      kMxMaxGroups, 0.0f, 0.0f, y, H, xcds, 1, wait_mlp1, s2, nthr, false, share2, route);
 
   // The gated combine (with the residual), done by whichever workgroup writes
   // a token's last y tile: every workgroup holds one mlp2 segment (a batch's
@@ -1283,7 +1288,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const int* rowmap = (const int*)(lds + L2.rowmap);  // the batch's sorted_pairs entries
     int* jobs = (int*)lds;                               // at most 15 x 180 ints
     int* njobs = (int*)(lds + L2.tile_ctr + 12);         // zero since the start
-    for (int id = threadIdx.x; id < nb * s2.len; id += blockDim.x) {
+    for (int id = threadIdx.x; id < nb * s2.len; id += nthr) {
       const int tt = id / s2.len, tile = s2.t0 + id - tt * s2.len;
       const int job = rowmap[tt] / k_top * ntiles2 + tile;
       const int prev = __hip_atomic_fetch_add(arrive + job, 1, __ATOMIC_RELAXED,
@@ -1294,7 +1299,7 @@ __global__ __launch_bounds__(768) void moe_mx_decode_kernel(
     const int nj = *njobs;
     const __amdgpu_buffer_rsrc_t yr =
         __builtin_amdgcn_make_buffer_rsrc(y, (short)0, ipl[E] * H * 4, kBufferWord3);
-    for (int q = threadIdx.x; q < nj * 4; q += blockDim.x) {
+    for (int q = threadIdx.x; q < nj * 4; q += nthr) {
       const int job = jobs[q >> 2];
       const int tok = job / ntiles2;
       combine4(yr, gw, resid, out, status, tok, k_top, H, (job - tok * ntiles2) * 16 + (q & 3) * 4);

@@ -682,7 +682,7 @@ __device__ __forceinline__ void select_halves(const float* lg, int n, int E, int
                                               int32_t* __restrict__ idx_out,
                                               uint16_t* __restrict__ w_out, int* ti, int* hist,
                                               uint32_t* wk, double* ex) {
-  rank_halves(lg, n, E, k, wk);
+  rank_halves(lg, n, E, k, wk, (int)(blockDim.x >> 6));
   lds_barrier();
   const int np = n * k;
   for (int p = threadIdx.x; p < np; p += blockDim.x) ex[p] = pair_exp(wk, p, k);

@@ -35,10 +35,12 @@ __device__ __forceinline__ double readlane_f64(double x, int l) {
 struct NoRankHook {
   __device__ void operator()(int, int, uint32_t) const {}
 };
+// nw = the workgroup's waves (blockDim.x / 64, passed in: a read of blockDim
+// is a vector load that waits for every load in flight before it).
 template <class F = NoRankHook>
 __device__ __forceinline__ void rank_halves(const float* lg, int n, int E, int k, uint32_t* wk,
-                                            F on_rank = F{}) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+                                            int nw, F on_rank = F{}) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, e = lane & 31;
   for (int t0 = 2 * wave; t0 < n; t0 += 2 * nw) {
     const int t = t0 + half;
