@@ -319,12 +319,14 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
   const int NC = (H + 127) >> 7;
 
   u32x4 gv[S];
-  auto load_gate = [&](int ee, u32x4* dst) {
+  uint16_t gbv = 0;  // the expert's bias, loaded with its gate row (not after the dots)
+  auto load_gate = [&](int ee, u32x4* dst, uint16_t& b) {
     const u32x4* gr = (const u32x4*)(gate_w + (size_t)min(ee, E - 1) * H);
 #pragma unroll
     for (int i = 0; i < S; ++i) dst[i] = gr[min(lane + 64 * i, H8 - 1)];
+    b = gate_b[min(ee, E - 1)];
   };
-  if constexpr (!kMfma) load_gate(e0, gv);
+  if constexpr (!kMfma) load_gate(e0, gv, gbv);
   // rows past n repeat the last token (computed, never stored)
   u32x4 xv[TT][J], wv[J];
 #pragma unroll
@@ -498,7 +500,8 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     const int e = e0 + ei * W;
     if (e >= E) break;  // wave-uniform
     u32x4 gn[S];
-    if (ei + 1 < epw) load_gate(e + W, gn);
+    uint16_t gbn = 0;
+    if (ei + 1 < epw) load_gate(e + W, gn, gbn);
     double acc[TT];
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) acc[tt] = 0.0;
@@ -517,7 +520,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
         }
       }
     }
-    const float bias = bf2f(gate_b[e]);
+    const float bias = bf2f(gbv);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       const double a = wave_sum_f64(acc[tt]);
@@ -533,6 +536,7 @@ __global__ __launch_bounds__(64 * W) void moe_router_logits_kernel(
     if (ei + 1 < epw) {
 #pragma unroll
       for (int i = 0; i < S; ++i) gv[i] = gn[i];
+      gbv = gbn;
     }
   }
   if constexpr (kSel) {
