@@ -223,6 +223,9 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     qb[0] = moe::as_bf16x8(src[g]);
     qb[1] = moe::as_bf16x8(src[4 + g]);
   }
+  // the sinks of this thread's two output heads (t / 64 and t / 64 + 4),
+  // loaded now: read at the end they cost a memory round trip of their own
+  const uint16_t sink0 = sinks[hk * kGroup + (t >> 6)], sink1 = sinks[hk * kGroup + (t >> 6) + 4];
   __syncthreads();
   // A chunk's loads, K and V alike: 16-byte unit u = t + 256 j, key u / 8 =
   // c + 32 j (c = t / 8), part t % 8 -- a wave reads eight whole 128-byte rows
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
         const float l = ((red_l[0][hl] + red_l[1][hl]) + red_l[2][hl]) + red_l[3][hl];
         const float lse = hm[hl] + __logf(l);
         const float ob = bf2f(f2bf((j == 0 ? o0 : o1) / l));
-        out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
+        out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, j == 0 ? sink0 : sink1));
       }
       return;
     }
@@ -411,6 +414,9 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
       out[((size_t)b * kHq + hk * kGroup + (t >> 6) + 4 * j) * kD + d] = 0x7FC0;
     return;
   }
+  // this thread's two output heads' sinks first (read at the end, they would
+  // cost a memory round trip of their own)
+  const uint16_t sk[2] = {sinks[hk * kGroup + (t >> 6)], sinks[hk * kGroup + (t >> 6) + 4]};
   // maxima: thread (head t / 32, lane i = t % 32) over splits i, i + 32, ...
   const int mh = t >> 5, mi = t & 31;
   const size_t mbase = ((size_t)b * kHq + hk * kGroup + mh) * splits;
@@ -469,7 +475,7 @@ __device__ void decode_merge_group(const float* part_o, const float* part_ml, in
     const float l = lsum[hl];
     const float lse = hmax[hl] + __logf(l);
     const float ob = bf2f(f2bf(o[j] / l));
-    out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sinks[h]));
+    out[((size_t)b * kHq + h) * kD + d] = f2bf(ob * sink_factor(lse, sk[j]));
   }
 }
 
