@@ -72,10 +72,13 @@ class PagedKVCache:
         self.seqs: dict[int, _Seq] = {}
         # The forward tables live in one device buffer at fixed offsets (kernels
         # captured in a graph keep their addresses), uploaded from a pinned
-        # staging buffer of the same layout in three small copies: the
-        # per-sequence tables with the positions, the slots, the page indices
-        # (each copy spans only what the forward uses).
-        sizes = (max_batch + 1, max_batch + 1, max_batch, max_tokens, max_tokens, num_pages)
+        # staging buffer of the same layout.  A forward of at most max_batch
+        # tokens (every decode step) keeps its positions and slots in short
+        # arrays ahead of the page indices, so its tables are one contiguous
+        # range and one copy; a longer forward uses the long arrays at the end
+        # (three copies, each spanning only what the forward uses).
+        sizes = (max_batch + 1, max_batch + 1, max_batch, max_batch, max_batch, num_pages,
+                 max_tokens, max_tokens)
         self._tables_dev = torch.zeros(sum(sizes), dtype=torch.int32, device=device)
         # two staging buffers used in turn: a forward waits only for the copy
         # made from its buffer two forwards ago (an event), not for the stream
@@ -88,8 +91,8 @@ class PagedKVCache:
             self._table_offsets.append(off)
             views.append(self._tables_dev[off:off + k])
             off += k
-        (self._q_indptr, self._page_indptr, self._kv_len, self._positions, self._slots,
-         self._page_indices) = views
+        (self._q_indptr, self._page_indptr, self._kv_len, self._positions_short,
+         self._slots_short, self._page_indices, self._positions, self._slots) = views
         self.tables: ForwardTables | None = None
         self._decode_ws: torch.Tensor | None = None
         self._decode_ws_held: list = []
@@ -185,11 +188,16 @@ class PagedKVCache:
         if self._stage_events[j] is not None:
             self._stage_events[j].synchronize()  # this buffer's previous copy is done
         host, offs = self._pinned[j], self._table_offsets
-        parts = [q_indptr, page_indptr, kv_len, positions, slots, page_indices]
-        for vals, off in zip(parts, offs):
+        short = n <= self.max_batch
+        parts = [q_indptr, page_indptr, kv_len, page_indices]
+        part_offs = [offs[0], offs[1], offs[2], offs[5]]
+        pos_off, slot_off = (offs[3], offs[4]) if short else (offs[6], offs[7])
+        for vals, off in zip(parts + [positions, slots], part_offs + [pos_off, slot_off]):
             host[off:off + len(vals)] = torch.tensor(vals, dtype=torch.int32)
-        for a, b in ((0, offs[3] + n), (offs[4], offs[4] + n),
-                     (offs[5], offs[5] + len(page_indices))):
+        ranges = [(0, offs[5] + len(page_indices))]
+        if not short:
+            ranges += [(pos_off, pos_off + n), (slot_off, slot_off + n)]
+        for a, b in ranges:
             self._tables_dev[a:b].copy_(host[a:b], non_blocking=True)
         if self.data.is_cuda:
             ev = torch.cuda.Event()
@@ -199,7 +207,8 @@ class PagedKVCache:
         self.tables = ForwardTables(
             batch=batch, num_tokens=n, max_q_len=max(append_lengths),
             max_kv_len=max(kv_len), q_indptr=self._q_indptr[:batch + 1],
-            positions=self._positions[:n], slots=self._slots[:n],
+            positions=(self._positions_short if short else self._positions)[:n],
+            slots=(self._slots_short if short else self._slots)[:n],
             page_indptr=self._page_indptr[:batch + 1],
             page_indices=self._page_indices[:max(1, len(page_indices))],
             kv_len=self._kv_len[:batch],
