@@ -1496,24 +1496,25 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
   const uint32_t sbase = kRows * kRS + kRows * kMxSclRow;  // weight scale staging
   float* const ys = (float*)(lds + sbase + KT * 16 * G);   // [KT][16]
   uint16_t* const wsl = (uint16_t*)(ys + KT * 16);          // [KT] gate weights
-  // the logits and the act values this thread encodes first (they complete
-  // first), then the tile's loads, once the token's experts are known
+  // the logits, the residual column of the combine (read at the end it would
+  // cost a memory round trip of its own) and the act values this thread
+  // encodes first (they complete first), then the tile's loads, once the
+  // token's experts are known
   const float v = lane < E ? logits[lane] : 0.0f;
+  const uint16_t xres = x[(blockIdx.x << 4) + (threadIdx.x & 15)];
   f32x4 av[kRounds][2];
 #pragma unroll
   for (int i = 0; i < kRounds; ++i) {
     const int id = i * kThreads + (int)threadIdx.x;
     const int idc = id < kTasks ? id : (id & 3);
     const int rb = idc >> 2, tt = rb / kBlk, blk = rb - tt * kBlk;
-    const int k0 = blk * 32 + (idc & 3) * 8;
-    if (blk * 32 < K) {
-      const f32x4* src = (const f32x4*)(act + (size_t)tt * K + k0);
-      av[i][0] = src[0];
-      av[i][1] = src[1];
-    } else {
-      av[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      av[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    // blocks past K load the row's first block (zeroed when encoded): with
+    // the loads under a branch the compiler waited for each round's loads
+    // before issuing the next round's
+    const int k0 = blk * 32 < K ? blk * 32 + (idc & 3) * 8 : 0;
+    const f32x4* src = (const f32x4*)(act + (size_t)tt * K + k0);
+    av[i][0] = src[0];
+    av[i][1] = src[1];
   }
   __builtin_amdgcn_sched_barrier(0);
   int id;
@@ -1537,8 +1538,11 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
     const int tt = rb / kBlk, blk = rb - tt * kBlk;
     const int k0 = blk * 32 + quarter * 8;
     const int c = blk >> 2, gg = blk & 3;
+    const bool in_k = blk * 32 < K;
     float rr[8] = {av[i][0][0], av[i][0][1], av[i][0][2], av[i][0][3],
                    av[i][1][0], av[i][1][1], av[i][1][2], av[i][1][3]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rr[j] = in_k ? rr[j] : 0.0f;
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
       float amax = 0.0f;
@@ -1595,7 +1599,7 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
     float a = 0.0f;
 #pragma unroll
     for (int s = 0; s < KT; ++s) a = a + ys[s * 16 + threadIdx.x] * bf2f(wsl[s]);
-    out[col] = f2bf(__fadd_rn(bf2f(x[col]), bf2f(f2bf(a))));
+    out[col] = f2bf(__fadd_rn(bf2f(xres), bf2f(f2bf(a))));
   }
 }
 
