@@ -110,6 +110,25 @@ def make_block(E: int, seed: int, zipf_beta: float, device):
     return blk
 
 
+def hbm_ceiling():
+    """The achievable HBM read bandwidth measured on these boxes (GB/s), from the
+    committed `bench.py --hbm-calibration` summary, or None."""
+    path = os.path.join(REPO, "profiles", "hbm_calibration.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("best_gbs")
+
+
+def with_ceiling(roof: dict) -> dict:
+    """Adds the HBM-bound roofline's fraction of the calibrated ceiling."""
+    c = hbm_ceiling()
+    if c:
+        roof["ceiling_gbs"] = c
+        roof["frac_of_ceiling"] = round(roof["achieved"] / c, 4)
+    return roof
+
+
 def read_traffic(workload: str, kernel: str):
     """Measured HBM bytes per launch of `kernel` (a name prefix) from a committed
     rocprofv3 PMC summary of this workload, if any."""
@@ -229,6 +248,7 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
                 "algorithmic_bytes": int(alg),
                 "intermediate_bytes": int(2 * nk * I * PIECES_ACT + nk * H * 4),
                 "avg_us": round(t, 2)}
+        with_ceiling(roof)
     elif not gemm:
         alg = avg_touched * (2 * I * (H // 32) * 17 + 2 * I * 2) + n * H * PIECES_T
         t = stage_us["mlp1"]
@@ -238,6 +258,7 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": read_traffic(name, "moe::moe_mx_gemv_kernel<2, 1, 23>"),
                 "algorithmic_bytes": int(alg), "avg_us": round(t, 2)}
+        with_ceiling(roof)
     else:
         f1 = 2 * nk * 2 * I * H
         t = stage_us["mlp1"]
@@ -257,9 +278,10 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
                   "fp8_hw_frac": round(tflops * PIECES_T / FP8_PEAK_TFLOPS, 4)}
         if bf / bb < ridge:
             # below the ridge (120B prefill 2048): HBM-bound
-            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "bf16_mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), **common}
+            roof = with_ceiling({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                 "bf16_mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                                 **common})
         else:
             roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
