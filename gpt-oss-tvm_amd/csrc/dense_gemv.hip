@@ -94,50 +94,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
   // occupancy) and the epilogue's operands first (they are needed first),
   // then every W load of this lane (K <= 4096: at most two rounds of 256
   // 16-byte chunks) with the norm weight's chunks when the rows are
-  // normalised.
+  // normalised.  Every load is unconditional (indices clamped into range,
+  // values past the row never used, raw bits converted where they are
+  // used): a load under a branch made the compiler wait for it inside the
+  // branch, which split the weight loads into three rounds with a full wait
+  // between them.
   const bool norm = a.norm_w != nullptr;
+  const uint16_t* const nw = norm ? a.norm_w : a.W;  // (loaded, unused, without a norm)
   constexpr bool kEarlyX = MM == 1;
   u32x4 xr[kEarlyX ? 1 : 0 + 1][kIters];
   if constexpr (kEarlyX) {
 #pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      const int c = it * kThreads + t;
-      xr[0][it] = c < chunks ? *(const u32x4*)(a.x + c * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int it = 0; it < kIters; ++it)
+      xr[0][it] = *(const u32x4*)(a.x + min(it * kThreads + t, chunks - 1) * 8);
   }
   // the epilogue task of this thread (one per row or rope pair, and token)
   constexpr int kTasks = EPI == kQkv ? RW / 2 : RW;
   const bool task = t < kTasks * M;
   const int ti = task ? t / M : 0, tm = task ? t % M : 0;
-  float eb0 = 0.f, eb1 = 0.f, er = 0.f, cs = 0.f, sn = 0.f, ifq = 0.f;
+  uint16_t eb0r = 0, eb1r = 0, err = 0;
+  float cs = 0.f, sn = 0.f, ifq = 0.f;
   int eslot = -1, epos = 0;
   if constexpr (EPI == kBiasResidual) {
-    const int n = rows[ti];
-    if (task && n < N) {
-      eb0 = bf2f(a.bias[n]);
-      er = bf2f(a.res[(size_t)tm * N + n]);
-    }
+    const int n = min(rows[ti], N - 1);
+    eb0r = a.bias[n];
+    err = a.res[(size_t)tm * N + n];
   } else if constexpr (EPI == kQkv) {
     const int nlo = rows[2 * ti], nhi = rows[2 * ti + 1];
-    if (task) {
-      eb0 = bf2f(a.bias[nlo]);
-      eb1 = bf2f(a.bias[nhi]);
-      eslot = a.slots[tm];
-      epos = a.positions[tm];
-      ifq = a.inv_freq[nlo % kD];
-    }
+    eb0r = a.bias[nlo];
+    eb1r = a.bias[nhi];
+    eslot = a.slots[tm];
+    epos = a.positions[tm];
+    ifq = a.inv_freq[nlo % kD];
   }
   __builtin_amdgcn_sched_barrier(0);
   u32x4 wv[kIters][RW];
   u32x4 nwv[kIters];
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
-    const int c = it * kThreads + wave * 64 + lane;
+    const int cc = min(it * kThreads + wave * 64 + lane, chunks - 1);
 #pragma unroll
     for (int i = 0; i < RW; ++i)
-      wv[it][i] = (c < chunks && rows[i] < N) ? *(const u32x4*)(a.W + (size_t)rows[i] * K + c * 8)
-                                              : u32x4{0u, 0u, 0u, 0u};
-    nwv[it] = (norm && c < chunks) ? *(const u32x4*)(a.norm_w + c * 8) : u32x4{0u, 0u, 0u, 0u};
+      wv[it][i] = *(const u32x4*)(a.W + (size_t)min(rows[i], N - 1) * K + cc * 8);
+    nwv[it] = *(const u32x4*)(nw + cc * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
   // the RoPE factors while W streams
@@ -237,8 +236,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
         if constexpr (EPI == kPlain) {
           a.out[(size_t)m * N + n] = y;
         } else {
-          const float tb = bf2f(f2bf(bf2f(y) + eb0));
-          a.out[(size_t)m * N + n] = f2bf(er + tb);
+          const float tb = bf2f(f2bf(bf2f(y) + bf2f(eb0r)));
+          a.out[(size_t)m * N + n] = f2bf(bf2f(err) + tb);
         }
       }
     }
@@ -249,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
       const int i = ti, m = tm;
       const int nlo = rows[2 * i];
       const int head = nlo / kD, d = nlo % kD;
-      float lo = bf2f(f2bf(bf2f(f2bf(total(2 * i, m))) + eb0));
-      float hi = bf2f(f2bf(bf2f(f2bf(total(2 * i + 1, m))) + eb1));
+      float lo = bf2f(f2bf(bf2f(f2bf(total(2 * i, m))) + bf2f(eb0r)));
+      float hi = bf2f(f2bf(bf2f(f2bf(total(2 * i + 1, m))) + bf2f(eb1r)));
       if (head < kHq + kHkv) {
         const float nl = lo * cs - hi * sn;
         const float nh = lo * sn + hi * cs;
