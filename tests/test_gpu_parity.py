@@ -210,11 +210,13 @@ def test_many_tokens_per_expert(native):
                                           (12, 192, 64, 1, 47), (40, 192, 64, 1, 48)])
 def test_block_internal_routing(native, E, H, I, n, seed):
     """The block's own router and grouping (logits kernel — VALU fp64 dots up
-    to 1024 tokens, fp64 MFMA dots above — then one workgroup of top-k +
-    grouping for n k <= 4096, or the chunked two-pass grouping above; at the
-    20B shape with n <= 128 the experts run in the one decode launch): t,
-    indices, weights and every grouping array bit-exact, output in
-    tolerance."""
+    to 1024 tokens, fp64 MFMA dots above — then top-k + grouping: at the 20B
+    shape by the one-token mlp1 / mlp2 launches at n = 1, by the logits
+    launch's last workgroup at n = 2 (the decode launch then runs the
+    experts), by the decode launch's own prologue at n = 64 and 128; one
+    workgroup of top-k + grouping for other shapes with n k <= 4096, the
+    chunked two-pass grouping above): t, indices, weights and every grouping
+    array bit-exact, output in tolerance."""
     p = O.make_params(seed, num_experts=E, hidden=H, inter=I)
     x = O.make_input(seed + 100, n, hidden=H)
     tr = O.block_forward(x, p)
