@@ -65,8 +65,8 @@ int moe_mx_token1_check(int E, int k, int H, int I);
 int moe_launch_mx_token1_mlp1(const void* t_packed, const void* logits, int E,
                               void* const* route, const void* blocks, const void* scales,
                               const void* bias, int k, int H, int I, float alpha, float limit,
-                              void* act, hipStream_t stream);
-int moe_launch_mx_token1_mlp2(const void* act, const void* logits, int E, const void* x,
+                              void* act_packed, hipStream_t stream);
+int moe_launch_mx_token1_mlp2(const void* act_packed, const void* logits, int E, const void* x,
                               const void* blocks, const void* scales, const void* bias, int k,
                               int H, int I, void* out, hipStream_t stream);
 int moe_launch_swiglu(const void* x, int64_t pairs, float alpha, float limit, void* out,
@@ -530,18 +530,20 @@ static int block_forward_impl(const uint16_t* x, int64_t n, int64_t E, int64_t k
   const bool fuse = decode && n <= kFusedCombineMaxTokens;
   const int zero_ints = fuse ? (int)(n * (H / 16)) : 0;
   // One token (the shape permitting): the logits launch, then mlp1 and mlp2
-  // with the gated combine, each wave on one weight tile (act by slot, [k][I]
-  // fp32); both route the token themselves from its logits, and mlp1's first
-  // workgroup writes idx, w and the grouping.
+  // with the gated combine, each wave on one weight tile; mlp1 writes act as
+  // mlp2's three fp8 pieces (act_pk, rows slot 3 + piece); both route the
+  // token themselves from its logits, and mlp1's first workgroup writes idx,
+  // w and the grouping.
   if (n == 1 && !gemm && moe_mx_token1_check((int)E, (int)k, (int)H, (int)I) == MOE_OK) {
     void* const route[7] = {idx, w, indptr, sp, ti, ei, pp};
     if ((rc = moe_launch_router_logits(x, norm_w, gate_w, gate_b, (int)n, (int)H, (int)E, eps, t,
                                        logits, t_pk, t_qs, nullptr, s)) ||
         (rc = mark(m, MOE_STAGE_ROUTER_LOGITS, s)) ||
         (rc = moe_launch_mx_token1_mlp1(t_pk, logits, (int)E, route, mlp1_blocks, mlp1_scales,
-                                        mlp1_bias, (int)k, (int)H, (int)I, alpha, limit, act, s)) ||
+                                        mlp1_bias, (int)k, (int)H, (int)I, alpha, limit, act_pk,
+                                        s)) ||
         (rc = mark(m, MOE_STAGE_MLP1, s)) ||
-        (rc = moe_launch_mx_token1_mlp2(act, logits, (int)E, x, mlp2_blocks, mlp2_scales,
+        (rc = moe_launch_mx_token1_mlp2(act_pk, logits, (int)E, x, mlp2_blocks, mlp2_scales,
                                         mlp2_bias, (int)k, (int)H, (int)I, out, s)))
       return rc;
     return mark(m, MOE_STAGE_MLP2, s);

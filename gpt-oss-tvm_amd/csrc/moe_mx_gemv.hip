@@ -1414,7 +1414,7 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
     const uint8_t* __restrict__ tq, const uint8_t* __restrict__ tqs,
     const float* __restrict__ logits, int E, Token1Route rt, const uint8_t* __restrict__ blocks,
     const uint8_t* __restrict__ scales, const uint16_t* __restrict__ bias, int N, int G,
-    float alpha, float limit, float* __restrict__ act, int act_ld) {
+    float alpha, float limit, uint8_t* __restrict__ aq, uint8_t* __restrict__ aqs) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kRS = mx_row_stride(kT1Nct);
   constexpr int kUnits = kT1Kp / 16, kSclUnits = kMxSclRow / 16;
@@ -1460,13 +1460,55 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
   // lane group 0 holds the token (rows 0 and 1: its two pieces)
   const float y0 = (acc[1] + acc[0]) + t.bn;
   const float l0 = lane_xor1(y0);  // odd rows hold the linear half
+  // The workgroup's four tiles are act columns 32 bx .. 32 bx + 31 of this
+  // slot: one 32-element block, which it encodes into mlp2's three fp8
+  // pieces itself, exactly as moe_pieces_kernel<3, true> does (thread q of
+  // the first quad takes wave q's eight values; the block maximum by lane
+  // exchange).  Piece rows: slot 3 + p, Kp bytes of codes each, 112 scale
+  // bytes (run (block & 3), slot block >> 2).
+  float* const actb = (float*)(lds + ss - wave * (16 * G) + 4 * (16 * G));  // 32 floats
   if (g == 0 && (r & 1) == 0) {
     const float xg = fminf(y0, limit);
     const float xl = fminf(fmaxf(l0, -limit), limit);
     const float z = __fmul_rn(alpha, xg);
     const float sig = 1.0f / (1.0f + expf(-z));
-    const float v = __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
-    act[(size_t)slot * act_ld + (((tile << 4) + r) >> 1)] = v;
+    actb[wave * 8 + (r >> 1)] = __fmul_rn(__fmul_rn(xg, sig), __fadd_rn(xl, 1.0f));
+  }
+  lds_barrier();
+  const int blk = blockIdx.x, c = blk >> 2, gg = blk & 3;
+  if (wave == 0 && lane < 4) {
+    float rr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rr[i] = actb[lane * 8 + i];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(rr[i]));
+      amax = fmaxf(amax, lane_xor1(amax));
+      amax = fmaxf(amax, lane_xor2(amax));
+      const uint32_t sc = e8m0_for_amax(amax);
+      const float inv = __uint_as_float((254u - sc) << 23);
+      const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
+      uint32_t lo, hi;
+      e4m3_piece8(rr, inv, scf, lo, hi);
+      const int prow = slot * 3 + p;
+      *(uint2*)(aq + (size_t)prow * kT1Kp + blk * 32 + lane * 8) = make_uint2(lo, hi);
+      if (lane == 0) aqs[prow * kMxSclRow + gg * kMxSclRun + c] = (uint8_t)sc;
+    }
+  } else if (wave == 1 && blk == (int)gridDim.x - 1) {
+    // the last block's workgroup also writes the zero blocks up to 128 x 23
+    // (codes 0, the scale of a zero block), as the pieces kernel encodes them
+    const int nz = 4 * kT1Nct - (blk + 1);  // zero blocks of each piece row
+    const uint32_t sc0 = e8m0_for_amax(0.0f);
+    for (int u = lane; u < 3 * nz * 2; u += 64) {
+      const int prow = slot * 3 + u / (2 * nz), h = u % (2 * nz);
+      *(u32x4*)(aq + (size_t)prow * kT1Kp + (blk + 1) * 32 + h * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+    if (lane < 3 * nz) {
+      const int prow = slot * 3 + lane / nz, zb = blk + 1 + lane % nz;
+      aqs[prow * kMxSclRow + (zb & 3) * kMxSclRun + (zb >> 2)] = (uint8_t)sc0;
+    }
   }
 }
 
@@ -1479,7 +1521,8 @@ __global__ __launch_bounds__(256) void moe_mx_token1_mlp1_kernel(
 // router's bf16 gate weights).
 template <int KT>
 __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
-    const float* __restrict__ act, int K, const float* __restrict__ logits, int E,
+    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ aqs,
+    const float* __restrict__ logits, int E,
     const uint16_t* __restrict__ x,
     const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, int N, int G, uint16_t* __restrict__ out) {
@@ -1488,33 +1531,34 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
   constexpr int kRS = mx_row_stride(kT1Nct);
   constexpr int kRows = 3 * KT;
   constexpr int kThreads = 64 * KT;
-  constexpr int kBlk = kT1Nct * 4;                  // 32-element blocks per row (past K: zero)
-  constexpr int kTasks = KT * kBlk * 4;             // four threads per (row, block)
-  constexpr int kRounds = (kTasks + kThreads - 1) / kThreads;
+  // the KT slots' act pieces (rows 3 s + p, written by the one-token mlp1
+  // launch): 16-byte units of the code rows, then of the scale rows
+  constexpr int kRowUnits = kT1Kp / 16, kSclUnits = kMxSclRow / 16;
+  constexpr int kUnits = kRows * (kRowUnits + kSclUnits);
+  constexpr int kRounds = (kUnits + kThreads - 1) / kThreads;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t sbase = kRows * kRS + kRows * kMxSclRow;  // weight scale staging
   float* const ys = (float*)(lds + sbase + KT * 16 * G);   // [KT][16]
   uint16_t* const wsl = (uint16_t*)(ys + KT * 16);          // [KT] gate weights
   // the logits, the residual column of the combine (read at the end it would
-  // cost a memory round trip of its own) and the act values this thread
-  // encodes first (they complete first), then the tile's loads, once the
-  // token's experts are known
+  // cost a memory round trip of its own) and this thread's units of the act
+  // pieces first (they complete first), then the tile's loads, once the
+  // token's experts are known; units past the end repeat the last one (the
+  // same bytes to the same place)
   const float v = lane < E ? logits[lane] : 0.0f;
   const uint16_t xres = x[(blockIdx.x << 4) + (threadIdx.x & 15)];
-  f32x4 av[kRounds][2];
+  u32x4 pv[kRounds];
+  uint32_t pd[kRounds];
 #pragma unroll
   for (int i = 0; i < kRounds; ++i) {
-    const int id = i * kThreads + (int)threadIdx.x;
-    const int idc = id < kTasks ? id : (id & 3);
-    const int rb = idc >> 2, tt = rb / kBlk, blk = rb - tt * kBlk;
-    // blocks past K load the row's first block (zeroed when encoded): with
-    // the loads under a branch the compiler waited for each round's loads
-    // before issuing the next round's
-    const int k0 = blk * 32 < K ? blk * 32 + (idc & 3) * 8 : 0;
-    const f32x4* src = (const f32x4*)(act + (size_t)tt * K + k0);
-    av[i][0] = src[0];
-    av[i][1] = src[1];
+    const int u = min(i * kThreads + (int)threadIdx.x, kUnits - 1);
+    const bool code = u < kRows * kRowUnits;
+    const int m = code ? u / kRowUnits : (u - kRows * kRowUnits) / kSclUnits;
+    const int cu = code ? u - m * kRowUnits : u - kRows * kRowUnits - m * kSclUnits;
+    const uint8_t* src = code ? aq + (size_t)m * kT1Kp + cu * 16 : aqs + m * kMxSclRow + cu * 16;
+    pv[i] = *(const u32x4*)src;  // (one load from a selected address: no branch)
+    pd[i] = code ? m * kRS + cu * 16 : kRows * kRS + m * kMxSclRow + cu * 16;
   }
   __builtin_amdgcn_sched_barrier(0);
   int id;
@@ -1525,43 +1569,8 @@ __global__ __launch_bounds__(64 * KT) void moe_mx_token1_mlp2_kernel(
   t1_issue(t, blocks, scales, bias, (size_t)e * N + ((size_t)blockIdx.x << 4), G);
   __builtin_amdgcn_sched_barrier(0);
   if (wave == 0 && lane < KT) wsl[lane] = wt;
-  // Encode the KT rows into three pieces, as moe_pieces_kernel<3, true>
-  // does: four threads per 32-element block, the block maximum by lane
-  // exchange.  Whole quads past the end encode the first block and store
-  // nothing.
 #pragma unroll
-  for (int i = 0; i < kRounds; ++i) {
-    const int id = i * kThreads + (int)threadIdx.x;
-    const bool valid = id < kTasks;
-    const int idc = valid ? id : (id & 3);
-    const int quarter = idc & 3, rb = idc >> 2;
-    const int tt = rb / kBlk, blk = rb - tt * kBlk;
-    const int k0 = blk * 32 + quarter * 8;
-    const int c = blk >> 2, gg = blk & 3;
-    const bool in_k = blk * 32 < K;
-    float rr[8] = {av[i][0][0], av[i][0][1], av[i][0][2], av[i][0][3],
-                   av[i][1][0], av[i][1][1], av[i][1][2], av[i][1][3]};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) rr[j] = in_k ? rr[j] : 0.0f;
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-      float amax = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(rr[j]));
-      amax = fmaxf(amax, lane_xor1(amax));
-      amax = fmaxf(amax, lane_xor2(amax));
-      const uint32_t sc = e8m0_for_amax(amax);
-      const float inv = __uint_as_float((254u - sc) << 23);
-      const float scf = sc ? __uint_as_float(sc << 23) : __uint_as_float(0x00400000u);
-      uint32_t lo, hi;
-      e4m3_piece8(rr, inv, scf, lo, hi);
-      if (valid) {
-        const int m = tt * 3 + p;
-        *(uint2*)(lds + m * kRS + k0) = make_uint2(lo, hi);
-        if (quarter == 0) lds[kRows * kRS + m * kMxSclRow + gg * kMxSclRun + c] = (uint8_t)sc;
-      }
-    }
-  }
+  for (int i = 0; i < kRounds; ++i) *(u32x4*)(lds + pd[i]) = pv[i];
   const uint32_t ss = sbase + wave * (16 * G);
   t1_stage_scales(t, lds + ss, G);
   lds_barrier();
@@ -1918,7 +1927,7 @@ int moe_mx_token1_check(int E, int k, int H, int I) {
 int moe_launch_mx_token1_mlp1(const void* t_packed, const void* logits, int E,
                               void* const* route, const void* blocks, const void* scales,
                               const void* bias, int k, int H, int I, float alpha, float limit,
-                              void* act, hipStream_t stream) {
+                              void* act_packed, hipStream_t stream) {
   using namespace moe;
   if (moe_mx_token1_check(E, k, H, I) != kOk) return kErrUnsupported;
   const Token1Route rt{(int32_t*)route[0], (uint16_t*)route[1], (int32_t*)route[2],
@@ -1926,19 +1935,22 @@ int moe_launch_mx_token1_mlp1(const void* t_packed, const void* logits, int E,
                        (int32_t*)route[6]};
   const uint8_t* tq = (const uint8_t*)t_packed;
   const int G = H / 32;
-  const size_t lds = 2 * mx_row_stride(kT1Nct) + 2 * kMxSclRow + 4 * 16 * G;
+  // LDS: t's two piece rows and their scales, the waves' scale staging, the
+  // workgroup's 32 act values
+  const size_t lds = 2 * mx_row_stride(kT1Nct) + 2 * kMxSclRow + 4 * 16 * G + 32 * 4;
+  uint8_t* aq = (uint8_t*)act_packed;
   hipLaunchKernelGGL(moe_mx_token1_mlp1_kernel, dim3(2 * I / 64, k), dim3(256), lds, stream, tq,
                      tq + moe_pieces_q_bytes(1, H, 2), (const float*)logits, E, rt,
                      (const uint8_t*)blocks,
-                     (const uint8_t*)scales, (const uint16_t*)bias, 2 * I, G, alpha, limit,
-                     (float*)act, I);
+                     (const uint8_t*)scales, (const uint16_t*)bias, 2 * I, G, alpha, limit, aq,
+                     aq + moe_pieces_q_bytes(k, I, 3));
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 // One token's mlp2 with the gated combine and the residual: act rows by slot
 // ([k][I], fp32), the token's E logits and x -> out = bf16(x + bf16(sum_s
 // y_s w_s)) ([H], bf16).
-int moe_launch_mx_token1_mlp2(const void* act, const void* logits, int E, const void* x,
+int moe_launch_mx_token1_mlp2(const void* act_packed, const void* logits, int E, const void* x,
                               const void* blocks, const void* scales, const void* bias, int k,
                               int H, int I, void* out, hipStream_t stream) {
   using namespace moe;
@@ -1947,8 +1959,9 @@ int moe_launch_mx_token1_mlp2(const void* act, const void* logits, int E, const 
   const int G = I / 32;
   const size_t lds =
       3 * KT * (mx_row_stride(kT1Nct) + kMxSclRow) + KT * 16 * G + KT * 16 * 4 + KT * 2;
-  hipLaunchKernelGGL(moe_mx_token1_mlp2_kernel<KT>, dim3(H / 16), dim3(64 * KT), lds, stream,
-                     (const float*)act, I, (const float*)logits, E,
+  const uint8_t* aq = (const uint8_t*)act_packed;
+  hipLaunchKernelGGL(moe_mx_token1_mlp2_kernel<KT>, dim3(H / 16), dim3(64 * KT), lds, stream, aq,
+                     aq + moe_pieces_q_bytes(k, I, 3), (const float*)logits, E,
                      (const uint16_t*)x, (const uint8_t*)blocks, (const uint8_t*)scales,
                      (const uint16_t*)bias, H, G, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
