@@ -213,6 +213,29 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
     sec = timed_steps(lambda i: blocks[i % nw](xs[i % nw]), steps, warmup)
     us = sec * 1e6
     log(f"{name}: {us:.1f} us/block, {n / sec:.0f} tok/s")
+    # Decode sizes also from one HIP graph holding one call per weight set:
+    # at one token the block's three launches take less GPU time than the
+    # host needs to issue them one call at a time, so the eager figure above
+    # is partly the host's; the graph replays them back to back.
+    graph_us = None
+    if n <= 128:
+        for blk in blocks:
+            blk.reserve(n, for_graph=True)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for j in range(nw):
+                blocks[j](xs[j])
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for j in range(nw):
+                blocks[j](xs[j])
+        reps = max(10, steps // nw)
+        graph_us = timed_steps(lambda i: graph.replay(), reps, 3) / nw * 1e6
+        del graph
+        log(f"{name}: {graph_us:.1f} us/block from one HIP graph")
 
     nk = n * K_TOP
     gemm = nk >= 48 * E
@@ -224,6 +247,7 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
     bf = block_flops(n, E)
     res = {
         "workload": label, "tokens": n, "experts": E, "us_per_block": round(us, 2),
+        "graph_us_per_block": round(graph_us, 2) if graph_us is not None else None,
         "tok_s": round(n / sec, 1), "touched_experts": avg_touched,
         "max_over_mean_load": round(sum(loads) / len(loads), 2),
         "block_hbm_frac": round(bb / sec / 1e9 / HBM_PEAK_GBS, 4),
