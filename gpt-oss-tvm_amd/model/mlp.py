@@ -110,6 +110,7 @@ class MLPBlock(torch.nn.Module):
         self.mlp2_bias = packed(E, H, dt=tdt)
         self._ws: torch.Tensor | None = None
         self._ws_held: list = []
+        self._ws_need: dict = {}  # workspace bytes by token count
 
     # -- parameters ---------------------------------------------------------
 
@@ -169,8 +170,12 @@ class MLPBlock(torch.nn.Module):
 
     def workspace_bytes(self, n: int) -> int:
         """Bytes of block workspace a call on n tokens needs (moe_workspace_bytes)."""
-        return _native.workspace_bytes(n, self.num_experts, self.experts_per_token,
-                                       self.hidden_size, self.intermediate_size)
+        need = self._ws_need.get(n)
+        if need is None:
+            need = _native.workspace_bytes(n, self.num_experts, self.experts_per_token,
+                                           self.hidden_size, self.intermediate_size)
+            self._ws_need[n] = need
+        return need
 
     def _workspace(self, n: int, device) -> torch.Tensor:
         need = self.workspace_bytes(n)
@@ -205,9 +210,19 @@ class MLPBlock(torch.nn.Module):
         if not x2.is_contiguous():
             x2 = x2.contiguous()
         ws = self._workspace(x2.shape[0], x2.device)
-        out = _native.block_forward(x2, self.packed_params(), self.experts_per_token,
+        out = _native.block_forward(x2, self._param_seq(), self.experts_per_token,
                                     self.norm.epsilon, SWIGLU_ALPHA, self.swiglu_limit, ws)
         return out.reshape(b, seq_len, dim)
+
+    def _param_seq(self) -> tuple:
+        """The nine parameters in moe_native.BLOCK_PARAM_NAMES order, read from
+        the modules' parameter dicts (attribute lookups on a module cost
+        microseconds of host time per call)."""
+        p, nm, g = self._parameters, self._modules["norm"]._parameters, \
+            self._modules["gate"]._parameters
+        return (nm["weight"], g["weight"], g["bias"], p["mlp1_weight_blocks"],
+                p["mlp1_weight_scales"], p["mlp1_bias"], p["mlp2_weight_blocks"],
+                p["mlp2_weight_scales"], p["mlp2_bias"])
 
     def forward_into(self, x2d: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
         """forward on x2d [n, hidden] into the caller's ``out`` [n, hidden] with the

@@ -88,12 +88,20 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed: {status_string(rc)} ({rc})")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    # (the raw handle of the current stream; the public call builds a Stream
+    # object first, a few microseconds of host time per block call)
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device())
+    return torch.cuda.current_stream().cuda_stream
 
 
 def _ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    # plain ints: the argtypes (c_void_p) convert them
+    return None if t is None else t.data_ptr()
 
 
 def _expect(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = None) -> None:
@@ -101,7 +109,7 @@ def _expect(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None 
         raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
     if t.dtype != dtype:
         raise TypeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name}: expected a GPU tensor, got device {t.device}")
     if not t.is_contiguous():
         raise ValueError(f"{name}: expected a contiguous tensor")
@@ -367,22 +375,28 @@ def workspace_layout(n, E, k, H, inter) -> list[int]:
     return list(offs)
 
 
-def block_forward(x, params: dict, k, eps, alpha, limit, workspace, out=None):
-    """Whole block in one C call (model/mlp.py:371-402).  x [n, H] bf16."""
+BLOCK_PARAM_NAMES = ("norm.weight", "gate.weight", "gate.bias", "mlp1_weight_blocks",
+                     "mlp1_weight_scales", "mlp1_bias", "mlp2_weight_blocks",
+                     "mlp2_weight_scales", "mlp2_bias")
+
+
+def block_forward(x, params, k, eps, alpha, limit, workspace, out=None):
+    """Whole block in one C call (model/mlp.py:371-402).  x [n, H] bf16;
+    params: the nine parameters by reference name, or as a sequence in
+    BLOCK_PARAM_NAMES order."""
+    p = params if isinstance(params, (tuple, list)) else [params[nm] for nm in BLOCK_PARAM_NAMES]
     n, H = x.shape
-    E = params["gate.weight"].shape[0]
-    inter = params["mlp2_weight_blocks"].shape[2] * 32
+    E = p[1].shape[0]
+    inter = p[6].shape[2] * 32
     _expect(x, "x", torch.bfloat16)
     if out is None:
         out = torch.empty_like(x)
     _expect(out, "out", torch.bfloat16, (n, H))
     _expect(workspace, "workspace", torch.uint8)
     _check(_lib.moe_block_forward(
-        _ptr(x), n, E, k, H, inter, _ptr(params["norm.weight"]), _ptr(params["gate.weight"]),
-        _ptr(params["gate.bias"]), _ptr(params["mlp1_weight_blocks"]),
-        _ptr(params["mlp1_weight_scales"]), _ptr(params["mlp1_bias"]),
-        _ptr(params["mlp2_weight_blocks"]), _ptr(params["mlp2_weight_scales"]),
-        _ptr(params["mlp2_bias"]), eps, alpha, limit, _ptr(out), _ptr(workspace),
+        x.data_ptr(), n, E, k, H, inter, p[0].data_ptr(), p[1].data_ptr(), p[2].data_ptr(),
+        p[3].data_ptr(), p[4].data_ptr(), p[5].data_ptr(), p[6].data_ptr(), p[7].data_ptr(),
+        p[8].data_ptr(), eps, alpha, limit, out.data_ptr(), workspace.data_ptr(),
         workspace.numel(), _stream()), "moe_block_forward")
     return out
 
