@@ -144,8 +144,8 @@ def read_traffic(workload: str, kernel: str):
 
 
 def block_bytes(n: int, touched: float, E: int) -> float:
-    """Compulsory HBM bytes of one block call: touched experts'
-    weights, router and norm weights, x in and out."""
+    """Compulsory HBM bytes of one block call: touched experts' weights,
+    router and norm weights, x in and out."""
     return touched * PER_EXPERT_BYTES + E * H * 2 + 2 * E + 2 * H + n * H * 4
 
 
@@ -255,9 +255,9 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
         "stages_us": {s: round(v, 2) for s, v in stage_us.items()},
     }
     if fused:
-        # touched experts' weights plus 4 bytes per token (the
-        # token in and out); the act pieces written and read back inside the
-        # launch are intermediates, listed apart and not counted
+        # compulsory bytes: the touched experts' weights plus 4 bytes per
+        # token element (the token in and out); the act pieces written and read
+        # back inside the launch are intermediates, listed apart and not counted
         alg = avg_touched * PER_EXPERT_BYTES + n * H * 4
         t = stage_us["decode"]
         achieved = alg / (t * 1e-6) / 1e9
@@ -301,7 +301,7 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
                   # at the fp8 (fp8 x fp4) dense rate
                   "fp8_hw_frac": round(tflops * PIECES_T / FP8_PEAK_TFLOPS, 4)}
         if bf / bb < ridge:
-            # below the ridge (120B prefill 2048): HBM-bound
+            # below the ridge (the 120B prefill of 2048 tokens): HBM-bound
             roof = with_ceiling({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                                  "bf16_mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
