@@ -402,7 +402,8 @@ def test_block_router_pieces_fused(native, block20b, n):
 def test_block_decode_act_pieces(native, block20b, n, seed):
     """The decode launch encodes act in LDS, block by block, into the same three
     pieces as moe_quantize_pieces of mlp1's fp32 output (rows by sorted pair).
-    The block runs that launch from two tokens up (one token: separate launches)."""
+    The block runs that launch from two tokens up (one token: separate launches,
+    checked by test_one_token_act_pieces)."""
     p, blk = block20b
     H, k = 2880, 4
     nk = n * k
@@ -417,6 +418,31 @@ def test_block_decode_act_pieces(native, block20b, n, seed):
     ref = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), nk, 2880, 3)
     for a, b in zip(fused, ref):
         assert np.array_equal(a, b), np.argwhere(a != b)[:4]
+
+
+@pytest.mark.parametrize("seed", [24, 25])
+def test_one_token_act_pieces(native, block20b, seed):
+    """At one token the mlp1 launch encodes act into mlp2's three pieces itself,
+    one 32-column block per workgroup (rows by slot, the zero blocks up to 128 x
+    23 written by the last block's workgroup): the same code bytes and scale
+    bytes as moe_quantize_pieces of mlp1's fp32 output (rows by sorted pair),
+    the rows matched through pair_pos."""
+    p, blk = block20b
+    n, H, k = 1, 2880, 4
+    x = bf16_dev(O.make_input(seed, n)).view(1, n, H)
+    blk(x)
+    torch.cuda.synchronize()
+    ws = blk._workspace(n, x.device)
+    offs = native.workspace_layout(n, p.num_experts, k, H, 2880)
+    nb = native.pieces_bytes(k, 2880, 3)
+    q, qs = PM.unpack(host(ws[offs[10]: offs[10] + nb]), k, 2880, 3)
+    st = blk.forward_staged(x)
+    rq, rqs = PM.unpack(host(native.quantize_pieces(st["act"].contiguous(), 3)), k, 2880, 3)
+    pos = host(st["perm"]["pair_pos"])
+    for s in range(k):
+        assert np.array_equal(q[s], rq[pos[s]]), s
+        # scale slots 0..22 of each run (chunks 0..22); 23..27 are never read
+        assert np.array_equal(qs[s, :, :, :23], rqs[pos[s], :, :, :23]), s
 
 
 @pytest.mark.parametrize("n,seed", [(1, 21), (64, 22), (128, 23)])
