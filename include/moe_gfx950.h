@@ -262,7 +262,9 @@ MOE_API size_t moe_workspace_bytes(int64_t n, int64_t E, int64_t k, int64_t H, i
  * 256 bytes of counters), in this order:
  * t, idx, w, indptr, sorted_pairs, token_indices, expert_ids, pair_pos,
  * t_pieces, act (fp32 [n*k, I]; where n*k > 2E it shares y's offset: its
- * last reader runs before y is written), act_pieces, y (fp32 [n*k, H], in a
+ * last reader runs before y is written; not written by the one-token and
+ * decode launches), act_pieces (at one token: rows by slot, written by the
+ * mlp1 launch), y (fp32 [n*k, H], in a
  * region of n*k*max(H, I) floats), logits (fp32 [n, E], bf16 values), counts
  * (int32 [ceil(n / 16), E], expert histogram per 16-token chunk, n > 128; or
  * int32 [n, H / 16], the decode launch's arrivals per token and 16-column
