@@ -277,10 +277,16 @@ def run_block_config(name: str, steps: int, warmup: int, weight_sets: int, dev) 
         alg = avg_touched * (2 * I * (H // 32) * 17 + 2 * I * 2) + n * H * PIECES_T
         t = stage_us["mlp1"]
         achieved = alg / (t * 1e-6) / 1e9
-        roof = {"bound": "hbm", "kernel": "moe_mx_gemv_kernel<2,1,23> (mlp1)",
+        # one token runs its own mlp1 launch (each wave on one weight tile,
+        # act's pieces written by the epilogue); more tokens the persistent GEMV
+        kern, trace_name = (("moe_mx_token1_mlp1_kernel (mlp1 + SwiGLU + act pieces)",
+                             "moe::moe_mx_token1_mlp1_kernel") if n == 1 else
+                            ("moe_mx_gemv_kernel<2,1,23> (mlp1)",
+                             "moe::moe_mx_gemv_kernel<2, 1, 23>"))
+        roof = {"bound": "hbm", "kernel": kern,
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": read_traffic(name, "moe::moe_mx_gemv_kernel<2, 1, 23>"),
+                "traffic": read_traffic(name, trace_name),
                 "algorithmic_bytes": int(alg), "avg_us": round(t, 2)}
         with_ceiling(roof)
     else:
